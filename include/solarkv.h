@@ -1,0 +1,108 @@
+/*
+ * solarkv.h — C ABI of libsolarkv.so, the MI355X (gfx950) block-causal KV-cache path.
+ *
+ * Every entry point is stream-ordered (it enqueues work on `stream` and returns without a
+ * host synchronisation), allocates nothing, and returns 0 on success or a negative SKV_E_*
+ * code; skv_last_error() then names the failing argument.  All tensors are owned by the
+ * caller; pointers are device addresses unless the parameter says "host".
+ *
+ * Frame-slot pool layout (one pair of pools per transformer layer):
+ *   K pool  [n_slots][B][H][Tp][D]   row-major keys of each frame, D contiguous
+ *   V pool  [n_slots][B][H][D][Tp]   values stored transposed (tokens contiguous per channel)
+ *   scales  [n_slots][B][H] float    fp8 pools only: dequantisation scale = absmax / 448
+ * T is the frame's token count and Tp = T rounded up to a multiple of 64; rows T..Tp-1 of a
+ * slot are zero so that a 64-key tile never straddles two frames.
+ *
+ * Token-major tensors (new K/V, queries, outputs, gathered views) are [B][L][H][D] with
+ * element strides (sb, st, sh) and a unit stride on D — the reference layout
+ * (solar/backends/wan22/runtime/stage2.py:1776-1793, attention.py:56-60).
+ */
+#ifndef SOLARKV_H
+#define SOLARKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* skv_stream_t; /* a hipStream_t; NULL = the null stream */
+
+enum skv_dtype {
+  SKV_F32 = 0,
+  SKV_BF16 = 1,
+  SKV_FP8_E4M3 = 2 /* OCP e4m3fn, pools only */
+};
+
+enum skv_mask_mode {
+  SKV_MASK_NONE = 0,        /* every query sees every key of the frame list */
+  SKV_MASK_CHUNK_CAUSAL = 1 /* query at position p sees keys < min((p / chunk + 1) * chunk, n_keys) */
+};
+
+enum skv_status {
+  SKV_OK = 0,
+  SKV_E_ARG = -1,         /* bad pointer, size, stride or dtype */
+  SKV_E_UNSUPPORTED = -2, /* valid request this build does not implement (e.g. head_dim != 128) */
+  SKV_E_LAUNCH = -3       /* the HIP launch itself failed */
+};
+
+#define SKV_MAX_APPEND_FRAMES 64
+#define SKV_MAX_FRAMES 256
+
+/* Library version as an integer (major * 10000 + minor * 100 + patch). */
+int skv_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* skv_last_error(void);
+
+/*
+ * skv_append — write n_frames whole frames of new K/V into pool slots.
+ * Replaces the slice assignments of the reference cache update:
+ *   causal_model.py:1074-1080 (rolling), :1115-1121 (direct), :2894-2898 / :2910-2914 (commit).
+ * Frame f (0 <= f < n_frames) is source tokens [(src_frame0 + f) * T, (src_frame0 + f + 1) * T)
+ * of k_new / v_new and goes to slot dst_slots[f] (host array, copied into the launch).
+ * pool_dtype SKV_FP8_E4M3 quantises with one scale per (slot, b, h):
+ *   scale = absmax / 448, code = e4m3fn(clamp(x * (448 / absmax), -448, 448)), 0 if absmax == 0;
+ * k_scale / v_scale must then be non-NULL, otherwise they are ignored.
+ */
+int skv_append(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
+               int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool, void* v_pool,
+               float* k_scale, float* v_scale, int pool_dtype, int n_slots,
+               const int32_t* dst_slots /* host */, int n_frames, int batch, int heads,
+               int head_dim, int frame_tokens, skv_stream_t stream);
+
+/*
+ * skv_gather — materialise pool frames slots[0..n_frames) as contiguous token-major K and V
+ * [B][n_frames * T][H][D] (the reference's torch.cat of cached frames:
+ * causal_model.py:1155-1156, memory_retrieval.py:79-86).  out_dtype must equal pool_dtype
+ * (an fp8 pool is copied as raw codes; its scales stay in the scale arrays).
+ */
+int skv_gather(const void* k_pool, const void* v_pool, int pool_dtype, int n_slots,
+               const int32_t* slots /* host */, int n_frames, int batch, int heads, int head_dim,
+               int frame_tokens, void* k_out, void* v_out, int64_t out_sb, int64_t out_st,
+               int64_t out_sh, skv_stream_t stream);
+
+/*
+ * skv_attention — out = softmax(q kᵀ · softmax_scale) v over the keys of the frame list
+ * frame_slots[0..n_frames) (host array) taken in order, i.e. n_keys = n_frames * T.
+ * Replaces attention(q, cat[sink, local]) of causal_model.py:1135-1226 → attention.py:141-188
+ * (mask_mode NONE) and the chunk-causal FlexAttention of causal_model.py:474-534, :984-989
+ * (mask_mode CHUNK_CAUSAL, query i at position q_pos0 + i).
+ * q and out are token-major [B][Lq][H][D]; q_dtype in {F32, BF16} (F32 is rounded to bf16 as the
+ * reference's flash path does, attention.py:69-73), out_dtype == q_dtype.  Pools may be F32,
+ * BF16 or FP8_E4M3 (k_scale / v_scale required for FP8).  Compute: bf16 (fp8 for FP8 pools)
+ * matrix-core products with fp32 accumulation and an fp32 online softmax.
+ */
+int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                  const void* k_pool, const void* v_pool, const float* k_scale,
+                  const float* v_scale, int pool_dtype, int n_slots,
+                  const int32_t* frame_slots /* host */, int n_frames, int batch, int heads,
+                  int head_dim, int q_len, int frame_tokens, float softmax_scale, int mask_mode,
+                  int64_t q_pos0, int64_t chunk_tokens, void* out, int64_t out_sb,
+                  int64_t out_st, int64_t out_sh, skv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOLARKV_H */

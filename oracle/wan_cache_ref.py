@@ -1,0 +1,360 @@
+"""CPU restatement of SolarWM's KV-cache inference path — TEST INFRASTRUCTURE ONLY.
+
+Written from reading the reference (not imported, not copied); citations are
+``solar/backends/wan22/runtime/...`` relative to the reference repository.  The functions keep
+the reference's op sequence — clone the cache, memmove the non-sink window, slice-assign the
+chunk, ``cat`` sink and local windows, attention — on dense ``[B, tokens, H, D]`` CPU tensors.
+
+Pinning (tests/test_oracle.py):
+* ``cached_self_attention`` / ``apply_cache_updates`` index math and data movement — the
+  published C1 known answer (visible key counts 1170..8190, evicted frames {1,2,3}, {4,5,6},
+  {7,8,9}, final order [0, 10..29]); a token-labelled brute-force list model of "sink frames +
+  the most recent window" on many geometries; recompute and ``none``-pass invariants.
+* ``attention`` — explicit float64 loops of softmax(q kᵀ/√d) v; closed forms (identical keys →
+  mean of V; one key → V; key-order invariance).
+* ``inference_window_mask`` / ``block_classes`` — brute-force rule "chunk i sees chunks 0..i"
+  and per-block full/partial/empty from the dense mask.
+* ``fp8_quantize`` — every e4m3fn code decoded from sign/exponent/mantissa; each quantised value
+  is the nearest code (ties to even) found by exhaustive search.
+* ``memory_gather`` — index semantics checked against per-frame slicing.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any, Callable, Sequence
+
+import torch
+
+E4M3_MAX = 448.0
+
+
+# ---------------------------------------------------------------------------------------------
+# attention (attention.py:141-188 — flash path semantics: cast non-half inputs to bf16,
+# compute, return in q's dtype)
+# ---------------------------------------------------------------------------------------------
+def attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    softmax_scale: float | None = None,
+    mask: torch.Tensor | None = None,
+    compute_dtype: torch.dtype = torch.float64,
+    round_inputs_to_bf16: bool = True,
+) -> torch.Tensor:
+    """softmax(q kᵀ · scale [masked]) v for [B, L, H, D]; ``mask`` [Lq, Lk] bool (True = keep).
+
+    Inputs are first rounded to bf16 (attention.py:69-73 ``half()``), then the product is
+    evaluated in ``compute_dtype`` with torch's SDPA math (the reference's own fallback op,
+    attention.py:172-188) and returned in ``q.dtype`` (attention.py:138).
+    """
+    out_dtype = q.dtype
+    if round_inputs_to_bf16:
+        q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    qt = q.transpose(1, 2).to(compute_dtype)
+    kt = k.transpose(1, 2).to(compute_dtype)
+    vt = v.transpose(1, 2).to(compute_dtype)
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else softmax_scale
+    out = torch.nn.functional.scaled_dot_product_attention(
+        qt, kt, vt, attn_mask=mask, scale=scale
+    )
+    return out.transpose(1, 2).contiguous().to(out_dtype)
+
+
+def sdpa_fallback_attention(q, k, v):
+    """The reference's SDPA fallback exactly (attention.py:172-188): bf16 SDPA, bf16 result.
+    Used as the timed CPU baseline of the reference path."""
+    qt = q.transpose(1, 2).to(torch.bfloat16)
+    kt = k.transpose(1, 2).to(torch.bfloat16)
+    vt = v.transpose(1, 2).to(torch.bfloat16)
+    out = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt)
+    return out.transpose(1, 2).contiguous()
+
+
+# ---------------------------------------------------------------------------------------------
+# cache allocation (stage2.py:1758-1817)
+# ---------------------------------------------------------------------------------------------
+def allocate_kv_cache(
+    num_layers: int,
+    batch_size: int,
+    cache_tokens: int,
+    num_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+) -> list[dict[str, Any]]:
+    return [
+        {
+            "k": torch.zeros(batch_size, cache_tokens, num_heads, head_dim, dtype=dtype),
+            "v": torch.zeros(batch_size, cache_tokens, num_heads, head_dim, dtype=dtype),
+            "global_end_index": torch.zeros(1, dtype=torch.long),
+            "local_end_index": torch.zeros(1, dtype=torch.long),
+        }
+        for _ in range(num_layers)
+    ]
+
+
+# ---------------------------------------------------------------------------------------------
+# the cache branch of CausalWanSelfAttention.forward (causal_model.py:1028-1235), with q/k/v
+# already projected and K already roped (RoPE is the identity here: inputs are post-RoPE)
+# ---------------------------------------------------------------------------------------------
+def cached_self_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_cache: dict[str, Any],
+    *,
+    current_start: int,
+    frame_seqlen: int,
+    sink_size: int,
+    local_attn_size: int,
+    sink_recache_after_switch: bool = False,
+    attn_fn: Callable[..., torch.Tensor] = attention,
+    memory_k: torch.Tensor | None = None,
+    memory_v: torch.Tensor | None = None,
+):
+    """Returns ``(x [B, Lq, H, D], (current_end, local_end_index, cache_update_info))``.
+
+    ``memory_k``/``memory_v`` ([B, M, H, D], already gathered) are placed ahead of the window,
+    as the H3 memory path orders ``[bank | history | current]`` (memory_kv_attention.py:97-137).
+    """
+    max_attention_size = 39600 if local_attn_size == -1 else local_attn_size * frame_seqlen
+    current_end = current_start + q.shape[1]
+    sink_tokens = sink_size * frame_seqlen
+    kv_cache_size = kv_cache["k"].shape[1]
+    num_new_tokens = q.shape[1]
+    global_end = int(kv_cache["global_end_index"].item())
+    local_end = int(kv_cache["local_end_index"].item())
+    is_recompute = current_end <= global_end and current_start > 0
+
+    if (
+        local_attn_size != -1
+        and current_end > global_end
+        and num_new_tokens + local_end > kv_cache_size
+    ):
+        # rolling: evict the oldest non-sink tokens (causal_model.py:1036-1094)
+        num_evicted = num_new_tokens + local_end - kv_cache_size
+        num_rolled = local_end - num_evicted - sink_tokens
+        local_end_index = local_end + current_end - global_end - num_evicted
+        local_start_index = local_end_index - num_new_tokens
+        temp_k = kv_cache["k"].detach().clone()
+        temp_v = kv_cache["v"].detach().clone()
+        src = slice(sink_tokens + num_evicted, sink_tokens + num_evicted + num_rolled)
+        dst = slice(sink_tokens, sink_tokens + num_rolled)
+        temp_k[:, dst] = temp_k[:, src].clone()
+        temp_v[:, dst] = temp_v[:, src].clone()
+        write_start = max(local_start_index, sink_tokens) if is_recompute else local_start_index
+        roped_offset = max(0, write_start - local_start_index)
+        write_len = max(0, local_end_index - write_start)
+        if write_len > 0:
+            temp_k[:, write_start:local_end_index] = k[:, roped_offset : roped_offset + write_len]
+            temp_v[:, write_start:local_end_index] = v[:, roped_offset : roped_offset + write_len]
+        info = {
+            "action": "roll_and_insert",
+            "sink_tokens": sink_tokens,
+            "num_rolled_tokens": num_rolled,
+            "num_evicted_tokens": num_evicted,
+            "local_start_index": local_start_index,
+            "local_end_index": local_end_index,
+            "write_start_index": write_start,
+            "write_end_index": local_end_index,
+            "new_k": k[:, roped_offset : roped_offset + write_len],
+            "new_v": v[:, roped_offset : roped_offset + write_len],
+            "current_end": current_end,
+            "is_recompute": is_recompute,
+        }
+    else:
+        # direct insert (causal_model.py:1095-1133)
+        local_end_index = local_end + current_end - global_end
+        local_start_index = local_end_index - num_new_tokens
+        temp_k = kv_cache["k"].detach().clone()
+        temp_v = kv_cache["v"].detach().clone()
+        write_start = max(local_start_index, sink_tokens) if is_recompute else local_start_index
+        if sink_recache_after_switch:
+            write_start = local_start_index
+        roped_offset = max(0, write_start - local_start_index)
+        write_len = max(0, local_end_index - write_start)
+        if write_len > 0:
+            temp_k[:, write_start:local_end_index] = k[:, roped_offset : roped_offset + write_len]
+            temp_v[:, write_start:local_end_index] = v[:, roped_offset : roped_offset + write_len]
+        info = {
+            "action": "direct_insert",
+            "local_start_index": local_start_index,
+            "local_end_index": local_end_index,
+            "write_start_index": write_start,
+            "write_end_index": local_end_index,
+            "new_k": k[:, roped_offset : roped_offset + write_len],
+            "new_v": v[:, roped_offset : roped_offset + write_len],
+            "current_end": current_end,
+            "is_recompute": is_recompute,
+        }
+
+    # visible window (causal_model.py:1135-1199)
+    if sink_tokens > 0:
+        local_budget = max_attention_size - sink_tokens
+        active_sink = min(sink_tokens, local_end_index)
+        parts_k = [temp_k[:, :active_sink]]
+        parts_v = [temp_v[:, :active_sink]]
+        if local_budget > 0:
+            local_start_for_window = max(sink_tokens, local_end_index - local_budget)
+            parts_k.append(temp_k[:, local_start_for_window:local_end_index])
+            parts_v.append(temp_v[:, local_start_for_window:local_end_index])
+        k_cat = torch.cat(parts_k, dim=1)
+        v_cat = torch.cat(parts_v, dim=1)
+    else:
+        window_start = max(0, local_end_index - max_attention_size)
+        k_cat = temp_k[:, window_start:local_end_index]
+        v_cat = temp_v[:, window_start:local_end_index]
+    if memory_k is not None:
+        k_cat = torch.cat([memory_k.to(k_cat.dtype), k_cat], dim=1)
+        v_cat = torch.cat([memory_v.to(v_cat.dtype), v_cat], dim=1)
+    if k_cat.shape[1] == 0:
+        raise RuntimeError("KV-cache attention window is empty")
+    x = attn_fn(q, k_cat, v_cat)
+    return x, (current_end, local_end_index, info)
+
+
+def apply_cache_updates(kv_cache: list[dict[str, Any]], cache_update_infos) -> None:
+    """CausalWanModel._apply_cache_updates (causal_model.py:2856-2921)."""
+    with torch.no_grad():
+        for block_index, (current_end, local_end_index, info) in cache_update_infos:
+            if info is not None:
+                cache = kv_cache[block_index]
+                ws = info.get("write_start_index", info["local_start_index"])
+                we = info.get("write_end_index", info["local_end_index"])
+                new_k = info["new_k"].detach()
+                new_v = info["new_v"].detach()
+                if info["action"] == "roll_and_insert":
+                    s = info["sink_tokens"]
+                    r = info["num_rolled_tokens"]
+                    e = info["num_evicted_tokens"]
+                    cache["k"][:, s : s + r] = cache["k"][:, s + e : s + e + r].clone()
+                    cache["v"][:, s : s + r] = cache["v"][:, s + e : s + e + r].clone()
+                if we > ws and new_k.shape[1] == we - ws:
+                    cache["k"][:, ws:we] = new_k
+                    cache["v"][:, ws:we] = new_v
+            is_recompute = False if info is None else info.get("is_recompute", False)
+            if not is_recompute:
+                kv_cache[block_index]["global_end_index"].fill_(current_end)
+                kv_cache[block_index]["local_end_index"].fill_(local_end_index)
+
+
+# ---------------------------------------------------------------------------------------------
+# rollout driver: per chunk, N "none" passes then commit (stage2.py:674-760).  `passes` lists
+# the policy of each forward of a chunk, e.g. ["none"] * 4 + ["commit"] (reference NFE4) or
+# ["none", "commit"].
+# ---------------------------------------------------------------------------------------------
+def rollout(
+    num_chunks: int,
+    passes: Sequence[str],
+    chunk_tokens: int,
+    layer_inputs: Callable[[int, int, int], tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
+    kv_cache: list[dict[str, Any]],
+    *,
+    frame_seqlen: int,
+    sink_size: int,
+    local_attn_size: int,
+    attn_fn: Callable[..., torch.Tensor] = attention,
+    on_output: Callable[[int, int, int, torch.Tensor], None] | None = None,
+) -> None:
+    """Drive ``cached_self_attention`` over every layer; ``layer_inputs(chunk, pass, layer)``
+    returns that layer's (q, k, v)."""
+    for c in range(num_chunks):
+        current_start = c * chunk_tokens
+        for p, policy in enumerate(passes):
+            infos = []
+            for layer in range(len(kv_cache)):
+                q, k, v = layer_inputs(c, p, layer)
+                x, upd = cached_self_attention(
+                    q, k, v, kv_cache[layer], current_start=current_start,
+                    frame_seqlen=frame_seqlen, sink_size=sink_size,
+                    local_attn_size=local_attn_size, attn_fn=attn_fn,
+                )
+                infos.append((layer, upd))
+                if on_output is not None:
+                    on_output(c, p, layer, x)
+            if policy != "none":
+                apply_cache_updates(kv_cache, infos)
+
+
+# ---------------------------------------------------------------------------------------------
+# chunk-causal mask (build_inference_window_block_mask, causal_model.py:474-534) and the block
+# classification of _build_direct_block_mask (:245-302)
+# ---------------------------------------------------------------------------------------------
+def inference_window_mask(
+    num_clean_frames: int, num_noisy_frames: int, frame_seqlen: int, num_frame_per_block: int
+) -> tuple[torch.Tensor, int]:
+    """Dense [P, P] mask over the right-padded sequence (P = total rounded up to 128) and the
+    pad length, evaluating the reference's mask_mod for every (q, kv) pair."""
+    total = (num_clean_frames + num_noisy_frames) * frame_seqlen
+    padded = math.ceil(total / 128) * 128
+    block = frame_seqlen * num_frame_per_block
+    qi = torch.arange(padded)[:, None]
+    ki = torch.arange(padded)[None, :]
+    valid_q = qi < total
+    chunk_index = qi // block
+    causal = ki < torch.clamp((chunk_index + 1) * block, max=total)
+    eye = qi == ki
+    return eye | (valid_q & causal), padded - total
+
+
+def block_classes(dense: torch.Tensor, block: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """(full, partial) [nq, nk] block matrices of a dense mask: full = every entry visible,
+    partial = some but not all."""
+    n = dense.shape[0]
+    nb = math.ceil(n / block)
+    full = torch.zeros(nb, nb, dtype=torch.bool)
+    partial = torch.zeros(nb, nb, dtype=torch.bool)
+    for i in range(nb):
+        for j in range(nb):
+            tile = dense[i * block : (i + 1) * block, j * block : (j + 1) * block]
+            full[i, j] = bool(tile.all())
+            partial[i, j] = bool(tile.any()) and not bool(tile.all())
+    return full, partial
+
+
+# ---------------------------------------------------------------------------------------------
+# memory bank gather (memory_retrieval.py:79-86): concatenate bank frames at arbitrary indices
+# ---------------------------------------------------------------------------------------------
+def memory_gather(bank: torch.Tensor, indices: Sequence[int], frame_seqlen: int) -> torch.Tensor:
+    """``bank`` [B, n_frames*T, H, D] → cat of frames ``indices`` along tokens."""
+    if not len(indices):
+        return bank[:, :0]
+    return torch.cat(
+        [bank[:, int(i) * frame_seqlen : (int(i) + 1) * frame_seqlen] for i in indices], dim=1
+    )
+
+
+# ---------------------------------------------------------------------------------------------
+# fp8 e4m3fn quantisation with one scale per (frame, head): scale = absmax / 448
+# ---------------------------------------------------------------------------------------------
+def fp8_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantise one frame of one head per leading index.
+
+    ``x`` [..., T, D] (bf16 or fp32) → (codes float8_e4m3fn [..., T, D], scale float32 [...]).
+    inv = 448 / absmax in fp32, y = clamp(x * inv, ±448) in fp32, code = RNE(y); absmax 0 → all
+    codes 0 and scale 0.
+    """
+    xf = x.float()
+    amax = xf.abs().amax(dim=(-2, -1))
+    inv = torch.where(amax > 0, torch.tensor(E4M3_MAX, dtype=torch.float32) / amax,
+                      torch.zeros_like(amax))
+    y = (xf * inv[..., None, None]).clamp(-E4M3_MAX, E4M3_MAX)
+    codes = y.to(torch.float8_e4m3fn)
+    scale = amax / torch.tensor(E4M3_MAX, dtype=torch.float32)
+    return codes, scale
+
+
+def fp8_dequantize(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    return codes.float() * scale[..., None, None]
+
+
+def e4m3_decode(code: int) -> float:
+    """Value of an e4m3fn byte from its fields (bias 7; e=0 subnormal; 0x7f/0xff NaN)."""
+    s = -1.0 if code & 0x80 else 1.0
+    e = (code >> 3) & 0xF
+    m = code & 0x7
+    if e == 0xF and m == 0x7:
+        return float("nan")
+    if e == 0:
+        return s * m * 2.0**-9
+    return s * (1.0 + m / 8.0) * 2.0 ** (e - 7)

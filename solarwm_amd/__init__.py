@@ -1,0 +1,25 @@
+"""solarwm_amd — MI355X-native block-causal KV-cache inference path for SolarWM-style
+chunked autoregressive video models.
+
+Public surface (the reference's call signatures, solar/backends/wan22/runtime):
+* :func:`make_kv_cache_allocator` → ``allocate_kv_cache(batch_size, *, dtype, device)``
+* :class:`SlotKVCache` — one layer's cache (dict surface ``k``/``v``/``*_end_index``)
+* :func:`attend_cached`, :func:`apply_cache_updates` — cached self-attention + deferred commit
+* :func:`attention`, :func:`chunk_causal_attention` — dense drop-in attention ops
+* :mod:`solarwm_amd.kernels` — thin wrappers of the C ABI in include/solarkv.h
+"""
+
+from .attention import apply_cache_updates, attend_cached, attention, chunk_causal_attention
+from .cache import CacheGeometry, CachePlan, SlotKVCache, make_kv_cache_allocator, plan_cached_forward
+
+__all__ = [
+    "CacheGeometry",
+    "CachePlan",
+    "SlotKVCache",
+    "apply_cache_updates",
+    "attend_cached",
+    "attention",
+    "chunk_causal_attention",
+    "make_kv_cache_allocator",
+    "plan_cached_forward",
+]

@@ -1,0 +1,98 @@
+"""ctypes binding of libsolarkv.so (the C ABI declared in include/solarkv.h).
+
+The library is loaded from the package directory only (it is built in-tree by
+``solarwm_amd.build``).  There is no fallback implementation: if the library is missing every
+entry point raises, so a product path can never silently run on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libsolarkv.so"
+
+SKV_F32 = 0
+SKV_BF16 = 1
+SKV_FP8_E4M3 = 2
+
+SKV_MASK_NONE = 0
+SKV_MASK_CHUNK_CAUSAL = 1
+
+SKV_OK = 0
+SKV_E_ARG = -1
+SKV_E_UNSUPPORTED = -2
+SKV_E_LAUNCH = -3
+
+SKV_MAX_APPEND_FRAMES = 64
+SKV_MAX_FRAMES = 256
+
+# Every symbol include/solarkv.h declares, with (restype, argtypes).
+_i32, _i64, _f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+_i32p = ctypes.POINTER(ctypes.c_int32)
+SIGNATURES: dict[str, tuple] = {
+    "skv_version": (_i32, []),
+    "skv_last_error": (ctypes.c_char_p, []),
+    "skv_append": (
+        _i32,
+        [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32p, _i32,
+         _i32, _i32, _i32, _i32, _vp],
+    ),
+    "skv_gather": (
+        _i32,
+        [_vp, _vp, _i32, _i32, _i32p, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _i64, _i64,
+         _vp],
+    ),
+    "skv_attention": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32p, _i32, _i32, _i32,
+         _i32, _i32, _i32, _f32, _i32, _i64, _i64, _vp, _i64, _i64, _i64, _vp],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class SolarKVError(RuntimeError):
+    """A libsolarkv entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn} failed with status {status}: {message}")
+        self.fn = fn
+        self.status = status
+        self.message = message
+
+
+def load() -> ctypes.CDLL:
+    """Load libsolarkv.so once per process; raise if it is absent."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -m solarwm_amd.build` "
+                "(there is no CPU fallback for the KV-cache kernels)"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != SKV_OK:
+        msg = load().skv_last_error().decode(errors="replace")
+        if status in (SKV_E_ARG, SKV_E_UNSUPPORTED):
+            raise ValueError(f"{fn}: {msg}")
+        raise SolarKVError(fn, status, msg)
+
+
+def int32_array(values) -> ctypes.Array:
+    vals = [int(v) for v in values]
+    return (ctypes.c_int32 * max(1, len(vals)))(*vals)

@@ -1,0 +1,196 @@
+"""Attention entry points with the reference's call signatures.
+
+* :func:`attention` — drop-in for ``attention(q, k, v, ...)`` of
+  solar/backends/wan22/runtime/modeling/attention.py:141-188 (dense ``[B, L, H, D]`` inputs).
+* :func:`chunk_causal_attention` — the chunk-causal FlexAttention of the cache-free
+  inference-window path (causal_model.py:474-534, :984-989).
+* :func:`attend_cached` — the KV-cache branch of ``CausalWanSelfAttention.forward``
+  (causal_model.py:1028-1235) after projection and RoPE: appends the chunk, resolves eviction and
+  the sink|local window through the slot table and attends, returning the reference's
+  ``(x, (current_end, local_end_index, cache_update_info))`` pair.
+* :func:`apply_cache_updates` — the deferred commit ``CausalWanModel._apply_cache_updates``
+  (causal_model.py:2856-2921).
+
+Every call runs the HIP kernels of libsolarkv.so; there is no other code path.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Iterable, Sequence
+
+import torch
+
+from . import _lib, kernels
+from .cache import CacheUpdate, SlotKVCache
+
+
+def _pack_dense(k: torch.Tensor, v: torch.Tensor, pool_dtype: torch.dtype):
+    """Stage dense K/V [B, L, H, D] as a one-frame pool (V transposed) for the kernel."""
+    b, lk, h, _ = k.shape
+    kpool, vpool, _, _ = kernels.new_pools(1, b, h, lk, pool_dtype, k.device)
+    kernels.append_frames(k, v, kpool, vpool, [0], frame_tokens=lk)
+    return kpool, vpool
+
+
+def _dense_attention(q, k, v, softmax_scale, mask_mode=_lib.SKV_MASK_NONE, q_pos0=0, chunk=0):
+    kpool, vpool = _pack_dense(k, v, k.dtype)
+    return kernels.attention_frames(
+        q, kpool, vpool, [0], frame_tokens=k.shape[1], softmax_scale=softmax_scale,
+        mask_mode=mask_mode, q_pos0=q_pos0, chunk_tokens=chunk,
+    )
+
+
+def attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_lens: torch.Tensor | None = None,
+    k_lens: torch.Tensor | None = None,
+    dropout_p: float = 0.0,
+    softmax_scale: float | None = None,
+    q_scale: float | None = None,
+    causal: bool = False,
+    window_size: tuple[int, int] = (-1, -1),
+    deterministic: bool = False,
+    dtype: torch.dtype = torch.bfloat16,
+    fa_version: int | None = None,
+) -> torch.Tensor:
+    """softmax(q kᵀ · scale) v for ``[B, L, H, D]`` tensors; returns ``q.dtype`` like the
+    reference's flash path (attention.py:66-138).  ``q_lens``/``k_lens`` select per-sample
+    prefixes (varlen); rows past ``q_lens[b]`` are returned as zeros.  Dropout, causal and
+    sliding-window options are not used by the cached path and raise ``NotImplementedError``.
+    """
+    if dropout_p:
+        raise NotImplementedError("dropout is not supported by the inference kernels")
+    if causal or tuple(window_size) != (-1, -1):
+        raise NotImplementedError("causal / sliding-window attention is not on this path")
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise AssertionError("dtype must be float16 or bfloat16")  # attention.py:63-64
+    out_dtype = q.dtype
+    if q.shape[-1] != kernels.HEAD_DIM:
+        raise ValueError(f"head_dim must be {kernels.HEAD_DIM}")
+    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("q, k, v must be [B, L, H, D] with matching B, H and k.shape == v.shape")
+    # attention.py:69-73 casts non-half inputs to `dtype` and q, k to v's dtype.  The kernels
+    # compute in bf16 and round fp32 operands to bf16 on load, which is that cast for
+    # dtype=bfloat16; fp16 arithmetic is not provided.
+    if torch.float16 in (q.dtype, k.dtype, v.dtype) or (
+        dtype == torch.float16 and v.dtype == torch.float32
+    ):
+        raise NotImplementedError("float16 attention is not provided (bf16 matrix path only)")
+    kv_dtype = v.dtype
+    qh, kh, vh = q.to(kv_dtype), k.to(kv_dtype), v
+    if q_scale is not None:
+        qh = (qh.float() * q_scale).to(kv_dtype)
+    if q_lens is None and k_lens is None:
+        out = _dense_attention(qh.contiguous(), kh.contiguous(), vh.contiguous(), softmax_scale)
+        return out.to(out_dtype)
+    b, lq = q.shape[:2]
+    lk = k.shape[1]
+    ql = [lq] * b if q_lens is None else [int(x) for x in q_lens.tolist()]
+    kl = [lk] * b if k_lens is None else [int(x) for x in k_lens.tolist()]
+    out = torch.zeros(q.shape, dtype=kv_dtype, device=q.device)
+    for i in range(b):
+        if ql[i] == 0:
+            continue
+        if kl[i] == 0:
+            raise RuntimeError("attention over an empty key window")
+        o = _dense_attention(
+            qh[i : i + 1, : ql[i]].contiguous(),
+            kh[i : i + 1, : kl[i]].contiguous(),
+            vh[i : i + 1, : kl[i]].contiguous(),
+            softmax_scale,
+        )
+        out[i : i + 1, : ql[i]] = o
+    return out.to(out_dtype)
+
+
+def chunk_causal_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    chunk_tokens: int,
+    q_pos0: int = 0,
+    softmax_scale: float | None = None,
+) -> torch.Tensor:
+    """Chunk-causal attention of ``build_inference_window_block_mask`` (causal_model.py:474-534):
+    query ``i`` (sequence position ``q_pos0 + i``) sees keys ``< min((pos // chunk + 1) * chunk,
+    Lk)``.  Inputs ``[B, L, H, D]`` (bf16 or fp32); returns ``q.dtype``.  Rows beyond the valid
+    length that FlexAttention pads (the mask's "eye" rows) do not exist here: nothing is padded.
+    """
+    if chunk_tokens <= 0:
+        raise ValueError("chunk_tokens must be positive")
+    out_dtype = q.dtype
+    kv_dtype = torch.bfloat16 if k.dtype not in (torch.float32, torch.bfloat16) else k.dtype
+    return _dense_attention(
+        q.to(kv_dtype), k.to(kv_dtype), v.to(kv_dtype), softmax_scale,
+        mask_mode=_lib.SKV_MASK_CHUNK_CAUSAL, q_pos0=q_pos0, chunk=chunk_tokens,
+    ).to(out_dtype)
+
+
+def attend_cached(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_cache: SlotKVCache,
+    current_start: int = 0,
+    *,
+    sink_recache_after_switch: bool = False,
+    memory_frames: Sequence[int] | None = None,
+    softmax_scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, tuple[int, int, CacheUpdate]]:
+    """One layer's cached self-attention (causal_model.py:1028-1235, post-projection/RoPE).
+
+    ``q``, ``k``, ``v`` are the chunk's ``[B, Lq, H, D]`` query/key/value (K already roped, as
+    stored in the cache).  The chunk is appended into staging slots, the visible window is the
+    reference's ``cat[sink, local]`` (including the chunk), optionally preceded by memory-bank
+    frames ``memory_frames`` (bank indices, in order), and nothing in the committed cache
+    changes until :func:`apply_cache_updates`.  Returns ``(out [B, Lq, H, D], (current_end,
+    local_end_index, update))``.
+    """
+    g = kv_cache.geom
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k, v must all be [B, Lq, H, D] of the same shape")
+    if q.shape[0] != g.batch or q.shape[2] != g.heads or q.shape[3] != g.head_dim:
+        raise ValueError(
+            f"chunk shape {tuple(q.shape)} does not match the cache (B={g.batch}, H={g.heads}, "
+            f"D={g.head_dim})"
+        )
+    if kv_cache.dtype != torch.float8_e4m3fn and k.dtype != kv_cache.dtype:
+        raise ValueError(f"k/v dtype {k.dtype} differs from the cache dtype {kv_cache.dtype}")
+    plan, temp, staging, window = kv_cache.plan(
+        int(current_start), q.shape[1], sink_recache_after_switch
+    )
+    T = g.frame_tokens
+    if plan.write_len > 0:
+        kernels.append_frames(
+            k, v, kv_cache.kpool, kv_cache.vpool, staging, frame_tokens=T,
+            src_frame0=plan.roped_offset // T, kscale=kv_cache.kscale, vscale=kv_cache.vscale,
+        )
+    frames = list(kv_cache.bank_slots(memory_frames)) if memory_frames else []
+    frames.extend(window)
+    if not frames:
+        raise RuntimeError("KV-cache attention window is empty")  # causal_model.py:785-787
+    x = kernels.attention_frames(
+        q, kv_cache.kpool, kv_cache.vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
+        kscale=kv_cache.kscale, vscale=kv_cache.vscale, out=out,
+    )
+    update = kv_cache.stage(plan, temp)
+    return x, (plan.current_end, plan.local_end_index, update)
+
+
+def apply_cache_updates(
+    kv_cache: Sequence[SlotKVCache],
+    cache_update_infos: Iterable[tuple[int, tuple[int, int, CacheUpdate | None]]],
+) -> None:
+    """Deferred commit of every block's update (causal_model.py:2856-2921): the table takes the
+    staged frames; indices advance unless the forward was a recompute."""
+    for block_index, (current_end, local_end_index, update) in cache_update_infos:
+        kv_cache[block_index].commit(update, current_end, local_end_index)
+
+
+def default_softmax_scale(head_dim: int = kernels.HEAD_DIM) -> float:
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,445 @@
+"""Frame-slot KV cache: the per-layer cache object of the block-causal inference path.
+
+The reference keeps each layer's cache as a dense ``[B, cache_tokens, H, D]`` buffer and, on
+every forward, clones it, memmoves the non-sink window to evict the oldest frames and
+slice-assigns the new chunk (solar/backends/wan22/runtime/modeling/causal_model.py:1028-1133;
+deferred commit :2856-2921).  Here the same cache is a pool of frame slots plus a host-side
+slot table:
+
+* ``table[p]`` is the pool slot holding reference cache rows ``[p*T, (p+1)*T)``;
+* eviction is the table permutation the reference's memmove performs (no bytes move);
+* the chunk being denoised is appended into free "staging" slots on every pass; committing it
+  is a table update (the reference's commit re-does the memmove and the copy);
+* all index state (``global_end_index``/``local_end_index``) is host integers, so no device to
+  host synchronisation happens on the path (the reference does ``.item()`` several times per
+  layer per pass, causal_model.py:1034-1051).
+
+All token counts the reference manipulates must be whole frames (true for every Wan
+configuration: chunks, capacity, sink and ``current_start`` are frame multiples); anything else
+raises ``ValueError``.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping
+from dataclasses import dataclass
+from typing import Any, Iterator, Sequence
+
+import torch
+
+from . import kernels
+
+# causal_model.py:572-574: local_attn_size == -1 means a fixed 39600-token attention budget.
+UNBOUNDED_ATTENTION_TOKENS = 39600
+
+
+@dataclass(frozen=True)
+class CacheGeometry:
+    """Static shape of one layer's cache.
+
+    ``capacity_frames`` is the reference's ``local_attn_size`` used by the allocator
+    (stage2.py:1778-1779: ``cache_tokens = local_attn_size * frame_sequence_length``).
+    """
+
+    batch: int
+    heads: int
+    head_dim: int
+    frame_tokens: int
+    capacity_frames: int
+    sink_frames: int = 0
+    local_attn_size: int | None = None  # frames; None -> capacity_frames; -1 -> unbounded
+    staging_frames: int = 3  # largest chunk (in frames) one call may write
+    bank_frames: int = 0  # memory-bank slots (never evicted), addressed by bank index
+
+    def __post_init__(self):
+        if self.head_dim != kernels.HEAD_DIM:
+            raise ValueError(f"head_dim must be {kernels.HEAD_DIM}, got {self.head_dim}")
+        for name in ("batch", "heads", "frame_tokens", "capacity_frames", "staging_frames"):
+            if getattr(self, name) <= 0:
+                raise ValueError(f"{name} must be positive")
+        if not 0 <= self.sink_frames <= self.capacity_frames:
+            raise ValueError("sink_frames must lie in [0, capacity_frames]")
+        if self.bank_frames < 0:
+            raise ValueError("bank_frames must be >= 0")
+
+    @property
+    def cache_tokens(self) -> int:
+        return self.capacity_frames * self.frame_tokens
+
+    @property
+    def sink_tokens(self) -> int:
+        return self.sink_frames * self.frame_tokens
+
+    @property
+    def max_attention_size(self) -> int:
+        las = self.capacity_frames if self.local_attn_size is None else self.local_attn_size
+        return UNBOUNDED_ATTENTION_TOKENS if las == -1 else las * self.frame_tokens
+
+    @property
+    def n_slots(self) -> int:
+        return self.capacity_frames + self.staging_frames + self.bank_frames
+
+    @property
+    def bank_slot0(self) -> int:
+        return self.capacity_frames + self.staging_frames
+
+
+@dataclass(frozen=True)
+class CachePlan:
+    """Index arithmetic of one cached forward, in tokens, exactly as the reference computes it
+    (causal_model.py:1028-1133), plus the visible window (:1135-1199)."""
+
+    current_start: int
+    current_end: int
+    num_new_tokens: int
+    sink_tokens: int
+    is_recompute: bool
+    action: str  # "roll_and_insert" | "direct_insert"
+    num_evicted_tokens: int
+    num_rolled_tokens: int
+    local_start_index: int
+    local_end_index: int
+    write_start_index: int
+    roped_offset: int
+    write_len: int
+    window: tuple[tuple[int, int], ...]  # visible [start, end) token ranges of the temp cache
+
+
+def plan_cached_forward(
+    geom: CacheGeometry,
+    global_end: int,
+    local_end: int,
+    current_start: int,
+    num_new_tokens: int,
+    sink_recache_after_switch: bool = False,
+) -> CachePlan:
+    """Restate the reference cache branch's scalar arithmetic.
+
+    Follows causal_model.py:1028-1052 (recompute / rolling test, eviction counts), :1096-1114
+    (direct insert), :1069-1073 / :1108-1114 (write window) and :1135-1199 (visible window).
+    """
+    sink = geom.sink_tokens
+    cap = geom.cache_tokens
+    current_end = current_start + num_new_tokens
+    is_recompute = current_end <= global_end and current_start > 0
+    rolling = (
+        geom.local_attn_size != -1
+        and current_end > global_end
+        and num_new_tokens + local_end > cap
+    )
+    if rolling:
+        evicted = num_new_tokens + local_end - cap
+        rolled = local_end - evicted - sink
+        new_local_end = local_end + current_end - global_end - evicted
+        local_start = new_local_end - num_new_tokens
+        write_start = max(local_start, sink) if is_recompute else local_start
+        action = "roll_and_insert"
+    else:
+        evicted = rolled = 0
+        new_local_end = local_end + current_end - global_end
+        local_start = new_local_end - num_new_tokens
+        write_start = max(local_start, sink) if is_recompute else local_start
+        if sink_recache_after_switch:
+            write_start = local_start
+        action = "direct_insert"
+    roped_offset = max(0, write_start - local_start)
+    write_len = max(0, new_local_end - write_start)
+
+    if sink > 0:
+        local_budget = geom.max_attention_size - sink
+        active_sink = min(sink, new_local_end)
+        window = [(0, active_sink)]
+        if local_budget > 0:
+            window.append((max(sink, new_local_end - local_budget), new_local_end))
+    else:
+        window = [(max(0, new_local_end - geom.max_attention_size), new_local_end)]
+    window = tuple((a, b) for a, b in window if b > a)
+    return CachePlan(
+        current_start=current_start,
+        current_end=current_end,
+        num_new_tokens=num_new_tokens,
+        sink_tokens=sink,
+        is_recompute=is_recompute,
+        action=action,
+        num_evicted_tokens=evicted,
+        num_rolled_tokens=rolled,
+        local_start_index=local_start,
+        local_end_index=new_local_end,
+        write_start_index=write_start,
+        roped_offset=roped_offset,
+        write_len=write_len,
+        window=window,
+    )
+
+
+def _frames(tokens: int, frame_tokens: int, what: str) -> int:
+    if tokens % frame_tokens:
+        raise ValueError(
+            f"{what}={tokens} is not a whole number of {frame_tokens}-token frames; the slot "
+            "cache only addresses whole frames"
+        )
+    return tokens // frame_tokens
+
+
+@dataclass
+class CacheUpdate:
+    """Deferred commit of one layer (the reference's ``cache_update_info`` dict,
+    causal_model.py:1082-1094 / :1123-1133)."""
+
+    plan: CachePlan
+    temp_table: tuple[int, ...]
+    pass_id: int
+    cache_id: int
+
+    # dict-style access to the reference's keys for callers that inspect the update
+    def __getitem__(self, key: str) -> Any:
+        p = self.plan
+        mapping = {
+            "action": p.action,
+            "sink_tokens": p.sink_tokens,
+            "num_rolled_tokens": p.num_rolled_tokens,
+            "num_evicted_tokens": p.num_evicted_tokens,
+            "local_start_index": p.local_start_index,
+            "local_end_index": p.local_end_index,
+            "write_start_index": p.write_start_index,
+            "write_end_index": p.local_end_index,
+            "current_end": p.current_end,
+            "is_recompute": p.is_recompute,
+        }
+        return mapping[key]
+
+    def get(self, key: str, default: Any = None) -> Any:
+        try:
+            return self[key]
+        except KeyError:
+            return default
+
+
+class SlotTable:
+    """Host state of one layer's cache: the reference's two indices and the slot table.
+
+    Pure host logic (no device memory), so the table algebra can be checked on any machine
+    against the reference's dense memmove semantics.
+    """
+
+    _next_id = 0
+
+    def __init__(self, geom: CacheGeometry):
+        self.geom = geom
+        SlotTable._next_id += 1
+        self._id = SlotTable._next_id
+        self.reset()
+
+    def reset(self) -> None:
+        self.global_end = 0
+        self.local_end = 0
+        # position frame p starts in slot p; slots 0..capacity-1 are zero-filled at allocation,
+        # matching the reference's torch.zeros cache (stage2.py:1780-1797)
+        self.table: list[int] = list(range(self.geom.capacity_frames))
+        self._pass_id = 0
+
+    def free_slots(self) -> list[int]:
+        used = set(self.table)
+        return [s for s in range(self.geom.bank_slot0) if s not in used]
+
+    def plan(
+        self, current_start: int, num_new_tokens: int, sink_recache_after_switch: bool = False
+    ) -> tuple[CachePlan, list[int], list[int], list[int]]:
+        """Plan one cached forward.
+
+        Returns ``(plan, temp_table, staging, window_slots)``: the table after the reference's
+        memmove + write (the ``temp_k`` of causal_model.py:1054-1080), the slots receiving the
+        written frames (free slots, so the committed cache is untouched), and the visible
+        frames' slots in attention order.
+        """
+        g = self.geom
+        T = g.frame_tokens
+        _frames(current_start, T, "current_start")
+        _frames(num_new_tokens, T, "num_new_tokens")
+        p = plan_cached_forward(
+            g, self.global_end, self.local_end, current_start, num_new_tokens,
+            sink_recache_after_switch,
+        )
+        sink_f = g.sink_frames
+        ev_f = _frames(p.num_evicted_tokens, T, "num_evicted_tokens")
+        rolled_f = _frames(p.num_rolled_tokens, T, "num_rolled_tokens")
+        ws_f = _frames(p.write_start_index, T, "write_start_index")
+        _frames(p.local_end_index, T, "local_end_index")
+        if p.local_end_index > g.cache_tokens or p.local_start_index < 0 or rolled_f < 0:
+            raise ValueError(
+                f"cache window [{p.local_start_index}, {p.local_end_index}) does not fit the "
+                f"{g.cache_tokens}-token cache"
+            )
+        wl_f = _frames(p.write_len, T, "write_len")
+        _frames(p.roped_offset, T, "roped_offset")
+        if wl_f > g.staging_frames:
+            raise ValueError(
+                f"a call writing {wl_f} frames exceeds the cache's {g.staging_frames} staging slots"
+            )
+
+        temp = list(self.table)
+        if p.action == "roll_and_insert" and rolled_f > 0:
+            src = temp[sink_f + ev_f : sink_f + ev_f + rolled_f]
+            temp[sink_f : sink_f + rolled_f] = src
+        staging = self.free_slots()[:wl_f]
+        for i in range(wl_f):
+            temp[ws_f + i] = staging[i]
+        window: list[int] = []
+        for a, b in p.window:
+            window.extend(temp[_frames(a, T, "window start") : _frames(b, T, "window end")])
+        return p, temp, staging, window
+
+    def stage(self, plan: CachePlan, temp_table: Sequence[int]) -> CacheUpdate:
+        """Record that this layer's staging slots now hold ``plan``'s chunk."""
+        self._pass_id += 1
+        return CacheUpdate(plan=plan, temp_table=tuple(temp_table), pass_id=self._pass_id,
+                           cache_id=self._id)
+
+    def commit(self, update: CacheUpdate | None, current_end: int, local_end_index: int) -> None:
+        """Apply a deferred update (mirrors causal_model.py:2863-2921 for one block)."""
+        if update is not None:
+            if update.cache_id != self._id:
+                raise RuntimeError("cache update belongs to a different cache")
+            if update.pass_id != self._pass_id:
+                raise RuntimeError(
+                    "stale cache update: another forward overwrote this layer's staging slots "
+                    "after the update was produced"
+                )
+            self.table = list(update.temp_table)
+            is_recompute = update.plan.is_recompute
+        else:
+            is_recompute = False
+        if not is_recompute:
+            self.global_end = int(current_end)
+            self.local_end = int(local_end_index)
+
+    def bank_slots(self, indices: Sequence[int]) -> list[int]:
+        g = self.geom
+        out = []
+        for i in indices:
+            i = int(i)
+            if not 0 <= i < g.bank_frames:
+                raise IndexError(f"memory-bank index {i} outside [0, {g.bank_frames})")
+            out.append(g.bank_slot0 + i)
+        return out
+
+
+class SlotKVCache(Mapping):
+    """One layer's KV cache in frame slots, with the reference dict surface.
+
+    Keys (stage2.py:1776-1798): ``"k"``/``"v"`` return the logical ``[B, cache_tokens, H, D]``
+    cache materialised by the gather kernel (for inspection; the hot path never builds it);
+    ``"global_end_index"``/``"local_end_index"`` return 1-element int64 CPU tensors mirroring
+    the host state.
+    """
+
+    def __init__(self, geom: CacheGeometry, *, dtype: torch.dtype, device: torch.device | str):
+        self.geom = geom
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.kpool, self.vpool, self.kscale, self.vscale = kernels.new_pools(
+            geom.n_slots, geom.batch, geom.heads, geom.frame_tokens, dtype, self.device
+        )
+        self.slots = SlotTable(geom)
+
+    def reset(self) -> None:
+        """Return to the freshly allocated state (every position reads as zeros)."""
+        self.slots.reset()
+        self.kpool.zero_()
+        self.vpool.zero_()
+        if self.kscale is not None:
+            self.kscale.zero_()
+            self.vscale.zero_()
+
+    @property
+    def global_end(self) -> int:
+        return self.slots.global_end
+
+    @property
+    def local_end(self) -> int:
+        return self.slots.local_end
+
+    @property
+    def table(self) -> list[int]:
+        return self.slots.table
+
+    def plan(self, current_start: int, num_new_tokens: int, sink_recache_after_switch=False):
+        return self.slots.plan(current_start, num_new_tokens, sink_recache_after_switch)
+
+    def stage(self, plan: CachePlan, temp_table: Sequence[int]) -> CacheUpdate:
+        return self.slots.stage(plan, temp_table)
+
+    def commit(self, update: CacheUpdate | None, current_end: int, local_end_index: int) -> None:
+        self.slots.commit(update, current_end, local_end_index)
+
+    def bank_slots(self, indices: Sequence[int]) -> list[int]:
+        return self.slots.bank_slots(indices)
+
+    def write_bank(self, indices: Sequence[int], k: torch.Tensor, v: torch.Tensor) -> None:
+        """Store frames of ``k``/``v`` ([B, len(indices)*T, H, D]) in memory-bank entries."""
+        kernels.append_frames(
+            k, v, self.kpool, self.vpool, self.bank_slots(indices),
+            frame_tokens=self.geom.frame_tokens, kscale=self.kscale, vscale=self.vscale,
+        )
+
+    def logical_kv(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The reference's physical cache contents, materialised from the slot table."""
+        return kernels.gather_frames(
+            self.kpool, self.vpool, self.table, frame_tokens=self.geom.frame_tokens
+        )
+
+    def __getitem__(self, key: str) -> Any:
+        if key == "k":
+            return self.logical_kv()[0]
+        if key == "v":
+            return self.logical_kv()[1]
+        if key == "global_end_index":
+            return torch.tensor([self.global_end], dtype=torch.long)
+        if key == "local_end_index":
+            return torch.tensor([self.local_end], dtype=torch.long)
+        raise KeyError(key)
+
+    def __iter__(self) -> Iterator[str]:
+        return iter(("k", "v", "global_end_index", "local_end_index"))
+
+    def __len__(self) -> int:
+        return 4
+
+
+def make_kv_cache_allocator(
+    *,
+    num_layers: int,
+    num_heads: int,
+    head_dim: int,
+    frame_sequence_length: int,
+    local_attn_size: int,
+    sink_size: int = 0,
+    num_frame_per_block: int = 3,
+    bank_frames: int = 0,
+    cache_dtype: torch.dtype | None = None,
+):
+    """Return ``allocate_kv_cache(batch_size, *, dtype, device) -> list[SlotKVCache]``.
+
+    Same signature as ``Wan5BStage2Runtime.allocate_kv_cache`` (stage2.py:1758-1817), so it can
+    be injected as that runtime's ``_kv_cache_allocator``.  ``cache_dtype`` overrides the storage
+    dtype (``torch.float8_e4m3fn`` for the fp8 cache); by default the model dtype is used.
+    """
+    if local_attn_size <= 0:
+        raise ValueError("the slot cache needs a positive local_attn_size (cache frames)")
+
+    def allocate_kv_cache(batch_size: int, *, dtype: torch.dtype, device: Any) -> list[SlotKVCache]:
+        geom = CacheGeometry(
+            batch=batch_size,
+            heads=num_heads,
+            head_dim=head_dim,
+            frame_tokens=frame_sequence_length,
+            capacity_frames=local_attn_size,
+            sink_frames=sink_size,
+            local_attn_size=local_attn_size,
+            staging_frames=num_frame_per_block,
+            bank_frames=bank_frames,
+        )
+        store = dtype if cache_dtype is None else cache_dtype
+        return [SlotKVCache(geom, dtype=store, device=device) for _ in range(num_layers)]
+
+    return allocate_kv_cache

@@ -1,0 +1,432 @@
+// Frame-slot K/V movement kernels for gfx950: append (token-major chunk -> pool slots, with
+// optional fp8 e4m3fn quantisation) and gather (pool slots -> token-major frames).
+//
+// The reference moves whole K/V windows on every forward (clone + memmove + slice-assign,
+// solar/backends/wan22/runtime/modeling/causal_model.py:1054-1080, :2881-2898).  Here a frame
+// is written once into a slot and never moved again; eviction is a slot-table update on the
+// host.  Both kernels are HBM-bound byte movers: one workgroup moves one 64-token tile of one
+// (frame, batch, head); K rows move as 16 B vectors, V is transposed through LDS so the pool
+// keeps V channel-major (tokens contiguous), which is what the attention kernel's PV product
+// reads.
+#include "skv_common.h"
+
+namespace skv {
+
+struct AppendArgs {
+  const void* ksrc;
+  const void* vsrc;
+  int64_t s_sb, s_st, s_sh;  // element strides of the token-major source
+  void* kpool;
+  void* vpool;
+  float* kscale;
+  float* vscale;
+  int64_t slot_stride;  // elements per slot in each pool (B*H*Tp*D)
+  int B, H, T, Tp, n_frames, src_frame0, ntiles;
+  int32_t slots[SKV_MAX_APPEND_FRAMES];
+};
+
+// LDS tile for the V transpose: 64 tokens x 128 channels, rows padded by 8 elements.
+constexpr int kVtRow = kHeadDim + 8;
+
+// grid.x = n_frames * B * H * ntiles (ntiles = Tp / 64), block = 256.
+template <typename E>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+  __shared__ E vt[kTile * kVtRow];
+  int wg = blockIdx.x;
+  const int t = wg % a.ntiles;
+  wg /= a.ntiles;
+  const int h = wg % a.H;
+  wg /= a.H;
+  const int b = wg % a.B;
+  const int f = wg / a.B;
+  const int64_t slot = a.slots[f];
+  const int tid = threadIdx.x;
+  const int tok0 = t * kTile;
+
+  const E* ks = static_cast<const E*>(a.ksrc);
+  const E* vs = static_cast<const E*>(a.vsrc);
+  const int64_t src_base = (int64_t)b * a.s_sb + (int64_t)h * a.s_sh +
+                           (int64_t)(a.src_frame0 + f) * a.T * a.s_st;
+  E* kp = static_cast<E*>(a.kpool) + slot * a.slot_stride +
+          ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+  E* vp = static_cast<E*>(a.vpool) + slot * a.slot_stride + (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
+
+  // 64 rows x 16 vec8 = 1024 vec8 per tile, 4 per thread.  Rows past T are zero padding.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = tid + 256 * r;
+    const int row = c >> 4, col = (c & 15) * 8;
+    const bool live = tok0 + row < a.T;
+    const int64_t so = src_base + (int64_t)(tok0 + row) * a.s_st + col;
+    Vec8<E> kv = live ? Vec8<E>::load(ks + so) : Vec8<E>::zero();
+    Vec8<E> vv = live ? Vec8<E>::load(vs + so) : Vec8<E>::zero();
+    kv.store(kp + row * kHeadDim + col);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vt[row * kVtRow + col + i] = vv.get(i);
+  }
+  __syncthreads();
+  // Transposed write: 128 channel rows x 8 vec8 (64 tokens) = 1024 vec8, 4 per thread.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = tid + 256 * r;
+    const int d = c >> 3, tc = (c & 7) * 8;
+    Vec8<E> o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o.set(i, vt[(tc + i) * kVtRow + d]);
+    o.store(vp + (int64_t)d * a.Tp + tc);
+  }
+}
+
+// fp8 append: one workgroup per (frame, batch, head, K|V).  Pass 1 reduces absmax over the
+// frame's T x 128 values; pass 2 re-reads them (L2/MALL resident), quantises with
+// inv = 448 / absmax and stores e4m3fn codes (V transposed through LDS).
+template <typename E>
+__device__ inline float absval8(const Vec8<E>& v, float m) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, __builtin_fabsf((float)v.get(i)));
+  return m;
+}
+
+template <typename E>
+__global__ __launch_bounds__(1024) void append_fp8_kernel(AppendArgs a) {
+  __shared__ float red[32];
+  __shared__ uint8_t vt8[kTile * (kHeadDim + 16)];
+  int wg = blockIdx.x;
+  const int is_v = wg & 1;
+  wg >>= 1;
+  const int h = wg % a.H;
+  wg /= a.H;
+  const int b = wg % a.B;
+  const int f = wg / a.B;
+  const int64_t slot = a.slots[f];
+  const int tid = threadIdx.x;
+
+  const E* src = static_cast<const E*>(is_v ? a.vsrc : a.ksrc);
+  src += (int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)(a.src_frame0 + f) * a.T * a.s_st;
+
+  // Pass 1: absmax over T rows x 16 vec8.
+  float m = 0.f;
+  const int nvec = a.T * 16;
+  for (int c = tid; c < nvec; c += 1024) {
+    const int row = c >> 4, col = (c & 15) * 8;
+    m = absval8(Vec8<E>::load(src + (int64_t)row * a.s_st + col), m);
+  }
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  if (tid < 64) {
+    float x = tid < 16 ? red[tid] : 0.f;
+    for (int off = 8; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    if (tid == 0) red[16] = x;
+  }
+  __syncthreads();
+  const float amax = red[16];
+  const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+  if (tid == 0) {
+    float* sc = is_v ? a.vscale : a.kscale;
+    sc[(slot * a.B + b) * a.H + h] = amax / 448.0f;
+  }
+
+  uint8_t* pool = static_cast<uint8_t*>(is_v ? a.vpool : a.kpool) + slot * a.slot_stride +
+                  (int64_t)(b * a.H + h) * a.Tp * kHeadDim;
+  // Pass 2: quantise tile by tile (64 tokens), padding rows encode 0.
+  for (int t0 = 0; t0 < a.Tp; t0 += kTile) {
+    const int c = tid;  // 64 rows x 16 vec8 = 1024 = one vec8 per thread
+    const int row = c >> 4, col = (c & 15) * 8;
+    const bool live = t0 + row < a.T;
+    Vec8<E> v = live ? Vec8<E>::load(src + (int64_t)(t0 + row) * a.s_st + col) : Vec8<E>::zero();
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float y = fminf(fmaxf((float)v.get(i) * inv, -448.0f), 448.0f);
+      uint32_t code = f32_to_e4m3(y);
+      if (i < 4) lo |= code << (8 * i); else hi |= code << (8 * (i - 4));
+    }
+    if (!is_v) {
+      *reinterpret_cast<u32x2*>(pool + (int64_t)(t0 + row) * kHeadDim + col) = u32x2{lo, hi};
+    } else {
+      *reinterpret_cast<u32x2*>(vt8 + row * (kHeadDim + 16) + col) = u32x2{lo, hi};
+      __syncthreads();
+      // channel d, tokens tc..tc+7 (8 B of codes)
+      const int d = c >> 3, tc = (c & 7) * 8;
+      uint32_t o0 = 0, o1 = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t code = vt8[(tc + i) * (kHeadDim + 16) + d];
+        if (i < 4) o0 |= code << (8 * i); else o1 |= code << (8 * (i - 4));
+      }
+      *reinterpret_cast<u32x2*>(pool + (int64_t)d * a.Tp + t0 + tc) = u32x2{o0, o1};
+      __syncthreads();
+    }
+  }
+}
+
+struct GatherArgs {
+  const void* kpool;
+  const void* vpool;
+  void* kout;
+  void* vout;
+  int64_t o_sb, o_st, o_sh;
+  int64_t slot_stride;
+  int B, H, T, Tp, n_frames, ntiles;
+  int32_t slots[SKV_MAX_FRAMES];
+};
+
+// grid.x = n_frames * B * H * ntiles, block = 256; E is the raw element type of the pool.
+template <typename E>
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+  __shared__ E vt[kHeadDim * (kTile + 8)];
+  int wg = blockIdx.x;
+  const int t = wg % a.ntiles;
+  wg /= a.ntiles;
+  const int h = wg % a.H;
+  wg /= a.H;
+  const int b = wg % a.B;
+  const int f = wg / a.B;
+  const int64_t slot = a.slots[f];
+  const int tid = threadIdx.x;
+  const int tok0 = t * kTile;
+  constexpr int kRow = kTile + 8;
+
+  const E* kp = static_cast<const E*>(a.kpool) + slot * a.slot_stride +
+                ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+  const E* vp = static_cast<const E*>(a.vpool) + slot * a.slot_stride +
+                (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
+  E* ko = static_cast<E*>(a.kout) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+          (int64_t)f * a.T * a.o_st;
+  E* vo = static_cast<E*>(a.vout) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+          (int64_t)f * a.T * a.o_st;
+
+  // V^T tile (128 channels x 64 tokens) -> LDS
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = tid + 256 * r;
+    const int d = c >> 3, tc = (c & 7) * 8;
+    Vec8<E> v = Vec8<E>::load(vp + (int64_t)d * a.Tp + tc);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vt[d * kRow + tc + i] = v.get(i);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = tid + 256 * r;
+    const int row = c >> 4, col = (c & 15) * 8;
+    if (tok0 + row < a.T) {
+      const int64_t oo = (int64_t)(tok0 + row) * a.o_st + col;
+      Vec8<E>::load(kp + row * kHeadDim + col).store(ko + oo);
+      Vec8<E> o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o.set(i, vt[(col + i) * kRow + row]);
+      o.store(vo + oo);
+    }
+  }
+}
+
+// fp8 pools hold raw bytes; gather copies the codes (scales stay in the scale arrays).
+struct U8x8 {
+  uint8_t b[8];
+};
+
+__global__ __launch_bounds__(256) void gather_u8_kernel(GatherArgs a) {
+  __shared__ uint8_t vt[kHeadDim * (kTile + 16)];
+  int wg = blockIdx.x;
+  const int t = wg % a.ntiles;
+  wg /= a.ntiles;
+  const int h = wg % a.H;
+  wg /= a.H;
+  const int b = wg % a.B;
+  const int f = wg / a.B;
+  const int64_t slot = a.slots[f];
+  const int tid = threadIdx.x;
+  const int tok0 = t * kTile;
+  constexpr int kRow = kTile + 16;
+  const uint8_t* kp = static_cast<const uint8_t*>(a.kpool) + slot * a.slot_stride +
+                      ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+  const uint8_t* vp = static_cast<const uint8_t*>(a.vpool) + slot * a.slot_stride +
+                      (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
+  uint8_t* ko = static_cast<uint8_t*>(a.kout) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+                (int64_t)f * a.T * a.o_st;
+  uint8_t* vo = static_cast<uint8_t*>(a.vout) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+                (int64_t)f * a.T * a.o_st;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = tid + 256 * r;
+    const int d = c >> 3, tc = (c & 7) * 8;
+    u32x2 v = *reinterpret_cast<const u32x2*>(vp + (int64_t)d * a.Tp + tc);
+    *reinterpret_cast<u32x2*>(vt + d * kRow + tc) = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = tid + 256 * r;
+    const int row = c >> 4, col = (c & 15) * 8;
+    if (tok0 + row < a.T) {
+      const int64_t oo = (int64_t)(tok0 + row) * a.o_st + col;
+      *reinterpret_cast<u32x2*>(ko + oo) = *reinterpret_cast<const u32x2*>(kp + row * kHeadDim + col);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t code = vt[(col + i) * kRow + row];
+        if (i < 4) lo |= code << (8 * i); else hi |= code << (8 * (i - 4));
+      }
+      *reinterpret_cast<u32x2*>(vo + oo) = u32x2{lo, hi};
+    }
+  }
+}
+
+}  // namespace skv
+
+using namespace skv;
+
+static bool aligned8(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)(8 * bytes)) == 0; }
+
+extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
+                          int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool,
+                          void* v_pool, float* k_scale, float* v_scale, int pool_dtype,
+                          int n_slots, const int32_t* dst_slots, int n_frames, int batch,
+                          int heads, int head_dim, int frame_tokens, skv_stream_t stream) {
+  clear_error();
+  if (!k_new || !v_new || !k_pool || !v_pool || !dst_slots) {
+    set_error("skv_append: null pointer argument");
+    return SKV_E_ARG;
+  }
+  if (head_dim != kHeadDim) {
+    set_error("skv_append: head_dim=%d unsupported (built for %d)", head_dim, kHeadDim);
+    return SKV_E_UNSUPPORTED;
+  }
+  if (n_frames < 0 || n_frames > SKV_MAX_APPEND_FRAMES || batch <= 0 || heads <= 0 ||
+      frame_tokens <= 0 || n_slots <= 0 || src_frame0 < 0) {
+    set_error("skv_append: bad sizes (n_frames=%d batch=%d heads=%d T=%d n_slots=%d frame0=%d)",
+              n_frames, batch, heads, frame_tokens, n_slots, src_frame0);
+    return SKV_E_ARG;
+  }
+  if (n_frames == 0) return SKV_OK;
+  const bool fp8 = pool_dtype == SKV_FP8_E4M3;
+  if (!(src_dtype == SKV_BF16 || src_dtype == SKV_F32) ||
+      !(pool_dtype == src_dtype || fp8)) {
+    set_error("skv_append: src_dtype=%d pool_dtype=%d unsupported (pool must equal src or be fp8)",
+              src_dtype, pool_dtype);
+    return SKV_E_UNSUPPORTED;
+  }
+  if (fp8 && (!k_scale || !v_scale)) {
+    set_error("skv_append: fp8 pool needs k_scale and v_scale");
+    return SKV_E_ARG;
+  }
+  const int esz = src_dtype == SKV_F32 ? 4 : 2;
+  if (src_sb % 8 || src_st % 8 || src_sh % 8 || !aligned8(k_new, esz) || !aligned8(v_new, esz)) {
+    set_error("skv_append: source strides/pointers must be multiples of 8 elements");
+    return SKV_E_ARG;
+  }
+  AppendArgs a;
+  a.ksrc = k_new;
+  a.vsrc = v_new;
+  a.s_sb = src_sb;
+  a.s_st = src_st;
+  a.s_sh = src_sh;
+  a.kpool = k_pool;
+  a.vpool = v_pool;
+  a.kscale = k_scale;
+  a.vscale = v_scale;
+  a.B = batch;
+  a.H = heads;
+  a.T = frame_tokens;
+  a.Tp = padded_tokens(frame_tokens);
+  a.n_frames = n_frames;
+  a.src_frame0 = src_frame0;
+  a.ntiles = a.Tp / kTile;
+  a.slot_stride = (int64_t)batch * heads * a.Tp * kHeadDim;
+  for (int f = 0; f < n_frames; ++f) {
+    if (dst_slots[f] < 0 || dst_slots[f] >= n_slots) {
+      set_error("skv_append: dst_slots[%d]=%d outside [0, %d)", f, dst_slots[f], n_slots);
+      return SKV_E_ARG;
+    }
+    a.slots[f] = dst_slots[f];
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fp8) {
+    dim3 grid(n_frames * batch * heads * 2);
+    if (src_dtype == SKV_BF16)
+      hipLaunchKernelGGL(append_fp8_kernel<bf16>, grid, dim3(1024), 0, s, a);
+    else
+      hipLaunchKernelGGL(append_fp8_kernel<float>, grid, dim3(1024), 0, s, a);
+  } else {
+    dim3 grid(n_frames * batch * heads * a.ntiles);
+    if (src_dtype == SKV_BF16)
+      hipLaunchKernelGGL(append_kernel<bf16>, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(append_kernel<float>, grid, dim3(256), 0, s, a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("skv_append: launch failed: %s", hipGetErrorString(e));
+    return SKV_E_LAUNCH;
+  }
+  return SKV_OK;
+}
+
+extern "C" int skv_gather(const void* k_pool, const void* v_pool, int pool_dtype, int n_slots,
+                          const int32_t* slots, int n_frames, int batch, int heads, int head_dim,
+                          int frame_tokens, void* k_out, void* v_out, int64_t out_sb,
+                          int64_t out_st, int64_t out_sh, skv_stream_t stream) {
+  clear_error();
+  if (!k_pool || !v_pool || !slots || !k_out || !v_out) {
+    set_error("skv_gather: null pointer argument");
+    return SKV_E_ARG;
+  }
+  if (head_dim != kHeadDim) {
+    set_error("skv_gather: head_dim=%d unsupported (built for %d)", head_dim, kHeadDim);
+    return SKV_E_UNSUPPORTED;
+  }
+  if (n_frames < 0 || n_frames > SKV_MAX_FRAMES || batch <= 0 || heads <= 0 ||
+      frame_tokens <= 0 || n_slots <= 0) {
+    set_error("skv_gather: bad sizes (n_frames=%d batch=%d heads=%d T=%d n_slots=%d)", n_frames,
+              batch, heads, frame_tokens, n_slots);
+    return SKV_E_ARG;
+  }
+  if (n_frames == 0) return SKV_OK;
+  if (!(pool_dtype == SKV_BF16 || pool_dtype == SKV_F32 || pool_dtype == SKV_FP8_E4M3)) {
+    set_error("skv_gather: pool_dtype=%d unsupported", pool_dtype);
+    return SKV_E_UNSUPPORTED;
+  }
+  const int esz = pool_dtype == SKV_F32 ? 4 : (pool_dtype == SKV_BF16 ? 2 : 1);
+  if (out_sb % 8 || out_st % 8 || out_sh % 8 || !aligned8(k_out, esz) || !aligned8(v_out, esz)) {
+    set_error("skv_gather: output strides/pointers must be multiples of 8 elements");
+    return SKV_E_ARG;
+  }
+  GatherArgs a;
+  a.kpool = k_pool;
+  a.vpool = v_pool;
+  a.kout = k_out;
+  a.vout = v_out;
+  a.o_sb = out_sb;
+  a.o_st = out_st;
+  a.o_sh = out_sh;
+  a.B = batch;
+  a.H = heads;
+  a.T = frame_tokens;
+  a.Tp = padded_tokens(frame_tokens);
+  a.n_frames = n_frames;
+  a.ntiles = a.Tp / kTile;
+  a.slot_stride = (int64_t)batch * heads * a.Tp * kHeadDim;
+  for (int f = 0; f < n_frames; ++f) {
+    if (slots[f] < 0 || slots[f] >= n_slots) {
+      set_error("skv_gather: slots[%d]=%d outside [0, %d)", f, slots[f], n_slots);
+      return SKV_E_ARG;
+    }
+    a.slots[f] = slots[f];
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid(n_frames * batch * heads * a.ntiles);
+  if (pool_dtype == SKV_BF16)
+    hipLaunchKernelGGL(gather_kernel<bf16>, grid, dim3(256), 0, s, a);
+  else if (pool_dtype == SKV_F32)
+    hipLaunchKernelGGL(gather_kernel<float>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(gather_u8_kernel, grid, dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("skv_gather: launch failed: %s", hipGetErrorString(e));
+    return SKV_E_LAUNCH;
+  }
+  return SKV_OK;
+}

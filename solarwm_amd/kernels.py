@@ -1,0 +1,297 @@
+"""Typed wrappers of the libsolarkv C ABI for torch tensors.
+
+The wrappers only check arguments and pass raw pointers, strides and the current HIP stream;
+all arithmetic happens in the HIP kernels.  Pool layouts (per layer):
+
+* K pool ``[n_slots, B, H, Tp, D]`` — keys of a frame, channel-contiguous rows;
+* V pool ``[n_slots, B, H, D, Tp]`` — values of a frame, stored transposed;
+* scales ``[n_slots, B, H]`` float32 (fp8 pools only), ``absmax / 448`` per (slot, b, h);
+
+with ``Tp = ceil(T / 64) * 64`` and zero padding rows.
+"""
+
+from __future__ import annotations
+
+import math
+from contextlib import contextmanager
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+TILE = 64
+
+_DTYPE_CODES = {
+    torch.float32: _lib.SKV_F32,
+    torch.bfloat16: _lib.SKV_BF16,
+    torch.float8_e4m3fn: _lib.SKV_FP8_E4M3,
+}
+
+
+class LaunchTimer:
+    """HIP events around each kernel launch, recorded on the launching stream.
+
+    ``records[kind]`` is a list of ``(start_event, end_event, work)`` where ``work`` is the
+    launch's algorithmic FLOPs (attention) or bytes moved (append / gather).
+    """
+
+    def __init__(self):
+        self.records: dict[str, list] = {"attention": [], "append": [], "gather": []}
+
+    def summary(self, kind: str) -> tuple[int, float, float]:
+        """(launches, total milliseconds, total work) of one kernel kind; synchronises."""
+        recs = self.records[kind]
+        if not recs:
+            return 0, 0.0, 0.0
+        recs[-1][1].synchronize()
+        ms = sum(a.elapsed_time(b) for a, b, _ in recs)
+        return len(recs), ms, float(sum(w for _, _, w in recs))
+
+
+_timer: LaunchTimer | None = None
+
+
+@contextmanager
+def timed_launches():
+    """Within the block, every append / gather / attention launch is bracketed by events."""
+    global _timer
+    prev, _timer = _timer, LaunchTimer()
+    try:
+        yield _timer
+    finally:
+        _timer = prev
+
+
+def _tic():
+    if _timer is None:
+        return None
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record()
+    return ev
+
+
+def _toc(kind: str, start, work: float) -> None:
+    if start is None or _timer is None:
+        return
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record()
+    _timer.records[kind].append((start, ev, work))
+
+
+def padded_tokens(frame_tokens: int) -> int:
+    return (frame_tokens + TILE - 1) // TILE * TILE
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float8_e4m3fn")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
+
+
+def _token_major(name: str, t: torch.Tensor) -> tuple[int, int, int]:
+    """Validate a [B, L, H, D] tensor with unit stride on D; return (sb, st, sh)."""
+    _require_cuda(name, t)
+    if t.dim() != 4 or t.shape[-1] != HEAD_DIM:
+        raise ValueError(f"{name} must be [B, L, H, {HEAD_DIM}], got {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} must be contiguous in its last dimension")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def check_pools(kpool: torch.Tensor, vpool: torch.Tensor, frame_tokens: int) -> tuple[int, int, int]:
+    """Validate a K/V pool pair; return (n_slots, B, H)."""
+    _require_cuda("k_pool", kpool)
+    _require_cuda("v_pool", vpool)
+    tp = padded_tokens(frame_tokens)
+    if kpool.dim() != 5 or vpool.dim() != 5:
+        raise ValueError("pools must be 5-D: K [S,B,H,Tp,D], V [S,B,H,D,Tp]")
+    s, b, h = kpool.shape[:3]
+    if tuple(kpool.shape) != (s, b, h, tp, HEAD_DIM) or tuple(vpool.shape) != (s, b, h, HEAD_DIM, tp):
+        raise ValueError(
+            f"pool shapes {tuple(kpool.shape)} / {tuple(vpool.shape)} do not match "
+            f"K [S,B,H,{tp},{HEAD_DIM}] / V [S,B,H,{HEAD_DIM},{tp}] for frame_tokens={frame_tokens}"
+        )
+    if not (kpool.is_contiguous() and vpool.is_contiguous()):
+        raise ValueError("pools must be contiguous")
+    if kpool.dtype != vpool.dtype or kpool.device != vpool.device:
+        raise ValueError("K and V pools must share dtype and device")
+    return s, b, h
+
+
+def _scales(kpool, kscale, vscale):
+    if kpool.dtype != torch.float8_e4m3fn:
+        return None, None
+    s, b, h = kpool.shape[:3]
+    for name, t in (("k_scale", kscale), ("v_scale", vscale)):
+        if t is None:
+            raise ValueError(f"fp8 pools need {name}")
+        _require_cuda(name, t)
+        if t.dtype != torch.float32 or tuple(t.shape) != (s, b, h) or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous float32 [{s},{b},{h}]")
+    return kscale.data_ptr(), vscale.data_ptr()
+
+
+def append_frames(
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    kpool: torch.Tensor,
+    vpool: torch.Tensor,
+    dst_slots: Sequence[int],
+    *,
+    frame_tokens: int,
+    src_frame0: int = 0,
+    kscale: torch.Tensor | None = None,
+    vscale: torch.Tensor | None = None,
+) -> None:
+    """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``."""
+    lib = _lib.load()
+    n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
+    sb, st, sh = _token_major("k_new", k_new)
+    if _token_major("v_new", v_new) != (sb, st, sh) or v_new.shape != k_new.shape:
+        raise ValueError("k_new and v_new must share shape and strides")
+    if k_new.dtype != v_new.dtype:
+        raise ValueError("k_new and v_new must share dtype")
+    if k_new.shape[0] != b or k_new.shape[2] != h:
+        raise ValueError(f"k_new batch/heads {tuple(k_new.shape)} do not match the pool ({b}, {h})")
+    n = len(dst_slots)
+    if (src_frame0 + n) * frame_tokens > k_new.shape[1]:
+        raise ValueError(
+            f"frames [{src_frame0}, {src_frame0 + n}) x {frame_tokens} tokens exceed k_new length {k_new.shape[1]}"
+        )
+    if k_new.device != kpool.device:
+        raise ValueError("k_new and pools must be on the same device")
+    ks, vs = _scales(kpool, kscale, vscale)
+    slots = _lib.int32_array(dst_slots)
+    t0 = _tic()
+    _lib.check(
+        "skv_append",
+        lib.skv_append(
+            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
+            kpool.data_ptr(), vpool.data_ptr(), ks, vs, dtype_code(kpool.dtype), n_slots, slots, n,
+            b, h, HEAD_DIM, frame_tokens, _stream(kpool.device),
+        ),
+    )
+    moved = 2 * n * frame_tokens * b * h * HEAD_DIM * (k_new.element_size() + kpool.element_size())
+    _toc("append", t0, moved)
+
+
+def gather_frames(
+    kpool: torch.Tensor,
+    vpool: torch.Tensor,
+    slots: Sequence[int],
+    *,
+    frame_tokens: int,
+    k_out: torch.Tensor | None = None,
+    v_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Materialise pool frames ``slots`` as token-major K, V ``[B, len(slots)*T, H, D]``."""
+    lib = _lib.load()
+    n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
+    n = len(slots)
+    shape = (b, n * frame_tokens, h, HEAD_DIM)
+    if k_out is None:
+        k_out = torch.empty(shape, dtype=kpool.dtype, device=kpool.device)
+    if v_out is None:
+        v_out = torch.empty(shape, dtype=kpool.dtype, device=kpool.device)
+    for name, t in (("k_out", k_out), ("v_out", v_out)):
+        if tuple(t.shape) != shape or t.dtype != kpool.dtype:
+            raise ValueError(f"{name} must be {shape} {kpool.dtype}")
+    sb, st, sh = _token_major("k_out", k_out)
+    if _token_major("v_out", v_out) != (sb, st, sh):
+        raise ValueError("k_out and v_out must share strides")
+    if n == 0:
+        return k_out, v_out
+    t0 = _tic()
+    _lib.check(
+        "skv_gather",
+        lib.skv_gather(
+            kpool.data_ptr(), vpool.data_ptr(), dtype_code(kpool.dtype), n_slots,
+            _lib.int32_array(slots), n, b, h, HEAD_DIM, frame_tokens, k_out.data_ptr(),
+            v_out.data_ptr(), sb, st, sh, _stream(kpool.device),
+        ),
+    )
+    _toc("gather", t0, 2 * 2 * n * frame_tokens * b * h * HEAD_DIM * kpool.element_size())
+    return k_out, v_out
+
+
+def attention_frames(
+    q: torch.Tensor,
+    kpool: torch.Tensor,
+    vpool: torch.Tensor,
+    frame_slots: Sequence[int],
+    *,
+    frame_tokens: int,
+    softmax_scale: float | None = None,
+    kscale: torch.Tensor | None = None,
+    vscale: torch.Tensor | None = None,
+    mask_mode: int = _lib.SKV_MASK_NONE,
+    q_pos0: int = 0,
+    chunk_tokens: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D]."""
+    lib = _lib.load()
+    n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
+    sb, st, sh = _token_major("q", q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"q dtype {q.dtype} unsupported (float32 or bfloat16)")
+    if q.shape[0] != b or q.shape[2] != h:
+        raise ValueError(f"q batch/heads {tuple(q.shape)} do not match the pool ({b}, {h})")
+    if q.device != kpool.device:
+        raise ValueError("q and pools must be on the same device")
+    if len(frame_slots) == 0:
+        raise RuntimeError("attention over an empty key window")
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    osb, ost, osh = _token_major("out", out)
+    scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
+    ks, vs = _scales(kpool, kscale, vscale)
+    t0 = _tic()
+    _lib.check(
+        "skv_attention",
+        lib.skv_attention(
+            q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(), ks,
+            vs, dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots), len(frame_slots),
+            b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode, q_pos0, chunk_tokens,
+            out.data_ptr(), osb, ost, osh, _stream(q.device),
+        ),
+    )
+    # algorithmic FLOPs: QKᵀ and PV over every key (masking is not discounted)
+    _toc("attention", t0, 4.0 * b * h * q.shape[1] * len(frame_slots) * frame_tokens * HEAD_DIM)
+    return out
+
+
+def new_pools(
+    n_slots: int,
+    batch: int,
+    heads: int,
+    frame_tokens: int,
+    dtype: torch.dtype,
+    device: torch.device | str,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor | None]:
+    """Allocate zeroed K/V pools (and fp8 scales) for ``n_slots`` frame slots."""
+    tp = padded_tokens(frame_tokens)
+    kpool = torch.zeros((n_slots, batch, heads, tp, HEAD_DIM), dtype=dtype, device=device)
+    vpool = torch.zeros((n_slots, batch, heads, HEAD_DIM, tp), dtype=dtype, device=device)
+    if dtype == torch.float8_e4m3fn:
+        kscale = torch.zeros((n_slots, batch, heads), dtype=torch.float32, device=device)
+        vscale = torch.zeros((n_slots, batch, heads), dtype=torch.float32, device=device)
+    else:
+        kscale = vscale = None
+    return kpool, vpool, kscale, vscale

@@ -1,0 +1,80 @@
+"""libsolarkv.so loads, exports every entry point include/solarkv.h declares, and rejects bad
+arguments with the documented status codes before touching a GPU."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from solarwm_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "solarkv.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(skv_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.skv_version() >= 100
+
+
+def test_constants_match_header():
+    text = HEADER.read_text()
+    for name in ("SKV_MAX_APPEND_FRAMES", "SKV_MAX_FRAMES"):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert int(m.group(1)) == getattr(_lib, name)
+    for name in ("SKV_F32", "SKV_BF16", "SKV_FP8_E4M3", "SKV_MASK_NONE", "SKV_MASK_CHUNK_CAUSAL",
+                 "SKV_OK", "SKV_E_ARG", "SKV_E_UNSUPPORTED", "SKV_E_LAUNCH"):
+        m = re.search(rf"\b{name} = (-?\d+)", text)
+        assert int(m.group(1)) == getattr(_lib, name), name
+
+
+def _slots(*v):
+    return _lib.int32_array(v)
+
+
+def test_argument_errors_do_not_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation
+    st = lib.skv_append(None, fake, _lib.SKV_BF16, 0, 0, 0, 0, fake, fake, None, None,
+                        _lib.SKV_BF16, 4, _slots(0), 1, 1, 1, 128, 64, None)
+    assert st == _lib.SKV_E_ARG and b"null" in lib.skv_last_error()
+    st = lib.skv_append(fake, fake, _lib.SKV_BF16, 0, 0, 0, 0, fake, fake, None, None,
+                        _lib.SKV_BF16, 4, _slots(0), 1, 1, 1, 64, 64, None)
+    assert st == _lib.SKV_E_UNSUPPORTED and b"head_dim" in lib.skv_last_error()
+    st = lib.skv_append(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, None, None,
+                        _lib.SKV_BF16, 4, _slots(7), 1, 1, 1, 128, 64, None)
+    assert st == _lib.SKV_E_ARG and b"dst_slots" in lib.skv_last_error()
+    st = lib.skv_append(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, None, None,
+                        _lib.SKV_FP8_E4M3, 4, _slots(0), 1, 1, 1, 128, 64, None)
+    assert st == _lib.SKV_E_ARG and b"scale" in lib.skv_last_error()
+    st = lib.skv_gather(fake, fake, _lib.SKV_BF16, 4, _slots(0), 1, 1, 1, 128, 64, fake, fake,
+                        3, 8, 8, None)
+    assert st == _lib.SKV_E_ARG and b"multiples of 8" in lib.skv_last_error()
+    st = lib.skv_attention(fake, _lib.SKV_BF16, 8, 8, 8, fake, fake, None, None, _lib.SKV_BF16,
+                           4, _slots(0), 0, 1, 1, 128, 16, 64, 0.1, 0, 0, 0, fake, 8, 8, 8, None)
+    assert st == _lib.SKV_E_ARG and b"empty key window" in lib.skv_last_error()
+    st = lib.skv_attention(fake, _lib.SKV_BF16, 8, 8, 8, fake, fake, None, None, _lib.SKV_BF16,
+                           4, _slots(0), 1, 1, 1, 128, 16, 64, 0.1, 5, 0, 0, fake, 8, 8, 8, None)
+    assert st == _lib.SKV_E_ARG and b"mask_mode" in lib.skv_last_error()
+    st = lib.skv_attention(fake, _lib.SKV_BF16, 8, 8, 8, fake, fake, None, None, _lib.SKV_BF16,
+                           4, _slots(9), 1, 1, 1, 128, 16, 64, 0.1, 0, 0, 0, fake, 8, 8, 8, None)
+    assert st == _lib.SKV_E_ARG and b"frame_slots" in lib.skv_last_error()
+
+
+def test_python_wrapper_raises_valueerror():
+    with pytest.raises(ValueError):
+        _lib.check("skv_append", _lib.SKV_E_ARG)
+    with pytest.raises(_lib.SolarKVError):
+        _lib.check("skv_append", _lib.SKV_E_LAUNCH)

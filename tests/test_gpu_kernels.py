@@ -1,0 +1,203 @@
+"""GPU parity of the append / gather / attention kernels against the CPU oracle.
+
+Bars: integer/byte movement bit-exact; attention within 2e-2 max-abs and 1e-3 mean-abs error
+(bf16 operands, fp32 accumulation) of the oracle's float64 SDPA on the same bf16-rounded inputs.
+"""
+
+import pytest
+import torch
+
+from oracle import wan_cache_ref as ref
+from solarwm_amd import _lib, kernels
+from solarwm_amd.attention import attention, chunk_causal_attention
+
+from .helpers import assert_attn_close
+
+pytestmark = pytest.mark.gpu
+
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _rand(shape, seed, dtype=torch.float32, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,H,T", [(1, 12, 390), (2, 3, 100), (1, 2, 64), (1, 1, 1560)])
+def test_append_gather_roundtrip_and_layout(gpu, dtype, B, H, T):
+    _say("append/gather", dtype, B, H, T)
+    n_slots, n_new = 7, 3
+    # strided source: K and V are views into one packed [B, L, 3, H, D] tensor
+    packed = _rand((B, n_new * T, 3, H, 128), seed=T + H, dtype=dtype).to(gpu)
+    k_src, v_src = packed[:, :, 1], packed[:, :, 2]
+    kpool, vpool, _, _ = kernels.new_pools(n_slots, B, H, T, dtype, gpu)
+    vpool.fill_(7)  # padding rows must come back as zeros after an append
+    slots = [5, 0, 3]
+    kernels.append_frames(k_src, v_src, kpool, vpool, slots, frame_tokens=T)
+    torch.cuda.synchronize()
+    Tp = kernels.padded_tokens(T)
+    for f, s in enumerate(slots):
+        want = k_src[:, f * T : (f + 1) * T].permute(0, 2, 1, 3)  # [B, H, T, D]
+        assert torch.equal(kpool[s, :, :, :T], want)
+        assert torch.equal(vpool[s, :, :, :, :T], want.transpose(-1, -2))
+        if Tp > T:
+            assert kpool[s, :, :, T:].abs().sum() == 0 and vpool[s, :, :, :, T:].abs().sum() == 0
+    order = [3, 5, 0, 5]
+    gk, gv = kernels.gather_frames(kpool, vpool, order, frame_tokens=T)
+    torch.cuda.synchronize()
+    for j, s in enumerate(order):
+        f = slots.index(s)
+        assert torch.equal(gk[:, j * T : (j + 1) * T], k_src[:, f * T : (f + 1) * T])
+        assert torch.equal(gv[:, j * T : (j + 1) * T], v_src[:, f * T : (f + 1) * T])
+
+
+@pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,H,T", [(1, 12, 1560), (4, 2, 390), (1, 3, 100)])
+def test_fp8_append_matches_oracle(gpu, src_dtype, B, H, T):
+    _say("fp8 append", src_dtype, B, H, T)
+    x = _rand((B, 2 * T, H, 128), seed=11, dtype=torch.float32)
+    g = torch.Generator().manual_seed(12)
+    outlier = torch.randperm(128, generator=g)[:2]
+    x[..., outlier] *= 20.0
+    x[0, :T, 0] = 0.0  # an all-zero (frame, head): scale 0, codes 0
+    x = x.to(src_dtype)
+    v = (x * -0.5).to(src_dtype)
+    kpool, vpool, ks, vs = kernels.new_pools(4, B, H, T, torch.float8_e4m3fn, gpu)
+    kernels.append_frames(x.to(gpu), v.to(gpu), kpool, vpool, [2, 1], frame_tokens=T,
+                          kscale=ks, vscale=vs)
+    torch.cuda.synchronize()
+    for f, s in enumerate([2, 1]):
+        for src, pool, sc, vt in ((x, kpool, ks, False), (v, vpool, vs, True)):
+            frame = src[:, f * T : (f + 1) * T].permute(0, 2, 1, 3)  # [B, H, T, D]
+            codes, scale = ref.fp8_quantize(frame)
+            got = pool[s].cpu()
+            got = got[..., :T].transpose(-1, -2) if vt else got[:, :, :T]
+            assert torch.equal(got.view(torch.uint8), codes.view(torch.uint8)), (f, vt)
+            assert torch.equal(sc[s].cpu(), scale), (f, vt)
+
+
+def _pool_from(k, v, T, dtype, device, perm_seed=0):
+    """Store dense K/V [B, n*T, H, D] frame by frame in shuffled slots; return pools + order."""
+    B, L, H, _ = k.shape
+    n = L // T
+    g = torch.Generator().manual_seed(perm_seed)
+    n_slots = n + 2
+    slots = torch.randperm(n_slots, generator=g)[:n].tolist()
+    kpool, vpool, _, _ = kernels.new_pools(n_slots, B, H, T, dtype, device)
+    kd, vd = k.to(device), v.to(device)
+    for f in range(n):
+        kernels.append_frames(kd, vd, kpool, vpool, [slots[f]], frame_tokens=T, src_frame0=f)
+    return kpool, vpool, slots
+
+
+@pytest.mark.parametrize(
+    "B,H,Lq,T,n,dtype",
+    [(1, 2, 128, 64, 2, torch.bfloat16), (1, 3, 200, 100, 5, torch.bfloat16),
+     (2, 2, 390, 390, 4, torch.float32), (1, 12, 1170, 390, 6, torch.bfloat16),
+     (1, 1, 37, 1560, 3, torch.bfloat16), (1, 4, 1, 70, 2, torch.bfloat16)],
+)
+def test_attention_frames_vs_oracle(gpu, B, H, Lq, T, n, dtype):
+    _say("attention", B, H, Lq, T, n, dtype)
+    q = _rand((B, Lq, H, 128), 1, dtype)
+    k = _rand((B, n * T, H, 128), 2, dtype)
+    v = _rand((B, n * T, H, 128), 3, dtype)
+    kpool, vpool, slots = _pool_from(k, v, T, dtype, gpu)
+    out = kernels.attention_frames(q.to(gpu), kpool, vpool, slots, frame_tokens=T)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == q.shape
+    assert_attn_close(out, ref.attention(q, k, v))
+
+
+def test_attention_sharp_and_scaled_logits(gpu):
+    """Large logits (peaked softmax) and a non-default softmax_scale."""
+    q = _rand((1, 256, 2, 128), 4, torch.bfloat16, scale=3.0)
+    k = _rand((1, 640, 2, 128), 5, torch.bfloat16, scale=3.0)
+    v = _rand((1, 640, 2, 128), 6, torch.bfloat16)
+    kpool, vpool, slots = _pool_from(k, v, 160, torch.bfloat16, gpu)
+    for scale in (None, 0.02):
+        out = kernels.attention_frames(q.to(gpu), kpool, vpool, slots, frame_tokens=160,
+                                       softmax_scale=scale)
+        torch.cuda.synchronize()
+        assert_attn_close(out, ref.attention(q, k, v, softmax_scale=scale))
+
+
+@pytest.mark.parametrize("clean,noisy,T,per_block", [(2, 1, 100, 1), (3, 3, 64, 3), (0, 3, 50, 3),
+                                                      (6, 3, 130, 3)])
+def test_chunk_causal_vs_oracle_mask(gpu, clean, noisy, T, per_block):
+    _say("chunk-causal", clean, noisy, T, per_block)
+    L = (clean + noisy) * T
+    q = _rand((1, L, 2, 128), 7, torch.bfloat16)
+    k = _rand((1, L, 2, 128), 8, torch.bfloat16)
+    v = _rand((1, L, 2, 128), 9, torch.bfloat16)
+    dense, _ = ref.inference_window_mask(clean, noisy, T, per_block)
+    want = ref.attention(q, k, v, mask=dense[:L, :L])
+    got = chunk_causal_attention(q.to(gpu), k.to(gpu), v.to(gpu), chunk_tokens=T * per_block)
+    torch.cuda.synchronize()
+    assert_attn_close(got, want)
+    # the same mask through the frame table, queries = the last chunk only (q_pos0 offset)
+    Lq = T * per_block
+    kpool, vpool, slots = _pool_from(k, v, T, torch.bfloat16, gpu)
+    got2 = kernels.attention_frames(
+        q[:, L - Lq :].to(gpu), kpool, vpool, slots, frame_tokens=T,
+        mask_mode=_lib.SKV_MASK_CHUNK_CAUSAL, q_pos0=L - Lq, chunk_tokens=Lq,
+    )
+    torch.cuda.synchronize()
+    assert_attn_close(got2, want[:, L - Lq :])
+
+
+def test_dropin_attention_signature(gpu):
+    q = _rand((2, 300, 3, 128), 10, torch.float32)
+    k = _rand((2, 500, 3, 128), 11, torch.float32)
+    v = _rand((2, 500, 3, 128), 12, torch.float32)
+    out = attention(q.to(gpu), k.to(gpu), v.to(gpu))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32  # flash path keeps q's dtype (attention.py:138)
+    assert_attn_close(out, ref.attention(q, k, v))
+    ql = torch.tensor([300, 120])
+    kl = torch.tensor([77, 500])
+    out = attention(q.to(gpu), k.to(gpu), v.to(gpu), q_lens=ql, k_lens=kl)
+    torch.cuda.synchronize()
+    assert_attn_close(out[0], ref.attention(q[:1], k[:1, :77], v[:1, :77])[0])
+    assert_attn_close(out[1, :120], ref.attention(q[1:, :120], k[1:], v[1:])[0])
+    assert out[1, 120:].abs().sum() == 0
+
+
+def test_full_size_closed_form_identical_keys(gpu):
+    """C2 shape (Lq 4680, 21 frames x 1560 keys, 12 heads): with every key equal, softmax is
+    uniform and the output is the mean of V over all 32760 keys."""
+    T, n, H = 1560, 21, 12
+    q = torch.randn(1, 4680, H, 128, device=gpu, dtype=torch.bfloat16)
+    k = torch.randn(1, 1, H, 128, device=gpu, dtype=torch.bfloat16).expand(1, n * T, H, 128).contiguous()
+    v = torch.randn(1, n * T, H, 128, device=gpu, dtype=torch.bfloat16)
+    kpool, vpool, _, _ = kernels.new_pools(n + 3, 1, H, T, torch.bfloat16, gpu)
+    slots = list(range(n + 3))[3:][::-1]
+    for f in range(n):
+        kernels.append_frames(k, v, kpool, vpool, [slots[f]], frame_tokens=T, src_frame0=f)
+    out = kernels.attention_frames(q, kpool, vpool, slots, frame_tokens=T)
+    want = v.double().mean(dim=1, keepdim=True)
+    torch.cuda.synchronize()
+    err = (out.double() - want).abs()
+    assert float(err.max()) < 2e-4, float(err.max())
+
+
+def test_attention_is_deterministic(gpu):
+    q = _rand((1, 700, 4, 128), 20, torch.bfloat16).to(gpu)
+    k = _rand((1, 1560, 4, 128), 21, torch.bfloat16)
+    kpool, vpool, slots = _pool_from(k, k * 0.5, 390, torch.bfloat16, gpu)
+    a = kernels.attention_frames(q, kpool, vpool, slots, frame_tokens=390)
+    b = kernels.attention_frames(q, kpool, vpool, slots, frame_tokens=390)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_empty_window_raises(gpu):
+    kpool, vpool, _, _ = kernels.new_pools(2, 1, 1, 64, torch.bfloat16, gpu)
+    q = torch.zeros(1, 4, 1, 128, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="empty key window"):
+        kernels.attention_frames(q, kpool, vpool, [], frame_tokens=64)
+    with pytest.raises(ValueError, match="outside"):
+        kernels.attention_frames(q, kpool, vpool, [5], frame_tokens=64)

@@ -1,0 +1,303 @@
+"""Pins the CPU oracle (oracle/wan_cache_ref.py) with checks that do not restate its formulas:
+published known answers, brute-force list models, explicit float64 loops, closed forms and an
+exhaustive fp8 code search."""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import wan_cache_ref as ref
+
+
+# ---------------------------------------------------------------------------------------------
+# token-labelled cache runs
+# ---------------------------------------------------------------------------------------------
+def _labelled(tokens_start, n, heads=1, dim=1, batch=1):
+    """K/V whose value at token t is the global token id t (same in every head/channel)."""
+    ids = torch.arange(tokens_start, tokens_start + n, dtype=torch.float64)
+    return ids.view(1, n, 1, 1).expand(batch, n, heads, dim).clone()
+
+
+class _Recorder:
+    def __init__(self):
+        self.k = None
+
+    def __call__(self, q, k, v):
+        self.k = k.clone()
+        return torch.zeros_like(q)
+
+
+def _frame_ids(k_labels, frame_tokens):
+    row = k_labels[0, :, 0, 0]
+    n = row.shape[0] // frame_tokens
+    out = []
+    for f in range(n):
+        seg = row[f * frame_tokens : (f + 1) * frame_tokens]
+        first = int(seg[0])
+        assert first % frame_tokens == 0 and torch.equal(
+            seg, torch.arange(first, first + frame_tokens, dtype=seg.dtype)
+        ), "a cached frame is not a contiguous run of one frame's token ids"
+        out.append(first // frame_tokens)
+    return out
+
+
+def _model_window(all_frames, sink_f, cap_f):
+    """Brute-force CausVid window: the first sink frames ever written, then the most recent
+    cap - sink frames."""
+    sink = all_frames[:sink_f]
+    rest = all_frames[sink_f:]
+    keep = cap_f - sink_f
+    return sink + (rest[-keep:] if keep > 0 else [])
+
+
+def _run(T, chunk_f, cap_f, sink_f, n_chunks, passes=("none", "commit")):
+    cache = ref.allocate_kv_cache(1, 1, cap_f * T, 1, 1, torch.float64)
+    rec = _Recorder()
+    visible = []
+    committed_frames = []
+    for c in range(n_chunks):
+        Lq = chunk_f * T
+        start = c * Lq
+        for policy in passes:
+            k = _labelled(start, Lq)
+            before = {key: val.clone() for key, val in cache[0].items()}
+            _, upd = ref.cached_self_attention(
+                k, k, k, cache[0], current_start=start, frame_seqlen=T, sink_size=sink_f,
+                local_attn_size=cap_f, attn_fn=rec,
+            )
+            visible.append(_frame_ids(rec.k, T))
+            if policy == "none":
+                for key in before:
+                    assert torch.equal(before[key], cache[0][key]), "a none pass changed the cache"
+            else:
+                ref.apply_cache_updates(cache, [(0, upd)])
+        committed_frames.extend(range(c * chunk_f, (c + 1) * chunk_f))
+        live = int(cache[0]["local_end_index"].item())
+        assert live % T == 0
+        got = _frame_ids(cache[0]["k"][:, :live], T)
+        assert got == _model_window(committed_frames, sink_f, cap_f), (c, got)
+        assert int(cache[0]["global_end_index"].item()) == (c + 1) * Lq
+    return visible, cache
+
+
+def test_c1_known_answer():
+    """BASELINE config 1 geometry (390 tokens/frame, chunk 3 frames, 21-frame cache, 1 sink
+    frame, 10 chunks x 2 passes): the published visible-key counts, eviction order and final
+    frame order."""
+    T = 390
+    visible, cache = _run(T, 3, 21, 1, 10)
+    lk = [len(v) * T for v in visible[1::2]]
+    assert lk == [1170, 2340, 3510, 4680, 5850, 7020, 8190, 8190, 8190, 8190]
+    commits = visible[1::2]
+    assert set(commits[6]) - set(commits[7]) == {1, 2, 3}
+    assert set(commits[7]) - set(commits[8]) == {4, 5, 6}
+    assert set(commits[8]) - set(commits[9]) == {7, 8, 9}
+    final = _frame_ids(cache[0]["k"], T)
+    assert final == [0] + list(range(10, 30))
+
+
+@pytest.mark.parametrize(
+    "T,chunk_f,cap_f,sink_f",
+    [(4, 3, 21, 1), (4, 3, 6, 0), (2, 1, 5, 2), (3, 2, 7, 1), (5, 4, 9, 3), (2, 3, 3, 0),
+     (2, 1, 1, 0), (3, 2, 8, 0)],
+)
+def test_window_matches_brute_force(T, chunk_f, cap_f, sink_f):
+    visible, _ = _run(T, chunk_f, cap_f, sink_f, n_chunks=9, passes=("none", "none", "commit"))
+    frames = []
+    for c in range(9):
+        cur = list(range(c * chunk_f, (c + 1) * chunk_f))
+        expect = _model_window(frames + cur, sink_f, cap_f)
+        for p in range(3):
+            assert visible[3 * c + p] == expect, (c, p)
+        frames += cur
+
+
+def test_recompute_rewrites_last_chunk_except_sink():
+    T, chunk_f, cap_f, sink_f = 2, 2, 7, 1
+    _, cache = _run(T, chunk_f, cap_f, sink_f, n_chunks=5)
+    ge = int(cache[0]["global_end_index"].item())
+    le = int(cache[0]["local_end_index"].item())
+    before = cache[0]["k"].clone()
+    Lq = chunk_f * T
+    start = ge - Lq
+    newk = _labelled(10_000, Lq)
+    _, upd = ref.cached_self_attention(
+        newk, newk, newk, cache[0], current_start=start, frame_seqlen=T, sink_size=sink_f,
+        local_attn_size=cap_f, attn_fn=_Recorder(),
+    )
+    assert upd[2]["is_recompute"] and upd[2]["action"] == "direct_insert"
+    ref.apply_cache_updates(cache, [(0, upd)])
+    assert int(cache[0]["global_end_index"].item()) == ge
+    assert int(cache[0]["local_end_index"].item()) == le
+    after = cache[0]["k"]
+    assert torch.equal(after[:, : le - Lq], before[:, : le - Lq])
+    assert torch.equal(after[:, le - Lq : le], newk)
+
+
+def test_first_chunk_recompute_keeps_sink_when_not_first():
+    """current_start == 0 is never a recompute (causal_model.py:1034)."""
+    T = 2
+    cache = ref.allocate_kv_cache(1, 1, 6 * T, 1, 1, torch.float64)
+    k = _labelled(0, 2 * T)
+    _, upd = ref.cached_self_attention(
+        k, k, k, cache[0], current_start=0, frame_seqlen=T, sink_size=1, local_attn_size=6,
+        attn_fn=_Recorder(),
+    )
+    ref.apply_cache_updates(cache, [(0, upd)])
+    _, upd = ref.cached_self_attention(
+        k, k, k, cache[0], current_start=0, frame_seqlen=T, sink_size=1, local_attn_size=6,
+        attn_fn=_Recorder(),
+    )
+    assert not upd[2]["is_recompute"]
+
+
+# ---------------------------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------------------------
+def _loops_attention(q, k, v, scale, mask=None):
+    q, k, v = (np.asarray(x.to(torch.bfloat16).double()) for x in (q, k, v))
+    B, Lq, H, D = q.shape
+    Lk = k.shape[1]
+    out = np.zeros((B, Lq, H, D))
+    for b in range(B):
+        for h in range(H):
+            for i in range(Lq):
+                logits = [
+                    sum(q[b, i, h, d] * k[b, j, h, d] for d in range(D)) * scale
+                    if (mask is None or mask[i, j]) else -math.inf
+                    for j in range(Lk)
+                ]
+                m = max(logits)
+                w = [math.exp(x - m) for x in logits]
+                s = sum(w)
+                for d in range(D):
+                    out[b, i, h, d] = sum(w[j] * v[b, j, h, d] for j in range(Lk)) / s
+    return out
+
+
+def test_attention_matches_explicit_loops():
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 3, 2, 4, generator=g)
+    k = torch.randn(1, 5, 2, 4, generator=g)
+    v = torch.randn(1, 5, 2, 4, generator=g)
+    got = ref.attention(q, k, v, softmax_scale=0.7).double().numpy()
+    assert np.allclose(got, _loops_attention(q, k, v, 0.7), atol=1e-12)
+    mask = torch.tensor([[1, 1, 0, 0, 0], [1, 1, 1, 1, 0], [1, 1, 1, 1, 1]], dtype=torch.bool)
+    got = ref.attention(q, k, v, softmax_scale=0.7, mask=mask).double().numpy()
+    assert np.allclose(got, _loops_attention(q, k, v, 0.7, mask), atol=1e-12)
+
+
+def test_attention_closed_forms():
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(2, 7, 3, 16, generator=g)
+    v = torch.randn(2, 11, 3, 16, generator=g)
+    same_k = torch.randn(2, 1, 3, 16, generator=g).expand(2, 11, 3, 16)
+    out = ref.attention(q, same_k, v)
+    mean_v = v.to(torch.bfloat16).double().mean(dim=1, keepdim=True)
+    assert torch.allclose(out.double(), mean_v.expand_as(out), atol=1e-6)
+    one = ref.attention(q, v[:, :1], v[:, :1])
+    assert torch.allclose(one.double(), v[:, :1].to(torch.bfloat16).double().expand_as(one), atol=1e-6)
+    perm = torch.randperm(11, generator=g)
+    k = torch.randn(2, 11, 3, 16, generator=g)
+    a = ref.attention(q, k, v)
+    b = ref.attention(q, k[:, perm], v[:, perm])
+    assert torch.allclose(a.double(), b.double(), atol=1e-6)
+    # the output keeps q's dtype (attention.py:138)
+    assert ref.attention(q.bfloat16(), k.bfloat16(), v.bfloat16()).dtype == torch.bfloat16
+
+
+# ---------------------------------------------------------------------------------------------
+# masks
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("clean,noisy,T,per_block", [(2, 1, 50, 1), (3, 3, 40, 3), (0, 3, 30, 3),
+                                                      (4, 2, 64, 2)])
+def test_inference_window_mask_brute_force(clean, noisy, T, per_block):
+    dense, pad = ref.inference_window_mask(clean, noisy, T, per_block)
+    total = (clean + noisy) * T
+    block = T * per_block
+    P = dense.shape[0]
+    assert P % 128 == 0 and P - total == pad and 0 <= pad < 128
+    chunk_of = lambda t: t // block  # noqa: E731
+    for qi in range(P):
+        for ki in range(0, P, 7):
+            if qi >= total:
+                want = qi == ki
+            else:
+                want = ki < total and chunk_of(ki) <= chunk_of(qi)
+                want = want or qi == ki
+            assert bool(dense[qi, ki]) == want, (qi, ki)
+
+
+def test_block_classes_small():
+    dense = torch.zeros(256, 256, dtype=torch.bool)
+    dense[:128, :100] = True
+    dense[128:, :] = True
+    full, partial = ref.block_classes(dense)
+    assert full.tolist() == [[False, False], [True, True]]
+    assert partial.tolist() == [[True, False], [False, False]]
+
+
+# ---------------------------------------------------------------------------------------------
+# memory gather
+# ---------------------------------------------------------------------------------------------
+def test_memory_gather_index_semantics():
+    T = 3
+    bank = torch.arange(2 * 10 * T * 2 * 4, dtype=torch.float32).view(2, 10 * T, 2, 4)
+    idx = [7, 2, 9, 2]
+    out = ref.memory_gather(bank, idx, T)
+    assert out.shape == (2, 4 * T, 2, 4)
+    for j, i in enumerate(idx):
+        assert torch.equal(out[:, j * T : (j + 1) * T], bank[:, i * T : (i + 1) * T])
+    assert ref.memory_gather(bank, [], T).shape[1] == 0
+
+
+# ---------------------------------------------------------------------------------------------
+# fp8 e4m3fn
+# ---------------------------------------------------------------------------------------------
+def test_e4m3_code_table():
+    codes = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    for c in range(256):
+        want = ref.e4m3_decode(c)
+        got = float(codes[c])
+        if math.isnan(want):
+            assert math.isnan(got)
+        else:
+            assert got == want, (c, got, want)
+    assert ref.e4m3_decode(0x7E) == 448.0 and ref.e4m3_decode(0x08) == 2.0**-6
+    assert ref.e4m3_decode(0x01) == 2.0**-9
+
+
+def _nearest_code(y, table):
+    best = None
+    for c, val in table:
+        d = abs(val - y)
+        if best is None or d < best[0] or (d == best[0] and (c & 1) == 0 and (best[1] & 1) == 1):
+            best = (d, c)
+    return best[1]
+
+
+def test_fp8_quantize_nearest_and_scale():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 3, 40, 8, generator=g)
+    x[0, 1, 5, 2] = 37.0  # outlier sets the absmax of that (b, h)
+    x[1, 2] = 0.0  # all-zero frame
+    codes, scale = ref.fp8_quantize(x)
+    assert codes.dtype == torch.float8_e4m3fn and scale.shape == (2, 3)
+    assert scale[1, 2] == 0 and codes[1, 2].float().abs().sum() == 0
+    assert float(scale[0, 1]) == pytest.approx(37.0 / 448.0, rel=1e-7)
+    table = [(c, ref.e4m3_decode(c)) for c in range(256) if not math.isnan(ref.e4m3_decode(c))]
+    raw = codes.view(torch.uint8)
+    for b, h in itertools.product(range(2), range(3)):
+        amax = float(x[b, h].abs().max())
+        if amax == 0:
+            continue
+        inv = np.float32(448.0) / np.float32(amax)
+        for t in range(0, 40, 3):
+            for d in range(8):
+                y = float(np.clip(np.float32(x[b, h, t, d]) * inv, -448, 448))
+                assert int(raw[b, h, t, d]) == _nearest_code(y, table), (b, h, t, d, y)
+    # the absmax element lands exactly on +-448
+    assert float(codes[0, 1, 5, 2].float()) == 448.0
