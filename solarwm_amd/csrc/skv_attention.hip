@@ -43,13 +43,22 @@ struct AttnArgs {
   int32_t slots[SKV_MAX_FRAMES];
 };
 
-constexpr int kBQ = 128;            // queries per workgroup
-constexpr int kKs = kHeadDim + 8;   // LDS row stride of the K tile (bf16 elements)
-constexpr int kVs = kTile + 8;      // LDS row stride of the V^T tile (bf16 elements)
+constexpr int kBQ = 128;  // queries per workgroup (4 waves x 32)
+
+// LDS holds each tile in MFMA operand order: one 1 KB block per A operand (64 lanes x 16 B),
+// lane L of the block at byte L*16.  K tile: 16 blocks (kb, s) = 32-key block x 16-channel
+// step; V^T tile: 16 blocks (db, kb, s2) = 32-channel block x 32-key block x 16-key step.
+// A direct global->LDS load (global_load_lds_dwordx4) writes exactly one block, so staging
+// needs no registers and every operand read is a linear, bank-conflict-free ds_read_b128.
+constexpr int kBlockBytes = 1024;
+constexpr int kTileBytes = 32 * kBlockBytes;  // K (16 KB) + V^T (16 KB)
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
 // Row m of a 32-row MFMA block reads key key_perm(m) of the block.  With the 32x32 C layout
 // (lane l, register i -> row (i/4)*8 + (l/32)*4 + i%4) this puts key (i/8)*16 + (l/32)*8 + i%8
-// in register i of lane l.
+// in register i of lane l: each 8 registers are 8 consecutive keys, the B operand of PV.
 __device__ inline int key_perm(int m) {
   const int a = m >> 3, h = (m >> 2) & 1, c = m & 3;
   return (a >> 1) * 16 + h * 8 + (a & 1) * 4 + c;
@@ -75,10 +84,60 @@ __device__ inline void store4<float>(float* p, float x0, float x1, float x2, flo
   *reinterpret_cast<f32x4*>(p) = f32x4{x0, x1, x2, x3};
 }
 
+// Stage tile `tau` into LDS buffer `buf`.  bf16 pools: 8 direct 16 B global->LDS loads per
+// lane (4 K blocks + 4 V^T blocks per wave).  fp32 pools: loaded through registers and
+// rounded to bf16 (the C1 fp32 path; not performance critical).
+template <typename KT>
+struct TileLoader;
+
+template <>
+struct TileLoader<bf16> {
+  int64_t koff, voff;
+  __device__ void init(int w, int lane, int Tp) {
+    const int n = lane & 31, hh = lane >> 5;
+    // wave w stages K blocks (kb = w>>1, s = (w&1)*4 + j) and V^T blocks (db = w, j = kb*2+s2)
+    koff = (int64_t)((w >> 1) * 32 + key_perm(n)) * kHeadDim + (w & 1) * 64 + hh * 8;
+    voff = (int64_t)(w * 32 + n) * Tp + hh * 8;
+  }
+  __device__ void issue(const bf16* kt, const bf16* vt, char* lds, int w) const {
+    char* kdst = lds + (w * 4) * kBlockBytes;
+    char* vdst = lds + 16 * kBlockBytes + (w * 4) * kBlockBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(kt + koff + j * 16),
+                                       (lds_void_t*)(kdst + j * kBlockBytes), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(vt + voff + j * 16),
+                                       (lds_void_t*)(vdst + j * kBlockBytes), 16, 0, 0);
+  }
+};
+
+template <>
+struct TileLoader<float> {
+  int64_t koff, voff;
+  int lane;
+  __device__ void init(int w, int lane_, int Tp) {
+    lane = lane_;
+    const int n = lane & 31, hh = lane >> 5;
+    koff = (int64_t)((w >> 1) * 32 + key_perm(n)) * kHeadDim + (w & 1) * 64 + hh * 8;
+    voff = (int64_t)(w * 32 + n) * Tp + hh * 8;
+  }
+  __device__ void issue(const float* kt, const float* vt, char* lds, int w) const {
+    char* kdst = lds + (w * 4) * kBlockBytes + lane * 16;
+    char* vdst = lds + 16 * kBlockBytes + (w * 4) * kBlockBytes + lane * 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<bf16x8*>(kdst + j * kBlockBytes) = Vec8<float>::load(kt + koff + j * 16).to_bf16();
+      *reinterpret_cast<bf16x8*>(vdst + j * kBlockBytes) = Vec8<float>::load(vt + voff + j * 16).to_bf16();
+    }
+  }
+};
+
 template <typename QT, typename KT>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16 lk[kTile * kKs];
-  __shared__ __attribute__((aligned(16))) bf16 lv[kHeadDim * kVs];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];  // 2 x kTileBytes
 
   // XCD-aware order: workgroup ids are dealt round-robin over the 8 XCDs; XCD x gets the
   // contiguous logical range starting at x*per + min(x, rem), so q-tiles of one head run on
@@ -131,19 +190,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const KT* kpool = static_cast<const KT*>(a.kpool);
   const KT* vpool = static_cast<const KT*>(a.vpool);
   const int64_t kbh = (int64_t)(b * a.H + h) * a.Tp * kHeadDim;  // (b,h) offset inside a slot
-
-  Vec8<KT> kr[4], vr[4];
-  auto load_tile = [&](int tau) {
+  TileLoader<KT> loader;
+  loader.init(w, lane, a.Tp);
+  auto stage = [&](int tau, int buf) {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
     const int64_t base = (int64_t)a.slots[j] * a.slot_stride + kbh;
-    const KT* kp = kpool + base + (int64_t)t * kTile * kHeadDim;
-    const KT* vp = vpool + base + t * kTile;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + 256 * r;
-      kr[r] = Vec8<KT>::load(kp + (c >> 4) * kHeadDim + (c & 15) * 8);
-      vr[r] = Vec8<KT>::load(vp + (int64_t)(c >> 3) * a.Tp + (c & 7) * 8);
-    }
+    loader.issue(kpool + base + (int64_t)t * kTile * kHeadDim, vpool + base + t * kTile,
+                 lds + buf * kTileBytes, w);
   };
 
   f32x16 oacc[4];
@@ -151,24 +204,27 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
+  // Running max in the log2 domain.  It is raised only when a tile's max exceeds it by more
+  // than kStale, so most tiles skip the O rescale; probabilities then stay <= 2^kStale, which
+  // bf16 and the fp32 sums represent exactly as well as values <= 1.
+  constexpr float kStale = 8.0f;
   float m_run = -INFINITY, l_run = 0.f;
-  const int krow = key_perm(n);
   const float c2 = a.scale_log2;
+  const int lane16 = lane * 16;
 
-  if (ntau > 0) load_tile(0);
+  if (ntau > 0) {
+    stage(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
   for (int tau = 0; tau < ntau; ++tau) {
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + 256 * r;
-      *reinterpret_cast<bf16x8*>(&lk[(c >> 4) * kKs + (c & 15) * 8]) = kr[r].to_bf16();
-      *reinterpret_cast<bf16x8*>(&lv[(c >> 3) * kVs + (c & 7) * 8]) = vr[r].to_bf16();
-    }
-    __syncthreads();
+    const int buf = tau & 1;
+    if (tau + 1 < ntau) stage(tau + 1, buf ^ 1);
+    const char* kl = lds + buf * kTileBytes + lane16;
+    const char* vl = kl + 16 * kBlockBytes;
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
     const int64_t key0 = (int64_t)j * a.T + t * kTile;
     const int tok0 = t * kTile;
-    if (tau + 1 < ntau) load_tile(tau + 1);
 
     // S^T (64 keys x 32 queries per wave) = K Q^T
     f32x16 sacc[2];
@@ -176,10 +232,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) sacc[kb][i] = 0.f;
-      const bf16* kp = &lk[(kb * 32 + krow) * kKs + hh * 8];
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const bf16x8 ak = *reinterpret_cast<const bf16x8*>(kp + s * 16);
+        const bf16x8 ak = *reinterpret_cast<const bf16x8*>(kl + (kb * 8 + s) * kBlockBytes);
         sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[s], sacc[kb], 0, 0, 0);
       }
     }
@@ -201,16 +256,18 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx * c2);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
-    l_run *= alpha;
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * c2;
+    if (mx > m_run + kStale) {
+      // per lane: raise the reference point; the wave rescales only if some lane did
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when m_run == -inf
+      m_run = mx;
+      l_run *= alpha;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
 
     bf16x8 pb[2][2];
 #pragma unroll
@@ -224,16 +281,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
     // O^T (128 x 32 per wave) += V^T P^T
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const bf16* vp = &lv[(db * 32 + n) * kVs + hh * 8];
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 av = *reinterpret_cast<const bf16x8*>(vp + kb * 32 + s2 * 16);
+          const bf16x8 av =
+              *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kb * 2 + s2) * kBlockBytes);
           oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[kb][s2], oacc[db], 0, 0, 0);
         }
-    }
+
+    // the next tile has landed in the other buffer; every wave is done with this one
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -345,14 +405,15 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(a.n_wg), block(256);
+  const size_t lds_bytes = 2 * kTileBytes;
   if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<bf16, bf16>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((attn_kernel<bf16, bf16>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
-    hipLaunchKernelGGL((attn_kernel<bf16, float>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((attn_kernel<bf16, float>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_F32 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<float, bf16>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((attn_kernel<float, bf16>), grid, block, lds_bytes, s, a);
   else
-    hipLaunchKernelGGL((attn_kernel<float, float>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((attn_kernel<float, float>), grid, block, lds_bytes, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("skv_attention: launch failed: %s", hipGetErrorString(e));

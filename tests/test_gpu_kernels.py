@@ -41,9 +41,10 @@ def test_append_gather_roundtrip_and_layout(gpu, dtype, B, H, T):
     torch.cuda.synchronize()
     Tp = kernels.padded_tokens(T)
     for f, s in enumerate(slots):
-        want = k_src[:, f * T : (f + 1) * T].permute(0, 2, 1, 3)  # [B, H, T, D]
-        assert torch.equal(kpool[s, :, :, :T], want)
-        assert torch.equal(vpool[s, :, :, :, :T], want.transpose(-1, -2))
+        want_k = k_src[:, f * T : (f + 1) * T].permute(0, 2, 1, 3)  # [B, H, T, D]
+        want_v = v_src[:, f * T : (f + 1) * T].permute(0, 2, 1, 3)
+        assert torch.equal(kpool[s, :, :, :T], want_k)
+        assert torch.equal(vpool[s, :, :, :, :T], want_v.transpose(-1, -2))
         if Tp > T:
             assert kpool[s, :, :, T:].abs().sum() == 0 and vpool[s, :, :, :, T:].abs().sum() == 0
     order = [3, 5, 0, 5]
