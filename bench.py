@@ -183,6 +183,35 @@ def gather_bandwidth(device, iters=10):
     return moved / (ms / 1e3) / 1e9, ms / n
 
 
+def probe(cfg, device, iters=20):
+    """Short fixed sequence for hardware-counter runs (rocprofv3 --pmc): a plain device copy of
+    exactly 1 GiB (the FETCH_SIZE / WRITE_SIZE calibration), then steady-state launches of the
+    append kernel (one chunk, Lq tokens) and the attention kernel (Lq x full window)."""
+    import torch
+
+    from solarwm_amd import kernels
+
+    src = torch.empty(1 << 29, dtype=torch.int16, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)  # 1 GiB read + 1 GiB written per launch
+    torch.cuda.synchronize()
+    del src, dst
+    T, Lq, H = cfg["T"], cfg["chunk_f"] * cfg["T"], cfg["heads"]
+    n = cfg["cap_f"]
+    kpool, vpool, _, _ = kernels.new_pools(n + cfg["chunk_f"], cfg["batch"], H, T, torch.bfloat16, device)
+    q, k, v = make_inputs(dict(cfg, layers=1), device)[0]
+    for f in range(n):
+        kernels.append_frames(k, v, kpool, vpool, [f], frame_tokens=T, src_frame0=f % cfg["chunk_f"])
+    slots = list(range(n))
+    for _ in range(iters):
+        kernels.append_frames(k, v, kpool, vpool, [n, n + 1, n + 2], frame_tokens=T)
+    for _ in range(iters):
+        kernels.attention_frames(q, kpool, vpool, slots, frame_tokens=T)
+    torch.cuda.synchronize()
+    log(f"[probe] copy 1 GiB x3, append x{iters} ({Lq} tokens), attention x{iters} (Lq {Lq}, Lk {n * T})")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -190,6 +219,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2, help="untimed warmup chunks")
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-baselines", action="store_true", help="skip CPU / reference-GPU legs")
+    ap.add_argument("--probe", action="store_true",
+                    help="run the fixed counter-collection sequence instead of the benchmark")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -203,6 +234,9 @@ def main():
     from solarwm_amd import kernels, make_kv_cache_allocator
 
     cfg = CONFIGS[args.config]
+    if args.probe:
+        probe(cfg, torch.device("cuda:0"))
+        return
     K = cfg["chunks"] if args.steps is None else args.steps
     W = args.warmup
     dev = torch.device("cuda:0")

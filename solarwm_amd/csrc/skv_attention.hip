@@ -7,16 +7,20 @@
 // sink|local concatenation, the eviction memmove and the memory-bank gather of the reference
 // all become addressing: nothing is copied before attention.
 //
-// Work decomposition (one workgroup = 4 waves = 128 queries of one (batch, head)):
+// Work decomposition (one workgroup = 8 waves = 256 queries of one (batch, head)):
 //   * each wave owns 32 queries and keeps them in registers as the B operand of
 //     v_mfma_f32_32x32x16_bf16, computing S^T = K Q^T so that one lane holds one query's
-//     scores; the softmax row statistics then need a single cross-lane exchange (lane ^ 32);
-//   * K (64 x 128) and V^T (128 x 64) tiles are staged in LDS and shared by the 4 waves;
-//     the next tile's global loads are in flight while the current tile is computed;
+//     scores; the softmax row statistics then need one lane-pair swap (v_permlane32_swap);
+//   * 64-key K and V^T tiles are staged in LDS and shared by the 8 waves, in MFMA operand
+//     order (see kBlockBytes) by direct global->LDS loads; K is staged two tiles ahead and V
+//     one tile ahead of their use, so every load has a full iteration to land;
 //   * the K rows of each 32-key block are loaded in the permuted order key_perm(), which makes
 //     the fp32 S^T accumulator of a lane hold, per 8 registers, 8 consecutive keys — exactly
 //     the bf16x8 B operand (P^T) of the PV product; V is stored transposed in the pool so
 //     its A operand (V^T rows) is one 16 B LDS read;
+//   * iteration tau runs three independent streams — QK(tau+1), softmax(tau), PV(tau-1) —
+//     interleaved by hand (one MFMA, then a slice of the softmax) so the matrix core and the
+//     VALU work at the same time;
 //   * tiles never straddle frames (frames are padded to 64 tokens); padding keys and keys
 //     beyond a query's chunk-causal limit get -inf, decided per tile: full tiles skip the
 //     mask, tiles past every query's limit are not visited.
@@ -43,7 +47,7 @@ struct AttnArgs {
   int32_t slots[SKV_MAX_FRAMES];
 };
 
-constexpr int kBQ = 128;  // queries per workgroup (4 waves x 32)
+constexpr int kBQ = 256;  // queries per workgroup (8 waves x 32)
 
 // LDS holds each tile in MFMA operand order: one 1 KB block per A operand (64 lanes x 16 B),
 // lane L of the block at byte L*16.  K tile: 16 blocks (kb, s) = 32-key block x 16-channel
@@ -62,6 +66,17 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 __device__ inline int key_perm(int m) {
   const int a = m >> 3, h = (m >> 2) & 1, c = m & 3;
   return (a >> 1) * 16 + h * 8 + (a & 1) * 4 + c;
+}
+
+// Combine a lane's value with lane l^32's (the other key half of the same query) using the
+// gfx950 VALU lane swap; for a symmetric op both outputs of the swap pair give the result.
+__device__ inline float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ inline int64_t chunk_limit(int64_t pos, int64_t chunk, int64_t n_keys) {
@@ -84,9 +99,9 @@ __device__ inline void store4<float>(float* p, float x0, float x1, float x2, flo
   *reinterpret_cast<f32x4*>(p) = f32x4{x0, x1, x2, x3};
 }
 
-// Stage tile `tau` into LDS buffer `buf`.  bf16 pools: 8 direct 16 B global->LDS loads per
-// lane (4 K blocks + 4 V^T blocks per wave).  fp32 pools: loaded through registers and
-// rounded to bf16 (the C1 fp32 path; not performance critical).
+// Stage one 64-key tile of K (or V^T) into a 16 KB LDS buffer: each wave writes 4 of the
+// 16 operand blocks.  bf16 pools use direct 16 B global->LDS loads (no registers); fp32 pools
+// (the C1 path, not performance critical) go through registers and are rounded to bf16.
 template <typename KT>
 struct TileLoader;
 
@@ -95,49 +110,82 @@ struct TileLoader<bf16> {
   int64_t koff, voff;
   __device__ void init(int w, int lane, int Tp) {
     const int n = lane & 31, hh = lane >> 5;
-    // wave w stages K blocks (kb = w>>1, s = (w&1)*4 + j) and V^T blocks (db = w, j = kb*2+s2)
-    koff = (int64_t)((w >> 1) * 32 + key_perm(n)) * kHeadDim + (w & 1) * 64 + hh * 8;
-    voff = (int64_t)(w * 32 + n) * Tp + hh * 8;
+    // 8 waves: wave w stages K blocks 2w+j (kb = w>>2, s = (w&3)*2 + j) and V^T blocks
+    // 2w+j (db = w>>1, kb*2+s2 = (w&1)*2 + j)
+    koff = (int64_t)((w >> 2) * 32 + key_perm(n)) * kHeadDim + (w & 3) * 32 + hh * 8;
+    voff = (int64_t)((w >> 1) * 32 + n) * Tp + (w & 1) * 32 + hh * 8;
   }
-  __device__ void issue(const bf16* kt, const bf16* vt, char* lds, int w) const {
-    char* kdst = lds + (w * 4) * kBlockBytes;
-    char* vdst = lds + 16 * kBlockBytes + (w * 4) * kBlockBytes;
+  __device__ void issue_k(const bf16* kt, char* dst, int w) const {
+    dst += w * 2 * kBlockBytes;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
       __builtin_amdgcn_global_load_lds((glb_void_t*)(kt + koff + j * 16),
-                                       (lds_void_t*)(kdst + j * kBlockBytes), 16, 0, 0);
+                                       (lds_void_t*)(dst + j * kBlockBytes), 16, 0, 0);
+  }
+  __device__ void issue_v(const bf16* vt, char* dst, int w) const {
+    dst += w * 2 * kBlockBytes;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
       __builtin_amdgcn_global_load_lds((glb_void_t*)(vt + voff + j * 16),
-                                       (lds_void_t*)(vdst + j * kBlockBytes), 16, 0, 0);
+                                       (lds_void_t*)(dst + j * kBlockBytes), 16, 0, 0);
   }
 };
 
 template <>
 struct TileLoader<float> {
   int64_t koff, voff;
-  int lane;
-  __device__ void init(int w, int lane_, int Tp) {
-    lane = lane_;
+  int lane16;
+  __device__ void init(int w, int lane, int Tp) {
+    lane16 = lane * 16;
     const int n = lane & 31, hh = lane >> 5;
-    koff = (int64_t)((w >> 1) * 32 + key_perm(n)) * kHeadDim + (w & 1) * 64 + hh * 8;
-    voff = (int64_t)(w * 32 + n) * Tp + hh * 8;
+    koff = (int64_t)((w >> 2) * 32 + key_perm(n)) * kHeadDim + (w & 3) * 32 + hh * 8;
+    voff = (int64_t)((w >> 1) * 32 + n) * Tp + (w & 1) * 32 + hh * 8;
   }
-  __device__ void issue(const float* kt, const float* vt, char* lds, int w) const {
-    char* kdst = lds + (w * 4) * kBlockBytes + lane * 16;
-    char* vdst = lds + 16 * kBlockBytes + (w * 4) * kBlockBytes + lane * 16;
+  __device__ void issue_k(const float* kt, char* dst, int w) const {
+    dst += w * 2 * kBlockBytes + lane16;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<bf16x8*>(kdst + j * kBlockBytes) = Vec8<float>::load(kt + koff + j * 16).to_bf16();
-      *reinterpret_cast<bf16x8*>(vdst + j * kBlockBytes) = Vec8<float>::load(vt + voff + j * 16).to_bf16();
-    }
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<bf16x8*>(dst + j * kBlockBytes) = Vec8<float>::load(kt + koff + j * 16).to_bf16();
+  }
+  __device__ void issue_v(const float* vt, char* dst, int w) const {
+    dst += w * 2 * kBlockBytes + lane16;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<bf16x8*>(dst + j * kBlockBytes) = Vec8<float>::load(vt + voff + j * 16).to_bf16();
   }
 };
 
+// S^T (64 keys x 32 queries of this wave) = K Q^T from a K tile in LDS.
+__device__ inline void qk_tile(const char* kl, const bf16x8 (&qf)[8], f32x16 (&s)[2]) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bf16x8 ak = *reinterpret_cast<const bf16x8*>(kl + (kb * 8 + k) * kBlockBytes);
+      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[k], s[kb], 0, 0, 0);
+    }
+  }
+}
+
+// Padding keys (token >= T inside the frame) and keys past the lane's chunk-causal limit.
+__device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int key0, int lim) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = kb * 32 + (i >> 3) * 16 + hh * 8 + (i & 7);
+      if (tok0 + kk >= T || key0 + kk >= lim) s[kb][i] = -INFINITY;
+    }
+}
+
 template <typename QT, typename KT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char lds[];  // 2 x kTileBytes
+  // LDS: K tiles in [0, 32 KB) (two buffers), V^T tiles in [32 KB, 64 KB) (two buffers).
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  constexpr int kHalf = 16 * kBlockBytes;
 
   // XCD-aware order: workgroup ids are dealt round-robin over the 8 XCDs; XCD x gets the
   // contiguous logical range starting at x*per + min(x, rem), so q-tiles of one head run on
@@ -158,33 +206,30 @@ void attn_kernel(AttnArgs a) {
   const int qrow = q0 + w * 32 + n;
   const bool qlive = qrow < a.Lq;
 
-  // Q^T operand: lane (n, hh) holds q[qrow][s*16 + hh*8 .. +7] for s = 0..7.
+  // Q^T operand: lane (n, hh) holds q[qrow][k*16 + hh*8 .. +7] for k = 0..7.
   bf16x8 qf[8];
   {
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
                    (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 8;
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      qf[s] = qlive ? Vec8<QT>::load(qp + s * 16).to_bf16() : Vec8<bf16>::zero().to_bf16();
+    for (int k = 0; k < 8; ++k)
+      qf[k] = qlive ? Vec8<QT>::load(qp + k * 16).to_bf16() : Vec8<bf16>::zero().to_bf16();
   }
 
-  // Visibility limits (keys are indexed 0..n_keys-1 in frame-list order).
-  int64_t lim_lane = a.n_keys, lim_lo = a.n_keys, lim_hi = a.n_keys;
+  // Visibility limits (keys indexed 0..n_keys-1 in frame-list order; n_keys < 2^31).
+  const int n_keys = (int)a.n_keys;
+  int lim_lane = n_keys, lim_lo = n_keys, lim_hi = n_keys;
   if (a.mask_mode == SKV_MASK_CHUNK_CAUSAL) {
     const int qlast = min(q0 + kBQ, a.Lq) - 1;
-    lim_lane = chunk_limit(a.q_pos0 + min(qrow, a.Lq - 1), a.chunk, a.n_keys);
-    lim_lo = chunk_limit(a.q_pos0 + q0, a.chunk, a.n_keys);
-    lim_hi = chunk_limit(a.q_pos0 + qlast, a.chunk, a.n_keys);
+    lim_lane = (int)chunk_limit(a.q_pos0 + min(qrow, a.Lq - 1), a.chunk, n_keys);
+    lim_lo = (int)chunk_limit(a.q_pos0 + q0, a.chunk, n_keys);
+    lim_hi = (int)chunk_limit(a.q_pos0 + qlast, a.chunk, n_keys);
   }
   int ntau;
   {
-    const int64_t jf = lim_hi / a.T;
-    if (jf >= a.n_frames) {
-      ntau = a.n_frames * a.ntiles_f;
-    } else {
-      const int64_t r = lim_hi - jf * a.T;
-      ntau = (int)jf * a.ntiles_f + (int)((r + kTile - 1) / kTile);
-    }
+    const int jf = lim_hi / a.T;
+    ntau = jf >= a.n_frames ? a.n_frames * a.ntiles_f
+                            : jf * a.ntiles_f + (lim_hi - jf * a.T + kTile - 1) / kTile;
   }
 
   const KT* kpool = static_cast<const KT*>(a.kpool);
@@ -192,11 +237,20 @@ void attn_kernel(AttnArgs a) {
   const int64_t kbh = (int64_t)(b * a.H + h) * a.Tp * kHeadDim;  // (b,h) offset inside a slot
   TileLoader<KT> loader;
   loader.init(w, lane, a.Tp);
-  auto stage = [&](int tau, int buf) {
+  auto tile_base = [&](int tau) -> int64_t {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
-    const int64_t base = (int64_t)a.slots[j] * a.slot_stride + kbh;
-    loader.issue(kpool + base + (int64_t)t * kTile * kHeadDim, vpool + base + t * kTile,
-                 lds + buf * kTileBytes, w);
+    return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
+  };
+  auto vtile_base = [&](int tau) -> int64_t {
+    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    return (int64_t)a.slots[j] * a.slot_stride + kbh + t * kTile;
+  };
+  // mask decision for tile tau (uniform): returns true if any key of the tile may be hidden
+  auto tile_needs_mask = [&](int tau, int& tok0, int& key0) -> bool {
+    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    tok0 = t * kTile;
+    key0 = j * a.T + tok0;
+    return (tok0 + kTile > a.T) || (key0 + kTile > lim_lo);
   };
 
   f32x16 oacc[4];
@@ -204,99 +258,149 @@ void attn_kernel(AttnArgs a) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
-  // Running max in the log2 domain.  It is raised only when a tile's max exceeds it by more
-  // than kStale, so most tiles skip the O rescale; probabilities then stay <= 2^kStale, which
-  // bf16 and the fp32 sums represent exactly as well as values <= 1.
   constexpr float kStale = 8.0f;
   float m_run = -INFINITY, l_run = 0.f;
   const float c2 = a.scale_log2;
   const int lane16 = lane * 16;
+  // LDS map: K buffers at [0, 32 KB), V^T buffers at [32 KB, 64 KB).
+  auto kb_lds = [&](int i) { return lds + i * kHalf; };
+  auto vb_lds = [&](int i) { return lds + (2 + i) * kHalf; };
 
+  // Prologue: K(0), K(1) resident; V buffer 1 zeroed so PV(-1) of iteration 0 adds nothing.
+  f32x16 s_cur[2];
+  bf16x8 pprev[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) pprev[x][y] = Vec8<bf16>::zero().to_bf16();
   if (ntau > 0) {
-    stage(0, 0);
+    loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
+    if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      *reinterpret_cast<bf16x8*>(vb_lds(1) + (tid + 512 * r) * 16) = Vec8<bf16>::zero().to_bf16();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    qk_tile(kb_lds(0) + lane16, qf, s_cur);
+    int tok0, key0;
+    if (tile_needs_mask(0, tok0, key0)) mask_tile(s_cur, hh, tok0, a.T, key0, lim_lane);
+    __syncthreads();  // K(0) read by every wave before its buffer takes K(2)
   }
+
+  // Iteration tau: QK(tau+1), softmax(tau) and PV(tau-1) are independent; their 32 MFMAs and
+  // ~130 VALU ops are interleaved by hand (one MFMA, then a slice of the softmax) so the
+  // matrix core and the VALU work at the same time.  Resident: K(tau+1), V(tau-1); in flight:
+  // K(tau+2) into K(tau)'s buffer, V(tau) into V(tau-2)'s buffer.
   for (int tau = 0; tau < ntau; ++tau) {
-    const int buf = tau & 1;
-    if (tau + 1 < ntau) stage(tau + 1, buf ^ 1);
-    const char* kl = lds + buf * kTileBytes + lane16;
-    const char* vl = kl + 16 * kBlockBytes;
-    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
-    const int64_t key0 = (int64_t)j * a.T + t * kTile;
-    const int tok0 = t * kTile;
+    const int cb = tau & 1;
+    if (tau + 2 < ntau) loader.issue_k(kpool + tile_base(tau + 2), kb_lds(cb), w);
+    loader.issue_v(vpool + vtile_base(tau), vb_lds(cb), w);
+    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
+    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
 
-    // S^T (64 keys x 32 queries per wave) = K Q^T
-    f32x16 sacc[2];
+    f32x16 s_nxt[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[kb][i] = 0.f;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const bf16x8 ak = *reinterpret_cast<const bf16x8*>(kl + (kb * 8 + s) * kBlockBytes);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[s], sacc[kb], 0, 0, 0);
+    for (int i = 0; i < 16; ++i) { s_nxt[0][i] = 0.f; s_nxt[1][i] = 0.f; }
+    float mx0 = -INFINITY, mx1 = -INFINITY, mx = 0.f, alpha = 1.f, m_use = 0.f;
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};
+    float pf[32];
+    bf16x8 pb[2][2];
+    // operand of MFMA step i: even i -> QK step i/2 (k = i/4, kb = (i/2)&1), odd i -> PV step
+    // i/2 (db = (i/2)/4, kb = ((i/2)>>1)&1, s2 = (i/2)&1)
+    auto operand = [&](int i) -> bf16x8 {
+      const int st = i >> 1;
+      if ((i & 1) == 0) {
+        const int k = st >> 1, kbb = st & 1;
+        return *reinterpret_cast<const bf16x8*>(kl + (kbb * 8 + k) * kBlockBytes);
       }
-    }
-
-    const bool full = (tok0 + kTile <= a.T) && (key0 + kTile <= lim_lo);
-    if (!full) {
+      const int db = st >> 2, kbb = (st >> 1) & 1, s2 = st & 1;
+      return *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
+    };
+    bf16x8 opq[4];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int i = 0; i < 3; ++i) opq[i] = operand(i);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kk = kb * 32 + (i >> 3) * 16 + hh * 8 + (i & 7);
-          if (tok0 + kk >= a.T || key0 + kk >= lim_lane) sacc[kb][i] = -INFINITY;
+    for (int i = 0; i < 32; ++i) {
+      if (i + 3 < 32) opq[(i + 3) & 3] = operand(i + 3);
+      const int st = i >> 1;
+      if ((i & 1) == 0) {
+        const int k = st >> 1, kbb = st & 1;
+        s_nxt[kbb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], qf[k], s_nxt[kbb], 0, 0, 0);
+      } else {
+        const int db = st >> 2, kbb = (st >> 1) & 1, s2 = st & 1;
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], pprev[kbb][s2], oacc[db], 0, 0, 0);
+      }
+      // softmax slice i of tile tau
+      if (i == 0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx0 = fmaxf(mx0, s_cur[0][e]);
+      } else if (i == 1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx1 = fmaxf(mx1, s_cur[1][e]);
+      } else if (i == 2) {
+        mx = pair_max(fmaxf(mx0, mx1)) * c2;
+        const bool raise = mx > m_run + kStale;
+        const float m_new = raise ? mx : m_run;
+        alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
+        m_run = m_new;
+        m_use = m_new == -INFINITY ? 0.f : m_new;
+      } else {
+        // slices 3..31 compute the 32 probabilities: slice i handles elements [e0, e1)
+        const int e0 = ((i - 3) * 32) / 29, e1 = ((i - 2) * 32) / 29;
+#pragma unroll
+        for (int e = e0; e < e1; ++e) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
+          asm volatile("" ::"v"(p));  // keep this slice's exp next to its MFMA
+          pf[e] = p;
+          ls[e & 3] += p;
+          asm volatile("" ::"v"(ls[e & 3]));
+          if (e & 1) {
+            pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
+            pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
+          }
+          if ((e & 7) == 7) asm volatile("" ::"v"(pb[e >> 4][(e >> 3) & 1]));
         }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-
-    // online softmax (base 2); lanes l and l^32 hold the two key halves of one query
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * c2;
-    if (mx > m_run + kStale) {
-      // per lane: raise the reference point; the wave rescales only if some lane did
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when m_run == -inf
-      m_run = mx;
-      l_run *= alpha;
+    l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
+    if (__any(alpha != 1.0f)) {  // rare: some query's running max was raised
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
     }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-
-    bf16x8 pb[2][2];
+    if (tau + 1 < ntau) {
+      int tok0, key0;
+      if (tile_needs_mask(tau + 1, tok0, key0)) mask_tile(s_nxt, hh, tok0, a.T, key0, lim_lane);
+    }
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kbb = 0; kbb < 2; ++kbb) s_cur[kbb] = s_nxt[kbb];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], c2, -m_use));
-        l_run += p;
-        pb[kb][i >> 3][i & 7] = (bf16)p;
-      }
-
-    // O^T (128 x 32 per wave) += V^T P^T
+    for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 av =
-              *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kb * 2 + s2) * kBlockBytes);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[kb][s2], oacc[db], 0, 0, 0);
-        }
-
-    // the next tile has landed in the other buffer; every wave is done with this one
+      for (int y = 0; y < 2; ++y) pprev[x][y] = pb[x][y];
+    // K(tau+2) and V(tau) have landed; every wave is done with K(tau+1)'s and V(tau-1)'s
+    // buffers (they take K(tau+3) and V(tau+1) next)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
+  // Epilogue: PV(ntau-1).
+  if (ntau > 0) {
+    const char* vl = vb_lds((ntau - 1) & 1) + lane16;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int kbb = 0; kbb < 2; ++kbb)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8 av =
+              *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
+          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pprev[kbb][s2], oacc[db], 0, 0, 0);
+        }
+  }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if (qlive) {
     QT* op = static_cast<QT*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
@@ -367,6 +471,11 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
     set_error("skv_attention: q strides must be multiples of 8 and out strides of 4 elements");
     return SKV_E_ARG;
   }
+  if ((int64_t)n_frames * padded_tokens(frame_tokens) >= ((int64_t)1 << 31)) {
+    set_error("skv_attention: key window of %d frames x %d tokens exceeds 2^31", n_frames,
+              frame_tokens);
+    return SKV_E_ARG;
+  }
   if (q_len == 0) return SKV_OK;
   AttnArgs a;
   a.q = q;
@@ -404,7 +513,7 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
     a.slots[j] = frame_slots[j];
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(a.n_wg), block(256);
+  dim3 grid(a.n_wg), block(512);
   const size_t lds_bytes = 2 * kTileBytes;
   if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
     hipLaunchKernelGGL((attn_kernel<bf16, bf16>), grid, block, lds_bytes, s, a);
