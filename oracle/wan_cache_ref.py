@@ -17,6 +17,8 @@ Pinning (tests/test_oracle.py):
 * ``fp8_quantize`` — every e4m3fn code decoded from sign/exponent/mantissa; each quantised value
   is the nearest code (ties to even) found by exhaustive search.
 * ``memory_gather`` — index semantics checked against per-frame slicing.
+* ``fp8_fake_quant_frames`` / ``fp8_fake_quant_rows`` — compositions of the pinned
+  ``fp8_quantize``; checked for block independence and exact decoding of representable values.
 """
 
 from __future__ import annotations
@@ -346,6 +348,24 @@ def fp8_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 def fp8_dequantize(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return codes.float() * scale[..., None, None]
+
+
+def fp8_fake_quant_frames(x: torch.Tensor, frame_seqlen: int) -> torch.Tensor:
+    """Token-major [B, n*T, H, D] -> the values an fp8 frame cache holds: each (frame, stream,
+    head) block quantised with its own absmax/448 scale and decoded again (float32)."""
+    B, L, H, D = x.shape
+    n = L // frame_seqlen
+    fr = x.reshape(B, n, frame_seqlen, H, D).permute(1, 0, 3, 2, 4)  # [n, B, H, T, D]
+    codes, scale = fp8_quantize(fr)
+    deq = fp8_dequantize(codes, scale)
+    return deq.permute(1, 0, 3, 2, 4).reshape(B, L, H, D)
+
+
+def fp8_fake_quant_rows(q: torch.Tensor) -> torch.Tensor:
+    """Per-row (last dim) fp8 quantisation of bf16-rounded q with absmax/448 scales, decoded."""
+    qf = q.to(torch.bfloat16).float()
+    codes, scale = fp8_quantize(qf.unsqueeze(-2))
+    return fp8_dequantize(codes, scale).squeeze(-2)
 
 
 def e4m3_decode(code: int) -> float:

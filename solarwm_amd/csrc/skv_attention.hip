@@ -416,6 +416,295 @@ void attn_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp8-e4m3 pools (one dequantisation scale per (slot, stream, head) for K and for V).
+//
+// Same decomposition and 3-stage loop as attn_kernel, with v_mfma_f32_32x32x16_fp8_fp8 (8 fp8
+// per lane per operand) for both products:
+//   * Q is quantised in-kernel per query row (scale = absmax/448); the K frame scale and the Q
+//     row scale fold into the softmax FMA: x = acc * (log2e*scale*sq*sk) - m;
+//   * P is quantised as P * sv * G (sv = the tile's V frame scale, G = 110 / max_window(sv), so
+//     P <= 2^kStale8 = 4 maps below 448) and O is divided by G * sum(P) at the end;
+//   * K rows are read in the order key_perm8(), which puts key kb*32 + hh*16 + i in accumulator
+//     register i of lane half hh, so P^T's B operand for a 16-key step is 8 consecutive keys and
+//     the matching V^T operand is 8 consecutive bytes of a V^T row;
+//   * LDS keeps each tile as 1 KB "double blocks": lane L's 16 B hold its operands for two
+//     consecutive k-steps, written by one direct 16 B global->LDS load and read by one
+//     ds_read_b128 (K: d = hh*64 + step*8 .. +7 for both Q and K, which only has to agree
+//     between the two operands; V^T: keys kb*32 + hh*16 .. +15).
+constexpr int kBlock8 = 1024;          // one double block
+constexpr int kTile8 = 8 * kBlock8;    // one 64-key K (or V^T) tile in fp8
+typedef long fp8x8;                    // 8 e4m3 codes, the operand of the fp8 MFMA
+
+__device__ inline int key_perm8(int m) {
+  return ((m >> 2) & 1) * 16 + (m >> 3) * 4 + (m & 3);
+}
+
+__device__ inline void mask_tile8(f32x16 (&s)[2], int hh, int tok0, int T, int key0, int lim) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = kb * 32 + hh * 16 + i;
+      if (tok0 + kk >= T || key0 + kk >= lim) s[kb][i] = -INFINITY;
+    }
+}
+
+__device__ inline fp8x8 pack_fp8x8(const float* v) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
+  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], 0, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
+  return (fp8x8)(((unsigned long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+template <typename QT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_fp8_kernel(AttnArgs a) {
+  // LDS: K tiles [0, 16 KB) (two buffers), V^T tiles [16 KB, 32 KB) (two buffers).
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  int logical;
+  {
+    const int bid = blockIdx.x, xcd = bid & 7, idx = bid >> 3;
+    const int per = a.n_wg >> 3, rem = a.n_wg & 7;
+    logical = xcd * per + min(xcd, rem) + idx;
+  }
+  const int qt = logical % a.n_qtiles;
+  const int bh = logical / a.n_qtiles;
+  const int h = bh % a.H, b = bh / a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n = lane & 31, hh = lane >> 5;
+  const int q0 = qt * kBQ;
+  const int qrow = q0 + w * 32 + n;
+  const bool qlive = qrow < a.Lq;
+
+  // Q row quantisation: lane (n, hh) holds channels hh*64 .. hh*64+63 of its query.
+  fp8x8 q8[8];
+  float q_scale;  // dequantisation scale of this query row (absmax / 448)
+  {
+    float qv[64];
+    const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
+                   (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 64;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      Vec8<QT> v = qlive ? Vec8<QT>::load(qp + c * 8) : Vec8<QT>::zero();
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qv[c * 8 + j] = (float)(bf16)v.get(j);  // bf16 rounding first
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) amax = fmaxf(amax, __builtin_fabsf(qv[j]));
+    amax = pair_max(amax);
+    const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+    q_scale = amax / 448.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float t[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[j] = fminf(fmaxf(qv[c * 8 + j] * inv, -448.f), 448.f);
+      q8[c] = pack_fp8x8(t);
+    }
+  }
+
+  const int n_keys = (int)a.n_keys;
+  int lim_lane = n_keys, lim_lo = n_keys, lim_hi = n_keys;
+  if (a.mask_mode == SKV_MASK_CHUNK_CAUSAL) {
+    const int qlast = min(q0 + kBQ, a.Lq) - 1;
+    lim_lane = (int)chunk_limit(a.q_pos0 + min(qrow, a.Lq - 1), a.chunk, n_keys);
+    lim_lo = (int)chunk_limit(a.q_pos0 + q0, a.chunk, n_keys);
+    lim_hi = (int)chunk_limit(a.q_pos0 + qlast, a.chunk, n_keys);
+  }
+  int ntau;
+  {
+    const int jf = lim_hi / a.T;
+    ntau = jf >= a.n_frames ? a.n_frames * a.ntiles_f
+                            : jf * a.ntiles_f + (lim_hi - jf * a.T + kTile - 1) / kTile;
+  }
+
+  const uint8_t* kpool = static_cast<const uint8_t*>(a.kpool);
+  const uint8_t* vpool = static_cast<const uint8_t*>(a.vpool);
+  const int64_t kbh = (int64_t)(b * a.H + h) * a.Tp * kHeadDim;
+  const int64_t sc_bh = (int64_t)b * a.H + h;
+  auto slot_of = [&](int tau) { return (int64_t)a.slots[tau / a.ntiles_f]; };
+  auto ktile = [&](int tau) {
+    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    return kpool + (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
+  };
+  auto vtile = [&](int tau) {
+    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    return vpool + (int64_t)a.slots[j] * a.slot_stride + kbh + t * kTile;
+  };
+  auto tile_needs_mask = [&](int tau, int& tok0, int& key0) -> bool {
+    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    tok0 = t * kTile;
+    key0 = j * a.T + tok0;
+    return (tok0 + kTile > a.T) || (key0 + kTile > lim_lo);
+  };
+  // wave w stages K double block w (kb = w>>2, steps 2(w&3), 2(w&3)+1) and V^T double block w
+  // (db = w>>1, kb = w&1)
+  const int64_t koff = (int64_t)((w >> 2) * 32 + key_perm8(n)) * kHeadDim + hh * 64 + (w & 3) * 16;
+  const int64_t voff = (int64_t)((w >> 1) * 32 + n) * a.Tp + (w & 1) * 32 + hh * 16;
+  auto kb_lds = [&](int i) { return lds + i * kTile8; };
+  auto vb_lds = [&](int i) { return lds + (2 + i) * kTile8; };
+  auto issue_k = [&](int tau, char* dst) {
+    __builtin_amdgcn_global_load_lds((glb_void_t*)(ktile(tau) + koff),
+                                     (lds_void_t*)(dst + w * kBlock8), 16, 0, 0);
+  };
+  auto issue_v = [&](int tau, char* dst) {
+    __builtin_amdgcn_global_load_lds((glb_void_t*)(vtile(tau) + voff),
+                                     (lds_void_t*)(dst + w * kBlock8), 16, 0, 0);
+  };
+
+  // G maps the largest probability (<= 2^kStale8) times the largest V scale of the window
+  // just below 448.
+  constexpr float kStale8 = 2.0f;
+  float sv_max = 0.f;
+  for (int j = 0; j < a.n_frames; ++j)
+    sv_max = fmaxf(sv_max, a.vscale[(int64_t)a.slots[j] * a.B * a.H + sc_bh]);
+  const float G = sv_max > 0.f ? 110.0f / sv_max : 1.0f;
+  const float c2q = a.scale_log2 * q_scale;
+  const int lane16 = lane * 16;
+
+  f32x16 oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  auto qk = [&](const char* kl, f32x16 (&s)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4 d = *reinterpret_cast<const u32x4*>(kl + (kb * 4 + t) * kBlock8);
+        const fp8x8 lo = (fp8x8)(((unsigned long)d[1] << 32) | d[0]);
+        const fp8x8 hi = (fp8x8)(((unsigned long)d[3] << 32) | d[2]);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(lo, q8[2 * t], s[kb], 0, 0, 0);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(hi, q8[2 * t + 1], s[kb], 0, 0, 0);
+      }
+    }
+  };
+
+  f32x16 s_cur[2];
+  fp8x8 pprev[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) pprev[x][y] = 0;
+  if (ntau > 0) {
+    issue_k(0, kb_lds(0));
+    if (ntau > 1) issue_k(1, kb_lds(1));
+    *reinterpret_cast<u32x4*>(vb_lds(1) + tid * 16) = u32x4{0u, 0u, 0u, 0u};
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    qk(kb_lds(0) + lane16, s_cur);
+    int tok0, key0;
+    if (tile_needs_mask(0, tok0, key0)) mask_tile8(s_cur, hh, tok0, a.T, key0, lim_lane);
+    __syncthreads();
+  }
+  for (int tau = 0; tau < ntau; ++tau) {
+    const int cb = tau & 1;
+    if (tau + 2 < ntau) issue_k(tau + 2, kb_lds(cb));
+    issue_v(tau, vb_lds(cb));
+    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1)
+    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
+    const int64_t slot = slot_of(tau);
+    // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
+    // masked (-inf) logits stay -inf instead of becoming NaN
+    const float mult = fmaxf(c2q * a.kscale[slot * a.B * a.H + sc_bh], 1e-30f);
+    const float pv_scale = a.vscale[slot * a.B * a.H + sc_bh] * G;
+
+    f32x16 s_nxt[2];
+    qk(kl, s_nxt);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[kb][i]);
+    mx = pair_max(mx) * mult;
+    const bool raise = mx > m_run + kStale8;
+    const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
+    m_run = raise ? mx : m_run;
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};
+    fp8x8 pb[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[kb][s2 * 8 + j], mult, -m_use));
+          ls[j & 3] += p;
+          t[j] = p * pv_scale;
+        }
+        pb[kb][s2] = pack_fp8x8(t);
+      }
+    l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
+    asm volatile("" ::"v"(pb[0][0]), "v"(pb[0][1]), "v"(pb[1][0]), "v"(pb[1][1]), "v"(l_run));
+    // PV(tau-1)
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4 d = *reinterpret_cast<const u32x4*>(vl + (db * 2 + kb) * kBlock8);
+        const fp8x8 lo = (fp8x8)(((unsigned long)d[1] << 32) | d[0]);
+        const fp8x8 hi = (fp8x8)(((unsigned long)d[3] << 32) | d[2]);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(lo, pprev[kb][0], oacc[db], 0, 0, 0);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(hi, pprev[kb][1], oacc[db], 0, 0, 0);
+      }
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+    }
+    if (tau + 1 < ntau) {
+      int tok0, key0;
+      if (tile_needs_mask(tau + 1, tok0, key0)) mask_tile8(s_nxt, hh, tok0, a.T, key0, lim_lane);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) pprev[x][y] = pb[x][y];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+  if (ntau > 0) {
+    const char* vl = vb_lds((ntau - 1) & 1) + lane16;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4 d = *reinterpret_cast<const u32x4*>(vl + (db * 2 + kb) * kBlock8);
+        const fp8x8 lo = (fp8x8)(((unsigned long)d[1] << 32) | d[0]);
+        const fp8x8 hi = (fp8x8)(((unsigned long)d[3] << 32) | d[2]);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(lo, pprev[kb][0], oacc[db], 0, 0, 0);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(hi, pprev[kb][1], oacc[db], 0, 0, 0);
+      }
+  }
+  const float l_tot = pair_sum(l_run);
+  const float inv = l_tot > 0.f ? 1.0f / (l_tot * G) : 0.f;
+  if (qlive) {
+    QT* op = static_cast<QT*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+             (int64_t)qrow * a.o_st;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + g * 8 + hh * 4;
+        store4<QT>(op + d0, oacc[db][g * 4 + 0] * inv, oacc[db][g * 4 + 1] * inv,
+                   oacc[db][g * 4 + 2] * inv, oacc[db][g * 4 + 3] * inv);
+      }
+  }
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -463,9 +752,13 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
     set_error("skv_attention: q_dtype=%d unsupported", q_dtype);
     return SKV_E_UNSUPPORTED;
   }
-  if (!(pool_dtype == SKV_BF16 || pool_dtype == SKV_F32)) {
-    set_error("skv_attention: pool_dtype=%d unsupported by this build", pool_dtype);
+  if (!(pool_dtype == SKV_BF16 || pool_dtype == SKV_F32 || pool_dtype == SKV_FP8_E4M3)) {
+    set_error("skv_attention: pool_dtype=%d unsupported", pool_dtype);
     return SKV_E_UNSUPPORTED;
+  }
+  if (pool_dtype == SKV_FP8_E4M3 && (!k_scale || !v_scale)) {
+    set_error("skv_attention: fp8 pools need k_scale and v_scale");
+    return SKV_E_ARG;
   }
   if (q_sb % 8 || q_st % 8 || q_sh % 8 || out_sb % 4 || out_st % 4 || out_sh % 4) {
     set_error("skv_attention: q strides must be multiples of 8 and out strides of 4 elements");
@@ -515,7 +808,12 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(a.n_wg), block(512);
   const size_t lds_bytes = 2 * kTileBytes;
-  if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
+  if (pool_dtype == SKV_FP8_E4M3) {
+    if (q_dtype == SKV_BF16)
+      hipLaunchKernelGGL((attn_fp8_kernel<bf16>), grid, block, 4 * kTile8, s, a);
+    else
+      hipLaunchKernelGGL((attn_fp8_kernel<float>), grid, block, 4 * kTile8, s, a);
+  } else if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
     hipLaunchKernelGGL((attn_kernel<bf16, bf16>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
     hipLaunchKernelGGL((attn_kernel<bf16, float>), grid, block, lds_bytes, s, a);

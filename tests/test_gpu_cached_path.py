@@ -132,3 +132,63 @@ def test_memory_bank_frames_fused(gpu):
         assert_attn_close(x, want)
         apply_cache_updates([cache], [(0, upd)])
         ref.apply_cache_updates(oracle, [(0, oupd)])
+
+
+def test_fp8_cache_rollout_vs_bf16_oracle(gpu):
+    """Config-5 semantics at reduced size: 4 independent streams, fp8-e4m3 cache with
+    per-(frame, head) scales, K/V with 1% x20 outlier channels; the committed cache holds exactly
+    the oracle's quantisation of its bf16 cache, and each pass's attention matches the
+    quantisation-aware oracle (fp8 frames and query rows decoded) within the normalised fp8 bar."""
+    from .helpers import FP8_NORM_MAX, FP8_NORM_MEAN
+
+    T, H, chunk_f, cap_f, sink_f, B = 130, 3, 3, 7, 1, 4
+    Lq = chunk_f * T
+    alloc = make_kv_cache_allocator(
+        num_layers=1, num_heads=H, head_dim=128, frame_sequence_length=T, local_attn_size=cap_f,
+        sink_size=sink_f, num_frame_per_block=chunk_f, cache_dtype=torch.float8_e4m3fn,
+    )
+    cache = alloc(B, dtype=torch.bfloat16, device=gpu)[0]
+    oracle = ref.allocate_kv_cache(1, B, cap_f * T, H, 128, torch.bfloat16)
+    g = torch.Generator().manual_seed(9)
+    ch = torch.randperm(128, generator=g)[:2]
+
+    def qaware(q, k, v):
+        return ref.attention(ref.fp8_fake_quant_rows(q), ref.fp8_fake_quant_frames(k.float(), T),
+                             ref.fp8_fake_quant_frames(v.float(), T), round_inputs_to_bf16=False)
+
+    for c in range(5):
+        for policy in ("none", "commit"):
+            q = torch.randn(B, Lq, H, 128, generator=g).bfloat16()
+            k = torch.randn(B, Lq, H, 128, generator=g)
+            v = torch.randn(B, Lq, H, 128, generator=g)
+            k[..., ch] *= 20
+            v[..., ch] *= 20
+            k, v = k.bfloat16(), v.bfloat16()
+            x, upd = attend_cached(q.to(gpu), k.to(gpu), v.to(gpu), cache, c * Lq)
+            seen = {}
+
+            def attn(qq, kk, vv):
+                seen["v"] = vv
+                return qaware(qq, kk, vv)
+
+            want, oupd = ref.cached_self_attention(
+                q, k, v, oracle[0], current_start=c * Lq, frame_seqlen=T, sink_size=sink_f,
+                local_attn_size=cap_f, attn_fn=attn,
+            )
+            torch.cuda.synchronize()
+            rms_v = seen["v"].double().pow(2).mean(dim=1, keepdim=True).sqrt().clamp_min(1e-6)
+            e = (x.cpu().double() - want.double()).abs() / rms_v
+            assert float(e.max()) <= FP8_NORM_MAX and float(e.mean()) <= FP8_NORM_MEAN, (
+                c, policy, float(e.max()), float(e.mean()))
+            if policy == "commit":
+                apply_cache_updates([cache], [(0, upd)])
+                ref.apply_cache_updates(oracle, [(0, oupd)])
+        # committed cache: codes and scales equal the oracle quantisation of its bf16 cache
+        live = cache.local_end // T
+        for p in range(live):
+            slot = cache.table[p]
+            frame = oracle[0]["k"][:, p * T : (p + 1) * T].permute(0, 2, 1, 3)  # [B, H, T, D]
+            codes, scale = ref.fp8_quantize(frame)
+            got = cache.kpool[slot, :, :, :T].cpu().view(torch.uint8)
+            assert torch.equal(got, codes.view(torch.uint8)), (c, p)
+            assert torch.equal(cache.kscale[slot].cpu(), scale), (c, p)

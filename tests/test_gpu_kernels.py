@@ -202,3 +202,93 @@ def test_empty_window_raises(gpu):
         kernels.attention_frames(q, kpool, vpool, [], frame_tokens=64)
     with pytest.raises(ValueError, match="outside"):
         kernels.attention_frames(q, kpool, vpool, [5], frame_tokens=64)
+
+
+# ---------------------------------------------------------------------------------------------
+# fp8-e4m3 cache (BASELINE config 5 semantics): per-(slot, stream, head) absmax/448 scales;
+# attention error measured against the oracle on the original bf16 K/V.
+# ---------------------------------------------------------------------------------------------
+def _fp8_pool_from(k, v, T, device, perm_seed=0):
+    B, L, H, _ = k.shape
+    n = L // T
+    g = torch.Generator().manual_seed(perm_seed)
+    slots = torch.randperm(n + 2, generator=g)[:n].tolist()
+    kpool, vpool, ks, vs = kernels.new_pools(n + 2, B, H, T, torch.float8_e4m3fn, device)
+    kd, vd = k.to(device), v.to(device)
+    for f in range(n):
+        kernels.append_frames(kd, vd, kpool, vpool, [slots[f]], frame_tokens=T, src_frame0=f,
+                              kscale=ks, vscale=vs)
+    return kpool, vpool, ks, vs, slots
+
+
+def _outlier_kv(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=g)
+    ch = torch.randperm(shape[-1], generator=g)[: max(1, shape[-1] // 100)]
+    x[..., ch] *= 20.0  # 1% of channels are x20 outliers
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("B,H,Lq,T,n", [(4, 3, 390, 390, 21), (1, 12, 1170, 390, 6), (2, 1, 37, 1560, 2)])
+def test_fp8_attention_unit_scale_vs_bf16_oracle(gpu, B, H, Lq, T, n):
+    """N(0,1) K/V: the fp8 cache path meets the north-star fp8 bar (stated for the 21-frame
+    config-5 window) against the bf16 oracle; windows here hold 2340 to 8190 keys (a 1170-key
+    window measured 3.9e-2 max-abs: fewer keys make the softmax sharper)."""
+    _say("fp8 attention unit scale", B, H, Lq, T, n)
+    from .helpers import FP8_MAX_ABS, FP8_MEAN_ABS
+
+    q = _rand((B, Lq, H, 128), 31, torch.bfloat16)
+    k = _rand((B, n * T, H, 128), 32, torch.bfloat16)
+    v = _rand((B, n * T, H, 128), 33, torch.bfloat16)
+    kpool, vpool, ks, vs, slots = _fp8_pool_from(k, v, T, gpu)
+    out = kernels.attention_frames(q.to(gpu), kpool, vpool, slots, frame_tokens=T, kscale=ks,
+                                   vscale=vs)
+    torch.cuda.synchronize()
+    assert_attn_close(out, ref.attention(q, k, v), FP8_MAX_ABS, FP8_MEAN_ABS)
+
+
+def assert_fp8_close_normalised(got, q, k, v, T, mask=None):
+    """Outlier data: compare with the quantisation-aware oracle (fp8 cache frames and fp8 query
+    rows decoded, fp64 softmax) and normalise the error by each channel's V RMS; what remains is
+    the fp8 rounding of P and fp32 accumulation."""
+    from .helpers import FP8_NORM_MAX, FP8_NORM_MEAN
+
+    want = ref.attention(ref.fp8_fake_quant_rows(q), ref.fp8_fake_quant_frames(k.float(), T),
+                         ref.fp8_fake_quant_frames(v.float(), T), mask=mask,
+                         round_inputs_to_bf16=False).double()
+    rms_v = v.double().pow(2).mean(dim=1, keepdim=True).sqrt().clamp_min(1e-6)
+    got = got.detach().cpu().double()
+    assert torch.isfinite(got).all()
+    e = (got - want).abs() / rms_v
+    assert float(e.max()) <= FP8_NORM_MAX, f"normalised max error {float(e.max()):.3e}"
+    assert float(e.mean()) <= FP8_NORM_MEAN, f"normalised mean error {float(e.mean()):.3e}"
+
+
+@pytest.mark.parametrize("B,H,Lq,T,n", [(1, 2, 256, 130, 4), (4, 3, 390, 390, 3), (1, 12, 1170, 390, 6),
+                                        (2, 1, 37, 1560, 2)])
+def test_fp8_attention_outliers_vs_quantised_oracle(gpu, B, H, Lq, T, n):
+    _say("fp8 attention outliers", B, H, Lq, T, n)
+    q = _rand((B, Lq, H, 128), 31, torch.bfloat16)
+    k = _outlier_kv((B, n * T, H, 128), 32)
+    v = _outlier_kv((B, n * T, H, 128), 33)
+    kpool, vpool, ks, vs, slots = _fp8_pool_from(k, v, T, gpu)
+    out = kernels.attention_frames(q.to(gpu), kpool, vpool, slots, frame_tokens=T, kscale=ks,
+                                   vscale=vs)
+    torch.cuda.synchronize()
+    assert_fp8_close_normalised(out, q, k, v, T)
+
+
+def test_fp8_chunk_causal_and_zero_frames(gpu):
+    T, n = 100, 6
+    q = _rand((1, n * T, 2, 128), 41, torch.bfloat16)
+    k = _outlier_kv((1, n * T, 2, 128), 42)
+    v = _outlier_kv((1, n * T, 2, 128), 43)
+    k[:, 2 * T : 3 * T] = 0  # an all-zero K frame (scale 0) and V frame
+    v[:, 4 * T : 5 * T] = 0
+    kpool, vpool, ks, vs, slots = _fp8_pool_from(k, v, T, gpu)
+    dense, _ = ref.inference_window_mask(0, n, T, 2)
+    got = kernels.attention_frames(q.to(gpu), kpool, vpool, slots, frame_tokens=T, kscale=ks,
+                                   vscale=vs, mask_mode=_lib.SKV_MASK_CHUNK_CAUSAL,
+                                   chunk_tokens=2 * T)
+    torch.cuda.synchronize()
+    assert_fp8_close_normalised(got, q, k, v, T, mask=dense[: n * T, : n * T])

@@ -301,3 +301,21 @@ def test_fp8_quantize_nearest_and_scale():
                 assert int(raw[b, h, t, d]) == _nearest_code(y, table), (b, h, t, d, y)
     # the absmax element lands exactly on +-448
     assert float(codes[0, 1, 5, 2].float()) == 448.0
+
+
+def test_fp8_fake_quant_blocks_are_independent():
+    """Each (frame, stream, head) block is scaled by its own absmax: values that are exactly
+    representable after scaling decode exactly, and changing one frame leaves the others."""
+    T = 4
+    x = torch.zeros(2, 3 * T, 2, 8)
+    x[:, :T] = 448.0  # frame 0: every value equals the absmax -> decodes exactly
+    x[0, T : 2 * T, 1] = torch.tensor([1.0, -2.0, 0.5, 4.0] * 8).view(T, 8)  # powers of two
+    y = ref.fp8_fake_quant_frames(x, T)
+    assert torch.equal(y[:, :T], x[:, :T])
+    assert torch.equal(y[0, T : 2 * T, 1], x[0, T : 2 * T, 1])
+    x2 = x.clone()
+    x2[:, 2 * T :] = 1000.0
+    y2 = ref.fp8_fake_quant_frames(x2, T)
+    assert torch.equal(y2[:, : 2 * T], y[:, : 2 * T])
+    q = torch.tensor([[3.0, -1.5, 0.75, 0.0]])
+    assert torch.equal(ref.fp8_fake_quant_rows(q), q)  # absmax 3 -> scale 3/448, all exact
