@@ -28,12 +28,19 @@ import time
 
 CONFIGS = {
     "c2": dict(workload="wan2.1-1.3b", layers=30, heads=12, T=1560, chunk_f=3, cap_f=21,
-               sink_f=1, chunks=27, batch=1),
+               sink_f=1, chunks=27, batch=1, cache="bf16"),
     "c3": dict(workload="wan2.2-5b", layers=30, heads=24, T=880, chunk_f=3, cap_f=21,
-               sink_f=1, chunks=40, batch=1),
+               sink_f=1, chunks=40, batch=1, cache="bf16"),
+    "c5": dict(workload="wan2.1-1.3b fp8-e4m3 kv, 4 streams", layers=30, heads=12, T=1560,
+               chunk_f=3, cap_f=21, sink_f=1, chunks=27, batch=4, cache="fp8"),
 }
+# config 4: 33B-class memory path (one GPU holds one layer's 256-slot bank: 8.4 GB; all 48
+# layers would need 403 GB)
+C4 = dict(workload="33b-class memory path", layers=48, heads=40, T=1560, chunk_f=3, cap_f=21,
+          sink_f=1, bank=256, mem_frames=8)
 PASSES = ["none"] * 4 + ["commit"]  # stage2.py:683-760: NFE4 then a t=0 commit forward
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 HBM_PEAK_GBPS = 8000.0
 
 
@@ -41,16 +48,70 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_inputs(cfg, device, seed=1234):
+def make_inputs(cfg, device, seed=1234, outliers=False):
+    """Per-layer bf16 Q/K/V of one chunk, N(0,1); with ``outliers`` 1% of K/V channels x20
+    (BASELINE config 5)."""
     import torch
 
     g = torch.Generator(device=device).manual_seed(seed)
     Lq = cfg["chunk_f"] * cfg["T"]
     shape = (cfg["batch"], Lq, cfg["heads"], 128)
-    return [
-        tuple(torch.randn(shape, generator=g, device=device, dtype=torch.bfloat16) for _ in range(3))
-        for _ in range(cfg["layers"])
-    ]
+    ch = torch.randperm(128, generator=g, device=device)[:2] if outliers else None
+    out = []
+    for _ in range(cfg["layers"]):
+        q, k, v = (torch.randn(shape, generator=g, device=device, dtype=torch.bfloat16) for _ in range(3))
+        if ch is not None:
+            k[..., ch] *= 20
+            v[..., ch] *= 20
+        out.append((q, k, v))
+    return out
+
+
+def make_caches(cfg, device):
+    import torch
+
+    from solarwm_amd import make_kv_cache_allocator
+
+    alloc = make_kv_cache_allocator(
+        num_layers=cfg["layers"], num_heads=cfg["heads"], head_dim=128,
+        frame_sequence_length=cfg["T"], local_attn_size=cfg["cap_f"], sink_size=cfg["sink_f"],
+        num_frame_per_block=cfg["chunk_f"],
+        cache_dtype=torch.float8_e4m3fn if cfg["cache"] == "fp8" else None,
+    )
+    return alloc(cfg["batch"], dtype=torch.bfloat16, device=device)
+
+
+def timed_rollout(cfg, inputs, caches, chunk_ids):
+    """Run chunks with HIP events around every launch; returns the measured figures."""
+    import torch
+
+    from solarwm_amd import kernels
+
+    with kernels.timed_launches() as tm:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run_ours(cfg, inputs, caches, chunk_ids)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    n_attn, attn_ms, attn_flops = tm.summary("attention")
+    n_app, app_ms, app_bytes = tm.summary("append")
+    recs = tm.records["attention"]
+    top = max(w for _, _, w in recs)
+    steady = [r for r in recs if r[2] == top]
+    st_ms = sum(a.elapsed_time(b) for a, b, _ in steady) / len(steady)
+    n = len(list(chunk_ids))
+    return {
+        "wall_s": wall,
+        "chunks": n,
+        "frames_per_s": cfg["chunk_f"] * cfg["batch"] * n / wall,
+        "attn_launches": n_attn,
+        "attn_avg_ms": attn_ms / n_attn,
+        "attn_tflops": attn_flops / (attn_ms / 1e3) / 1e12,
+        "attn_steady_ms": st_ms,
+        "attn_steady_tflops": top / (st_ms / 1e3) / 1e12,
+        "append_gbps": app_bytes / (app_ms / 1e3) / 1e9,
+        "append_avg_us": app_ms / n_app * 1e3,
+    }
 
 
 def run_ours(cfg, inputs, caches, chunk_ids):
@@ -212,6 +273,115 @@ def probe(cfg, device, iters=20):
     log(f"[probe] copy 1 GiB x3, append x{iters} ({Lq} tokens), attention x{iters} (Lq {Lq}, Lk {n * T})")
 
 
+def steady_state(name, device, fill=7, timed=3):
+    """Configs 3 and 5: fill the 21-frame window (chunks 0..fill-1, untimed), then time `timed`
+    steady-state chunks (4 none + 1 commit passes over all layers)."""
+    import torch
+
+    cfg = CONFIGS[name]
+    inputs = make_inputs(cfg, device, outliers=cfg["cache"] == "fp8")
+    caches = make_caches(cfg, device)
+    run_ours(cfg, inputs, caches, range(fill))
+    st = timed_rollout(cfg, inputs, caches, range(fill, fill + timed))
+    st["workload"] = (
+        f"{cfg['workload']}: {cfg['layers']} layers, H{cfg['heads']}xD128, {cfg['T']} tok/frame, "
+        f"Lq {cfg['chunk_f'] * cfg['T']}, window {cfg['cap_f'] * cfg['T']} keys, batch "
+        f"{cfg['batch']}, {cfg['cache']} cache; chunks {fill}..{fill + timed - 1} (steady state)"
+    )
+    del inputs, caches
+    torch.cuda.empty_cache()
+    return st
+
+
+def c5_quality(device):
+    """Config 5 cache memory and attention error: one steady-state layer pass with the fp8
+    cache against the same pass with a bf16 cache (4 streams, 1% x20 outlier channels)."""
+    import torch
+
+    cfg = dict(CONFIGS["c5"], layers=1)
+    inputs = make_inputs(cfg, device, outliers=True)
+    outs = {}
+    mem = {}
+    for cache in ("fp8", "bf16"):
+        c = dict(cfg, cache=cache)
+        caches = make_caches(c, device)
+        run_ours(c, inputs, caches, range(7))
+        from solarwm_amd import attend_cached
+
+        q, k, v = inputs[0]
+        x, _ = attend_cached(q, k, v, caches[0], 7 * cfg["chunk_f"] * cfg["T"])
+        outs[cache] = x.float()
+        kp = caches[0].kpool
+        live = cfg["cap_f"] * kp[0].numel() * kp.element_size() * 2  # K+V of the live window
+        if caches[0].kscale is not None:
+            live += 2 * cfg["cap_f"] * caches[0].kscale[0].numel() * 4
+        mem[cache] = live
+        del caches
+    torch.cuda.synchronize()
+    v = inputs[0][2].float()
+    err = (outs["fp8"] - outs["bf16"]).abs()
+    rms_v = v.pow(2).mean(dim=1, keepdim=True).sqrt()
+    return {
+        "cache_bytes_per_layer_bf16": mem["bf16"],
+        "cache_bytes_per_layer_fp8": mem["fp8"],
+        "memory_saved_pct": round(100 * (1 - mem["fp8"] / mem["bf16"]), 2),
+        "err_vs_bf16_max_abs": float(err.max()),
+        "err_vs_bf16_mean_abs": float(err.mean()),
+        "err_vs_bf16_normalised_mean": float((err / rms_v).mean()),
+        "note": "error of the fp8-cache attention output against the bf16-cache output of the "
+                "same kernel family on one steady-state pass (Lk 32760, 4 streams, outliers x20)",
+    }
+
+
+def c4_memory_path(device, timed_chunks=3):
+    """Config 4 at its real per-layer shape: 40 heads, 1560 tok/frame, a 256-slot memory bank
+    per layer; each chunk attends 8 seeded bank frames ahead of the 21-frame live window
+    (45240 keys) straight from the slot table.  One layer is timed and extrapolated to 48."""
+    import torch
+
+    from solarwm_amd import apply_cache_updates, attend_cached, kernels
+    from solarwm_amd.cache import CacheGeometry, SlotKVCache
+
+    c = C4
+    geom = CacheGeometry(batch=1, heads=c["heads"], head_dim=128, frame_tokens=c["T"],
+                         capacity_frames=c["cap_f"], sink_frames=c["sink_f"],
+                         staging_frames=c["chunk_f"], bank_frames=c["bank"])
+    cache = SlotKVCache(geom, dtype=torch.bfloat16, device=device)
+    b0 = geom.bank_slot0
+    cache.kpool[b0:].normal_()
+    cache.vpool[b0:].normal_()
+    q, k, v = make_inputs(dict(c, layers=1, batch=1), device)[0]
+    Lq = c["chunk_f"] * c["T"]
+    for ch in range(7):  # fill the live window
+        _, upd = attend_cached(q, k, v, cache, ch * Lq)
+        apply_cache_updates([cache], [(0, upd)])
+    g = torch.Generator().manual_seed(11)
+    out = torch.empty_like(q)
+    with kernels.timed_launches() as tm:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for ch in range(7, 7 + timed_chunks):
+            idx = torch.randperm(c["bank"], generator=g)[: c["mem_frames"]].tolist()
+            for policy in PASSES:
+                _, upd = attend_cached(q, k, v, cache, ch * Lq, memory_frames=idx, out=out)
+                if policy != "none":
+                    apply_cache_updates([cache], [(0, upd)])
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    n, ms, flops = tm.summary("attention")
+    per_pass = wall / (timed_chunks * len(PASSES))
+    del cache
+    torch.cuda.empty_cache()
+    return {
+        "workload": "33B-class memory path: H40xD128, 1560 tok/frame, Lq 4680, 8 of 256 bank "
+                    "frames + 21-frame window (45240 keys), one layer timed, x48 extrapolated",
+        "frames_per_s_48_layers_extrapolated": round(c["chunk_f"] / (per_pass * c["layers"] * len(PASSES)), 4),
+        "layer_pass_ms": round(per_pass * 1e3, 3),
+        "attn_tflops": round(flops / (ms / 1e3) / 1e12, 1),
+        "attn_avg_ms": round(ms / n, 3),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,6 +389,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2, help="untimed warmup chunks")
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-baselines", action="store_true", help="skip CPU / reference-GPU legs")
+    ap.add_argument("--no-aux", action="store_true",
+                    help="skip the steady-state legs of configs 3, 4 and 5")
     ap.add_argument("--probe", action="store_true",
                     help="run the fixed counter-collection sequence instead of the benchmark")
     args = ap.parse_args()
@@ -231,7 +403,7 @@ def main():
 
     import torch
 
-    from solarwm_amd import kernels, make_kv_cache_allocator
+    from solarwm_amd import kernels
 
     cfg = CONFIGS[args.config]
     if args.probe:
@@ -242,12 +414,8 @@ def main():
     dev = torch.device("cuda:0")
     T, Lq = cfg["T"], cfg["chunk_f"] * cfg["T"]
     log(f"[bench] config {args.config}: {cfg}; timed chunks {K}, warmup {W}")
-    inputs = make_inputs(cfg, dev)
-    alloc = make_kv_cache_allocator(
-        num_layers=cfg["layers"], num_heads=cfg["heads"], head_dim=128, frame_sequence_length=T,
-        local_attn_size=cfg["cap_f"], sink_size=cfg["sink_f"], num_frame_per_block=cfg["chunk_f"],
-    )
-    caches = alloc(cfg["batch"], dtype=torch.bfloat16, device=dev)
+    inputs = make_inputs(cfg, dev, outliers=cfg["cache"] == "fp8")
+    caches = make_caches(cfg, dev)
 
     # warmup on its own rollout, then reset every cache to the empty state
     run_ours(cfg, inputs, caches, range(W))
@@ -257,24 +425,15 @@ def main():
     torch.cuda.synchronize()
     log("[bench] warmup done")
 
-    with kernels.timed_launches() as tm:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        run_ours(cfg, inputs, caches, range(K))
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    wall = t1 - t0
-    fps = cfg["chunk_f"] * K / wall
-    n_attn, attn_ms, attn_flops = tm.summary("attention")
-    n_app, app_ms, app_bytes = tm.summary("append")
-    steady = [r for r in tm.records["attention"] if r[2] == max(w for _, _, w in tm.records["attention"])]
-    st_ms = sum(a.elapsed_time(b) for a, b, _ in steady) / len(steady)
-    st_tflops = steady[0][2] / (st_ms / 1e3) / 1e12
-    achieved = attn_flops / (attn_ms / 1e3) / 1e12
+    st = timed_rollout(cfg, inputs, caches, range(K))
+    wall, fps = st["wall_s"], st["frames_per_s"]
+    achieved = st["attn_tflops"]
     log(f"[bench] ours: {wall:.3f} s for {K} chunks -> {fps:.3f} latent frames/s; attention "
-        f"{n_attn} launches avg {attn_ms / n_attn:.3f} ms, {achieved:.1f} TFLOP/s "
-        f"(steady {st_ms:.3f} ms, {st_tflops:.1f} TFLOP/s); append {app_bytes / (app_ms / 1e3) / 1e9:.0f} GB/s")
+        f"{st['attn_launches']} launches avg {st['attn_avg_ms']:.3f} ms, {achieved:.1f} TFLOP/s "
+        f"(steady {st['attn_steady_ms']:.3f} ms, {st['attn_steady_tflops']:.1f} TFLOP/s); "
+        f"append {st['append_gbps']:.0f} GB/s")
 
+    peak = BF16_PEAK_TFLOPS if cfg["cache"] == "bf16" else FP8_PEAK_TFLOPS
     result = {
         "metric": "latent frames/s per 30-layer stack",
         "value": round(fps, 4),
@@ -286,8 +445,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) bf16 Q/K/V per layer, resident in HBM before timing",
+        "dtype": "bf16" if cfg["cache"] == "bf16" else "fp8-e4m3 K/V, bf16 Q/O",
+        "data": "synthetic: seeded N(0,1) bf16 Q/K/V per layer, resident in HBM before timing"
+                + ("; 1% of K/V channels x20" if cfg["cache"] == "fp8" else ""),
         "config": {
             "workload": (
                 f"{cfg['workload']} kv-cache rollout: {cfg['layers']} layers, H{cfg['heads']}xD128, "
@@ -301,23 +461,22 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_kernel<bf16,bf16>",
+            "kernel": "attn_kernel<bf16,bf16>" if cfg["cache"] == "bf16" else "attn_fp8_kernel<bf16>",
             "achieved": round(achieved, 2),
-            "peak": BF16_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "frac": round(achieved / peak, 4),
             "traffic": None,
-            "launches": n_attn,
-            "avg_launch_ms": round(attn_ms / n_attn, 4),
-            "steady_state": {"Lk": cfg["cap_f"] * T, "avg_launch_ms": round(st_ms, 4),
-                             "achieved": round(st_tflops, 2)},
+            "launches": st["attn_launches"],
+            "avg_launch_ms": round(st["attn_avg_ms"], 4),
+            "steady_state": {"Lk": cfg["cap_f"] * T, "avg_launch_ms": round(st["attn_steady_ms"], 4),
+                             "achieved": round(st["attn_steady_tflops"], 2)},
         },
-        "attn_mfma_util_pct": round(100 * achieved / BF16_PEAK_TFLOPS, 2),
-        "append_gbps": round(app_bytes / (app_ms / 1e3) / 1e9, 1),
-        "append_frac_hbm": round(app_bytes / (app_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
-        "append_avg_launch_us": round(app_ms / n_app * 1e3, 2),
+        "attn_mfma_util_pct": round(100 * achieved / peak, 2),
+        "append_gbps": round(st["append_gbps"], 1),
+        "append_frac_hbm": round(st["append_gbps"] / HBM_PEAK_GBPS, 4),
+        "append_avg_launch_us": round(st["append_avg_us"], 2),
     }
-    del tm
 
     gbps, g_ms = gather_bandwidth(dev)
     result["gather_gbps"] = round(gbps, 1)
@@ -334,8 +493,10 @@ def main():
             for _ in range(cfg["layers"])
         ]
         reference_gpu_step(cfg, inputs, dense, range(1))
-        for st in dense:
-            st["k"].zero_(); st["v"].zero_(); st["g"] = st["l"] = 0
+        for d in dense:
+            d["k"].zero_()
+            d["v"].zero_()
+            d["g"] = d["l"] = 0
         torch.cuda.synchronize()
         log("[bench] reference GPU path: timing")
         t0 = time.perf_counter()
@@ -356,6 +517,24 @@ def main():
         log(f"[bench] CPU baseline: {result['cpu_baseline']}")
     else:
         result["cpu_baseline"] = None
+    del inputs
+    caches = None
+    torch.cuda.empty_cache()
+    if not args.no_aux and args.config == "c2":
+        aux = {}
+        for name in ("c3", "c5"):
+            log(f"[bench] aux {name}: steady state")
+            r = steady_state(name, dev)
+            aux[name] = {k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in r.items()}
+            log(f"[bench] aux {name}: {aux[name]}")
+        log("[bench] aux c5: fp8 vs bf16 quality")
+        aux["c5"]["quality"] = c5_quality(dev)
+        log(f"[bench] aux c5 quality: {aux['c5']['quality']}")
+        log("[bench] aux c4: memory path")
+        aux["c4"] = c4_memory_path(dev)
+        aux["c4"]["gather_gbps"] = result["gather_gbps"]
+        log(f"[bench] aux c4: {aux['c4']}")
+        result["aux"] = aux
     print(json.dumps(result), flush=True)
 
 

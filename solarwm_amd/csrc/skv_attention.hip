@@ -47,7 +47,8 @@ struct AttnArgs {
   int32_t slots[SKV_MAX_FRAMES];
 };
 
-constexpr int kBQ = 256;  // queries per workgroup (8 waves x 32)
+// Workgroups have NW = 4 or 8 waves (128 or 256 queries); the launcher picks the shape that
+// fills the 256 CUs best (8-wave groups halve the K/V bytes staged per query).
 
 // LDS holds each tile in MFMA operand order: one 1 KB block per A operand (64 lanes x 16 B),
 // lane L of the block at byte L*16.  K tile: 16 blocks (kb, s) = 32-key block x 16-channel
@@ -99,59 +100,38 @@ __device__ inline void store4<float>(float* p, float x0, float x1, float x2, flo
   *reinterpret_cast<f32x4*>(p) = f32x4{x0, x1, x2, x3};
 }
 
-// Stage one 64-key tile of K (or V^T) into a 16 KB LDS buffer: each wave writes 4 of the
-// 16 operand blocks.  bf16 pools use direct 16 B global->LDS loads (no registers); fp32 pools
-// (the C1 path, not performance critical) go through registers and are rounded to bf16.
-template <typename KT>
-struct TileLoader;
-
-template <>
-struct TileLoader<bf16> {
-  int64_t koff, voff;
-  __device__ void init(int w, int lane, int Tp) {
-    const int n = lane & 31, hh = lane >> 5;
-    // 8 waves: wave w stages K blocks 2w+j (kb = w>>2, s = (w&3)*2 + j) and V^T blocks
-    // 2w+j (db = w>>1, kb*2+s2 = (w&1)*2 + j)
-    koff = (int64_t)((w >> 2) * 32 + key_perm(n)) * kHeadDim + (w & 3) * 32 + hh * 8;
-    voff = (int64_t)((w >> 1) * 32 + n) * Tp + (w & 1) * 32 + hh * 8;
-  }
-  __device__ void issue_k(const bf16* kt, char* dst, int w) const {
-    dst += w * 2 * kBlockBytes;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(kt + koff + j * 16),
-                                       (lds_void_t*)(dst + j * kBlockBytes), 16, 0, 0);
-  }
-  __device__ void issue_v(const bf16* vt, char* dst, int w) const {
-    dst += w * 2 * kBlockBytes;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(vt + voff + j * 16),
-                                       (lds_void_t*)(dst + j * kBlockBytes), 16, 0, 0);
-  }
-};
-
-template <>
-struct TileLoader<float> {
+// Stage one 64-key tile of K (or V^T) into a 16 KB LDS buffer: wave w writes operand blocks
+// [w*kBpw, (w+1)*kBpw) of the 16.  K block b = (kb = b/8, k-step s = b%8); V^T block
+// b = (db = b/4, kb*2+s2 = b%4).  bf16 pools use direct 16 B global->LDS loads (no registers);
+// fp32 pools (the C1 path, not performance critical) go through registers and are rounded.
+template <int NW, typename KT>
+struct TileLoader {
+  static constexpr int kBpw = 16 / NW;
   int64_t koff, voff;
   int lane16;
   __device__ void init(int w, int lane, int Tp) {
     lane16 = lane * 16;
     const int n = lane & 31, hh = lane >> 5;
-    koff = (int64_t)((w >> 2) * 32 + key_perm(n)) * kHeadDim + (w & 3) * 32 + hh * 8;
-    voff = (int64_t)((w >> 1) * 32 + n) * Tp + (w & 1) * 32 + hh * 8;
+    const int b0 = w * kBpw;
+    koff = (int64_t)((b0 >> 3) * 32 + key_perm(n)) * kHeadDim + (b0 & 7) * 16 + hh * 8;
+    voff = (int64_t)((b0 >> 2) * 32 + n) * Tp + (b0 & 3) * 16 + hh * 8;
   }
-  __device__ void issue_k(const float* kt, char* dst, int w) const {
-    dst += w * 2 * kBlockBytes + lane16;
+  __device__ void issue_k(const KT* kt, char* dst, int w) const {
+    dst += w * kBpw * kBlockBytes;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<bf16x8*>(dst + j * kBlockBytes) = Vec8<float>::load(kt + koff + j * 16).to_bf16();
+    for (int j = 0; j < kBpw; ++j) stage(kt + koff + j * 16, dst + j * kBlockBytes);
   }
-  __device__ void issue_v(const float* vt, char* dst, int w) const {
-    dst += w * 2 * kBlockBytes + lane16;
+  __device__ void issue_v(const KT* vt, char* dst, int w) const {
+    dst += w * kBpw * kBlockBytes;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<bf16x8*>(dst + j * kBlockBytes) = Vec8<float>::load(vt + voff + j * 16).to_bf16();
+    for (int j = 0; j < kBpw; ++j) stage(vt + voff + j * 16, dst + j * kBlockBytes);
+  }
+  __device__ void stage(const KT* src, char* block) const {
+    if constexpr (sizeof(KT) == 2) {
+      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)block, 16, 0, 0);
+    } else {
+      *reinterpret_cast<bf16x8*>(block + lane16) = Vec8<KT>::load(src).to_bf16();
+    }
   }
 };
 
@@ -180,9 +160,10 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
     }
 }
 
-template <typename QT, typename KT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int NW, typename QT, typename KT>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
+  constexpr int kBQ = NW * 32;
   // LDS: K tiles in [0, 32 KB) (two buffers), V^T tiles in [32 KB, 64 KB) (two buffers).
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr int kHalf = 16 * kBlockBytes;
@@ -235,7 +216,7 @@ void attn_kernel(AttnArgs a) {
   const KT* kpool = static_cast<const KT*>(a.kpool);
   const KT* vpool = static_cast<const KT*>(a.vpool);
   const int64_t kbh = (int64_t)(b * a.H + h) * a.Tp * kHeadDim;  // (b,h) offset inside a slot
-  TileLoader<KT> loader;
+  TileLoader<NW, KT> loader;
   loader.init(w, lane, a.Tp);
   auto tile_base = [&](int tau) -> int64_t {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
@@ -277,8 +258,8 @@ void attn_kernel(AttnArgs a) {
     loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
     if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-      *reinterpret_cast<bf16x8*>(vb_lds(1) + (tid + 512 * r) * 16) = Vec8<bf16>::zero().to_bf16();
+    for (int r = 0; r < 16 / NW; ++r)
+      *reinterpret_cast<bf16x8*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = Vec8<bf16>::zero().to_bf16();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     qk_tile(kb_lds(0) + lane16, qf, s_cur);
@@ -458,9 +439,11 @@ __device__ inline fp8x8 pack_fp8x8(const float* v) {
   return (fp8x8)(((unsigned long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
-template <typename QT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int NW, typename QT>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fp8_kernel(AttnArgs a) {
+  constexpr int kBQ = NW * 32;
+  constexpr int kDpw = 8 / NW;  // double blocks per wave per tile
   // LDS: K tiles [0, 16 KB) (two buffers), V^T tiles [16 KB, 32 KB) (two buffers).
   extern __shared__ __attribute__((aligned(16))) char lds[];
   int logical;
@@ -540,19 +523,24 @@ void attn_fp8_kernel(AttnArgs a) {
     key0 = j * a.T + tok0;
     return (tok0 + kTile > a.T) || (key0 + kTile > lim_lo);
   };
-  // wave w stages K double block w (kb = w>>2, steps 2(w&3), 2(w&3)+1) and V^T double block w
-  // (db = w>>1, kb = w&1)
-  const int64_t koff = (int64_t)((w >> 2) * 32 + key_perm8(n)) * kHeadDim + hh * 64 + (w & 3) * 16;
-  const int64_t voff = (int64_t)((w >> 1) * 32 + n) * a.Tp + (w & 1) * 32 + hh * 16;
+  // wave w stages K double blocks b = w*kDpw + j (kb = b>>2, steps 2(b&3), 2(b&3)+1) and V^T
+  // double blocks b (db = b>>1, kb = b&1)
+  const int b0 = w * kDpw;
+  const int64_t koff = (int64_t)((b0 >> 2) * 32 + key_perm8(n)) * kHeadDim + hh * 64 + (b0 & 3) * 16;
+  const int64_t voff = (int64_t)((b0 >> 1) * 32 + n) * a.Tp + (b0 & 1) * 32 + hh * 16;
   auto kb_lds = [&](int i) { return lds + i * kTile8; };
   auto vb_lds = [&](int i) { return lds + (2 + i) * kTile8; };
   auto issue_k = [&](int tau, char* dst) {
-    __builtin_amdgcn_global_load_lds((glb_void_t*)(ktile(tau) + koff),
-                                     (lds_void_t*)(dst + w * kBlock8), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kDpw; ++j)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(ktile(tau) + koff + j * 16),
+                                       (lds_void_t*)(dst + (b0 + j) * kBlock8), 16, 0, 0);
   };
   auto issue_v = [&](int tau, char* dst) {
-    __builtin_amdgcn_global_load_lds((glb_void_t*)(vtile(tau) + voff),
-                                     (lds_void_t*)(dst + w * kBlock8), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kDpw; ++j)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(vtile(tau) + voff + j * 32),
+                                       (lds_void_t*)(dst + (b0 + j) * kBlock8), 16, 0, 0);
   };
 
   // G maps the largest probability (<= 2^kStale8) times the largest V scale of the window
@@ -597,7 +585,9 @@ void attn_fp8_kernel(AttnArgs a) {
   if (ntau > 0) {
     issue_k(0, kb_lds(0));
     if (ntau > 1) issue_k(1, kb_lds(1));
-    *reinterpret_cast<u32x4*>(vb_lds(1) + tid * 16) = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int r = 0; r < 8 / NW; ++r)
+      *reinterpret_cast<u32x4*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     qk(kb_lds(0) + lane16, s_cur);
@@ -709,6 +699,40 @@ void attn_fp8_kernel(AttnArgs a) {
 
 using namespace skv;
 
+static int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+template <int NW>
+static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, hipStream_t s) {
+  dim3 grid(a.n_wg), block(NW * 64);
+  if (pool_dtype == SKV_FP8_E4M3) {
+    if (q_dtype == SKV_BF16)
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 4 * kTile8, s, a);
+    else
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 4 * kTile8, s, a);
+    return;
+  }
+  const size_t lds_bytes = 2 * kTileBytes;
+  if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16>), grid, block, lds_bytes, s, a);
+  else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, float>), grid, block, lds_bytes, s, a);
+  else if (q_dtype == SKV_F32 && pool_dtype == SKV_BF16)
+    hipLaunchKernelGGL((attn_kernel<NW, float, bf16>), grid, block, lds_bytes, s, a);
+  else
+    hipLaunchKernelGGL((attn_kernel<NW, float, float>), grid, block, lds_bytes, s, a);
+}
+
 extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
                              int64_t q_sh, const void* k_pool, const void* v_pool,
                              const float* k_scale, const float* v_scale, int pool_dtype,
@@ -790,7 +814,18 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
   a.Tp = padded_tokens(frame_tokens);
   a.n_frames = n_frames;
   a.ntiles_f = a.Tp / kTile;
-  a.n_qtiles = (q_len + kBQ - 1) / kBQ;
+  // Workgroup shape: 8 waves (256 queries, 1 workgroup per CU) stages half the K/V bytes per
+  // query of 4 waves (128 queries, 2 per CU) and measured ~4% faster per FLOP, but a grid that
+  // barely spills into a second round of CUs leaves most of the chip idle; pick the shape with
+  // the better CU fill (ties and near-ties go to 8 waves).
+  const int n_cu = cu_count();
+  auto fill = [&](int bq, int per_cu) {
+    const int64_t wg = (int64_t)((q_len + bq - 1) / bq) * heads * batch;
+    const int64_t slots = (int64_t)n_cu * per_cu;
+    return (double)wg / (double)(((wg + slots - 1) / slots) * slots);
+  };
+  const int nw = fill(256, 1) * 1.04 >= fill(128, 2) ? 8 : 4;
+  a.n_qtiles = (q_len + nw * 32 - 1) / (nw * 32);
   a.n_wg = a.n_qtiles * heads * batch;
   a.slot_stride = (int64_t)batch * heads * a.Tp * kHeadDim;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
@@ -806,21 +841,10 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
     a.slots[j] = frame_slots[j];
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(a.n_wg), block(512);
-  const size_t lds_bytes = 2 * kTileBytes;
-  if (pool_dtype == SKV_FP8_E4M3) {
-    if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_fp8_kernel<bf16>), grid, block, 4 * kTile8, s, a);
-    else
-      hipLaunchKernelGGL((attn_fp8_kernel<float>), grid, block, 4 * kTile8, s, a);
-  } else if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<bf16, bf16>), grid, block, lds_bytes, s, a);
-  else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
-    hipLaunchKernelGGL((attn_kernel<bf16, float>), grid, block, lds_bytes, s, a);
-  else if (q_dtype == SKV_F32 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<float, bf16>), grid, block, lds_bytes, s, a);
+  if (nw == 8)
+    launch<8>(a, q_dtype, pool_dtype, s);
   else
-    hipLaunchKernelGGL((attn_kernel<float, float>), grid, block, lds_bytes, s, a);
+    launch<4>(a, q_dtype, pool_dtype, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("skv_attention: launch failed: %s", hipGetErrorString(e));

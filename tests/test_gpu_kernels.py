@@ -99,7 +99,8 @@ def _pool_from(k, v, T, dtype, device, perm_seed=0):
     "B,H,Lq,T,n,dtype",
     [(1, 2, 128, 64, 2, torch.bfloat16), (1, 3, 200, 100, 5, torch.bfloat16),
      (2, 2, 390, 390, 4, torch.float32), (1, 12, 1170, 390, 6, torch.bfloat16),
-     (1, 1, 37, 1560, 3, torch.bfloat16), (1, 4, 1, 70, 2, torch.bfloat16)],
+     (1, 1, 37, 1560, 3, torch.bfloat16), (1, 4, 1, 70, 2, torch.bfloat16),
+     (1, 24, 2640, 880, 3, torch.bfloat16)],  # last: config-3 shape, runs 4-wave workgroups
 )
 def test_attention_frames_vs_oracle(gpu, B, H, Lq, T, n, dtype):
     _say("attention", B, H, Lq, T, n, dtype)
@@ -229,7 +230,8 @@ def _outlier_kv(shape, seed):
     return x.to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("B,H,Lq,T,n", [(4, 3, 390, 390, 21), (1, 12, 1170, 390, 6), (2, 1, 37, 1560, 2)])
+@pytest.mark.parametrize("B,H,Lq,T,n", [(4, 3, 390, 390, 21), (1, 12, 1170, 390, 6), (2, 1, 37, 1560, 2),
+                                        (1, 24, 2640, 880, 7)])
 def test_fp8_attention_unit_scale_vs_bf16_oracle(gpu, B, H, Lq, T, n):
     """N(0,1) K/V: the fp8 cache path meets the north-star fp8 bar (stated for the 21-frame
     config-5 window) against the bf16 oracle; windows here hold 2340 to 8190 keys (a 1170-key
@@ -244,7 +246,8 @@ def test_fp8_attention_unit_scale_vs_bf16_oracle(gpu, B, H, Lq, T, n):
     out = kernels.attention_frames(q.to(gpu), kpool, vpool, slots, frame_tokens=T, kscale=ks,
                                    vscale=vs)
     torch.cuda.synchronize()
-    assert_attn_close(out, ref.attention(q, k, v), FP8_MAX_ABS, FP8_MEAN_ABS)
+    want = ref.attention(q, k, v, compute_dtype=torch.float32)
+    assert_attn_close(out, want, FP8_MAX_ABS, FP8_MEAN_ABS)
 
 
 def assert_fp8_close_normalised(got, q, k, v, T, mask=None):
