@@ -42,6 +42,11 @@ PASSES = ["none"] * 4 + ["commit"]  # stage2.py:683-760: NFE4 then a t=0 commit 
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per steady-state attention launch (Lq 4680 x Lk 32760, H12) measured with rocprofv3
+# on `bench.py --probe`: FETCH_SIZE x2.0 (341.40 MB) + WRITE_SIZE x1.0 (14.38 MB); the scale
+# factors are what the same counters read for a 1 GiB device copy.  Counters cannot be read
+# from inside the process, so the figure is recorded here for the config it was measured on.
+ATTN_TRAFFIC_BYTES = {"c2": 355.78e6}
 
 
 def log(*a):
@@ -466,7 +471,8 @@ def main():
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": ATTN_TRAFFIC_BYTES.get(args.config),
+            "traffic_per": "steady-state launch (Lk = cache window), rocprofv3 FETCH_SIZE + WRITE_SIZE",
             "launches": st["attn_launches"],
             "avg_launch_ms": round(st["attn_avg_ms"], 4),
             "steady_state": {"Lk": cfg["cap_f"] * T, "avg_launch_ms": round(st["attn_steady_ms"], 4),

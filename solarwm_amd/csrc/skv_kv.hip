@@ -25,13 +25,26 @@ struct AppendArgs {
   int32_t slots[SKV_MAX_APPEND_FRAMES];
 };
 
-// LDS tile for the V transpose: 64 tokens x 128 channels, rows padded by 8 elements.
-constexpr int kVtRow = kHeadDim + 8;
+// 8x8 transpose of 16-bit elements held as 8 rows of 4 x u32 (row r = token, word c/2 half c%2
+// = channel c): out[c].word[w] = (in[2w] half c, in[2w+1] half c).
+__device__ inline void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t a = in[2 * w][c >> 1], b = in[2 * w + 1][c >> 1];
+      // v_perm_b32 selector: bytes 0-3 come from the second operand, 4-7 from the first
+      out[c][w] = (c & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)   // hi halves
+                          : __builtin_amdgcn_perm(b, a, 0x05040100u);  // lo halves
+    }
+}
 
-// grid.x = n_frames * B * H * ntiles (ntiles = Tp / 64), block = 256.
+// grid.x = n_frames * B * H * ntiles (ntiles = Tp / 64), block = 256.  Threads 0-127 copy the
+// 64 K rows (16 B vectors); threads 128-255 each move one 8-token x 8-channel block of V,
+// transposed in registers, so V^T rows are written as 16 B vectors without an LDS stage.
+// Rows past T are written as zeros.
 template <typename E>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
-  __shared__ E vt[kTile * kVtRow];
   int wg = blockIdx.x;
   const int t = wg % a.ntiles;
   wg /= a.ntiles;
@@ -42,38 +55,56 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const int64_t slot = a.slots[f];
   const int tid = threadIdx.x;
   const int tok0 = t * kTile;
-
-  const E* ks = static_cast<const E*>(a.ksrc);
-  const E* vs = static_cast<const E*>(a.vsrc);
   const int64_t src_base = (int64_t)b * a.s_sb + (int64_t)h * a.s_sh +
                            (int64_t)(a.src_frame0 + f) * a.T * a.s_st;
-  E* kp = static_cast<E*>(a.kpool) + slot * a.slot_stride +
-          ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
-  E* vp = static_cast<E*>(a.vpool) + slot * a.slot_stride + (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
-
-  // 64 rows x 16 vec8 = 1024 vec8 per tile, 4 per thread.  Rows past T are zero padding.
+  if (tid < 128) {
+    const E* ks = static_cast<const E*>(a.ksrc);
+    E* kp = static_cast<E*>(a.kpool) + slot * a.slot_stride +
+            ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+    // 64 rows x 16 vec8 = 1024 vec8, 8 per thread
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int c = tid + 256 * r;
-    const int row = c >> 4, col = (c & 15) * 8;
-    const bool live = tok0 + row < a.T;
-    const int64_t so = src_base + (int64_t)(tok0 + row) * a.s_st + col;
-    Vec8<E> kv = live ? Vec8<E>::load(ks + so) : Vec8<E>::zero();
-    Vec8<E> vv = live ? Vec8<E>::load(vs + so) : Vec8<E>::zero();
-    kv.store(kp + row * kHeadDim + col);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vt[row * kVtRow + col + i] = vv.get(i);
+    for (int r = 0; r < 8; ++r) {
+      const int c = tid + 128 * r;
+      const int row = c >> 4, col = (c & 15) * 8;
+      const bool live = tok0 + row < a.T;
+      Vec8<E> kv = live ? Vec8<E>::load(ks + src_base + (int64_t)(tok0 + row) * a.s_st + col)
+                        : Vec8<E>::zero();
+      kv.store(kp + row * kHeadDim + col);
+    }
+    return;
   }
-  __syncthreads();
-  // Transposed write: 128 channel rows x 8 vec8 (64 tokens) = 1024 vec8, 4 per thread.
+  const E* vs = static_cast<const E*>(a.vsrc);
+  E* vp = static_cast<E*>(a.vpool) + slot * a.slot_stride +
+          (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
+  const int i = tid - 128;
+  const int db = i & 15, tb = i >> 4;  // channels db*8.., tokens tb*8..
+  if constexpr (sizeof(E) == 2) {
+    u32x4 in[8], out[8];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int c = tid + 256 * r;
-    const int d = c >> 3, tc = (c & 7) * 8;
-    Vec8<E> o;
+    for (int r = 0; r < 8; ++r) {
+      const int tok = tok0 + tb * 8 + r;
+      in[r] = tok < a.T ? *reinterpret_cast<const u32x4*>(vs + src_base + (int64_t)tok * a.s_st + db * 8)
+                        : u32x4{0u, 0u, 0u, 0u};
+    }
+    transpose8x8_b16(in, out);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o.set(i, vt[(tc + i) * kVtRow + d]);
-    o.store(vp + (int64_t)d * a.Tp + tc);
+    for (int c = 0; c < 8; ++c)
+      *reinterpret_cast<u32x4*>(vp + (int64_t)(db * 8 + c) * a.Tp + tb * 8) = out[c];
+  } else {
+    Vec8<E> in[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int tok = tok0 + tb * 8 + r;
+      in[r] = tok < a.T ? Vec8<E>::load(vs + src_base + (int64_t)tok * a.s_st + db * 8)
+                        : Vec8<E>::zero();
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      Vec8<E> o;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) o.set(r, in[r].get(c));
+      o.store(vp + (int64_t)(db * 8 + c) * a.Tp + tb * 8);
+    }
   }
 }
 
