@@ -7,20 +7,28 @@
 // sink|local concatenation, the eviction memmove and the memory-bank gather of the reference
 // all become addressing: nothing is copied before attention.
 //
-// Work decomposition (one workgroup = 8 waves = 256 queries of one (batch, head)):
+// Work decomposition (one workgroup = NW waves = 32*NW queries of one (batch, head); NW = 8 or
+// 4, chosen per launch by how well the grid fills the CUs):
 //   * each wave owns 32 queries and keeps them in registers as the B operand of
 //     v_mfma_f32_32x32x16_bf16, computing S^T = K Q^T so that one lane holds one query's
 //     scores; the softmax row statistics then need one lane-pair swap (v_permlane32_swap);
-//   * 64-key K and V^T tiles are staged in LDS and shared by the 8 waves, in MFMA operand
-//     order (see kBlockBytes) by direct global->LDS loads; K is staged two tiles ahead and V
-//     one tile ahead of their use, so every load has a full iteration to land;
+//   * the row max is not recomputed per tile: probabilities are formed as
+//     exp2(s * scale * log2(e) - m) with the running max m (one fma, one v_exp_f32, one add
+//     and half a bf16 pack per score), and a tile whose probabilities could exceed 2^8
+//     (detected from the lane's partial sum) takes a rare path that raises the max to the
+//     tile's true max, recomputes the tile and rescales O;
+//   * 64-key K and V^T tiles are staged in LDS and shared by the waves, in MFMA operand order
+//     (see kBlockBytes), by buffer loads straight into LDS: one descriptor per tile, the
+//     lane's byte offset in a VGPR that never changes, the block offset in an SGPR.  K is
+//     staged two tiles ahead and V one tile ahead of their use;
 //   * the K rows of each 32-key block are loaded in the permuted order key_perm(), which makes
 //     the fp32 S^T accumulator of a lane hold, per 8 registers, 8 consecutive keys — exactly
 //     the bf16x8 B operand (P^T) of the PV product; V is stored transposed in the pool so
 //     its A operand (V^T rows) is one 16 B LDS read;
 //   * iteration tau runs three independent streams — QK(tau+1), softmax(tau), PV(tau-1) —
-//     interleaved by hand (one MFMA, then a slice of the softmax) so the matrix core and the
-//     VALU work at the same time;
+//     interleaved by hand (one MFMA, then one probability) so the matrix core and the VALU
+//     work at the same time; the loop is unrolled twice so score and probability registers
+//     alternate between two sets instead of being copied;
 //   * tiles never straddle frames (frames are padded to 64 tokens); padding keys and keys
 //     beyond a query's chunk-causal limit get -inf, decided per tile: full tiles skip the
 //     mask, tiles past every query's limit are not visited.
@@ -107,31 +115,55 @@ __device__ inline void store4<float>(float* p, float x0, float x1, float x2, flo
 template <int NW, typename KT>
 struct TileLoader {
   static constexpr int kBpw = 16 / NW;
-  int64_t koff, voff;
+  int64_t koff, voff;   // element offsets of this lane's first block (register path)
+  uint32_t klane, vlane;  // byte offsets of this lane inside a block (buffer path)
+  int wu, Tp;
   int lane16;
-  __device__ void init(int w, int lane, int Tp) {
+  __device__ void init(int w, int lane, int Tp_) {
     lane16 = lane * 16;
+    Tp = Tp_;
+    wu = __builtin_amdgcn_readfirstlane(w);
     const int n = lane & 31, hh = lane >> 5;
     const int b0 = w * kBpw;
     koff = (int64_t)((b0 >> 3) * 32 + key_perm(n)) * kHeadDim + (b0 & 7) * 16 + hh * 8;
     voff = (int64_t)((b0 >> 2) * 32 + n) * Tp + (b0 & 3) * 16 + hh * 8;
+    klane = (uint32_t)(key_perm(n) * kHeadDim + hh * 8) * 2u;
+    vlane = (uint32_t)(n * Tp + hh * 8) * 2u;
   }
+  // bf16 pools: one buffer descriptor per tile (base = the tile's first element), the lane's
+  // byte offset in a VGPR that never changes, the block's offset in an SGPR.
   __device__ void issue_k(const KT* kt, char* dst, int w) const {
-    dst += w * kBpw * kBlockBytes;
+    if constexpr (sizeof(KT) == 2) {
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)kt, (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < kBpw; ++j) stage(kt + koff + j * 16, dst + j * kBlockBytes);
+      for (int j = 0; j < kBpw; ++j) {
+        const int b = wu * kBpw + j;
+        const uint32_t so = (uint32_t)((b >> 3) * 32 * kHeadDim + (b & 7) * 16) * 2u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + b * kBlockBytes), 16, klane, so, 0, 0);
+      }
+    } else {
+      dst += w * kBpw * kBlockBytes;
+#pragma unroll
+      for (int j = 0; j < kBpw; ++j) stage(kt + koff + j * 16, dst + j * kBlockBytes);
+    }
   }
   __device__ void issue_v(const KT* vt, char* dst, int w) const {
-    dst += w * kBpw * kBlockBytes;
+    if constexpr (sizeof(KT) == 2) {
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)vt, (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < kBpw; ++j) stage(vt + voff + j * 16, dst + j * kBlockBytes);
+      for (int j = 0; j < kBpw; ++j) {
+        const int b = wu * kBpw + j;
+        const uint32_t so = (uint32_t)((b >> 2) * 32 * Tp + (b & 3) * 16) * 2u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + b * kBlockBytes), 16, vlane, so, 0, 0);
+      }
+    } else {
+      dst += w * kBpw * kBlockBytes;
+#pragma unroll
+      for (int j = 0; j < kBpw; ++j) stage(vt + voff + j * 16, dst + j * kBlockBytes);
+    }
   }
   __device__ void stage(const KT* src, char* block) const {
-    if constexpr (sizeof(KT) == 2) {
-      __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)block, 16, 0, 0);
-    } else {
-      *reinterpret_cast<bf16x8*>(block + lane16) = Vec8<KT>::load(src).to_bf16();
-    }
+    *reinterpret_cast<bf16x8*>(block + lane16) = Vec8<KT>::load(src).to_bf16();
   }
 };
 
@@ -239,7 +271,11 @@ void attn_kernel(AttnArgs a) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
-  constexpr float kStale = 8.0f;
+  // The fast path assumes a tile needs no new row max: p = exp2(s * c2 - m).  A lane whose
+  // partial probability sum exceeds 2^kStale (or is not finite), or whose running max is
+  // still -inf, sends the wave to the rare path, which raises the max to the tile's true max,
+  // recomputes the tile's probabilities and rescales O and l.
+  constexpr float kMaxPart = 256.0f;  // 2^kStale, kStale = 8
   float m_run = -INFINITY, l_run = 0.f;
   const float c2 = a.scale_log2;
   const int lane16 = lane * 16;
@@ -248,12 +284,15 @@ void attn_kernel(AttnArgs a) {
   auto vb_lds = [&](int i) { return lds + (2 + i) * kHalf; };
 
   // Prologue: K(0), K(1) resident; V buffer 1 zeroed so PV(-1) of iteration 0 adds nothing.
-  f32x16 s_cur[2];
-  bf16x8 pprev[2][2];
+  // Score and probability registers ping-pong between two sets (A, B) across iterations, so no
+  // loop-carried copy is needed.
+  f32x16 sA[2], sB[2];
+  bf16x8 pA[2][2], pB[2][2];
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y) pprev[x][y] = Vec8<bf16>::zero().to_bf16();
+    for (int y = 0; y < 2; ++y) pA[x][y] = Vec8<bf16>::zero().to_bf16();
+  f32x16 (&s_cur)[2] = sA;
   if (ntau > 0) {
     loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
     if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
@@ -272,20 +311,20 @@ void attn_kernel(AttnArgs a) {
   // ~130 VALU ops are interleaved by hand (one MFMA, then a slice of the softmax) so the
   // matrix core and the VALU work at the same time.  Resident: K(tau+1), V(tau-1); in flight:
   // K(tau+2) into K(tau)'s buffer, V(tau) into V(tau-2)'s buffer.
-  for (int tau = 0; tau < ntau; ++tau) {
-    const int cb = tau & 1;
+  // cb = tau & 1, passed as a literal so buffer addresses fold into immediate offsets
+  f32x16 zero16;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zero16[i] = 0.f;
+  auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
+                  bf16x8 (&pprev)[2][2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
     if (tau + 2 < ntau) loader.issue_k(kpool + tile_base(tau + 2), kb_lds(cb), w);
     loader.issue_v(vpool + vtile_base(tau), vb_lds(cb), w);
     const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
     const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
 
-    f32x16 s_nxt[2];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { s_nxt[0][i] = 0.f; s_nxt[1][i] = 0.f; }
-    float mx0 = -INFINITY, mx1 = -INFINITY, mx = 0.f, alpha = 1.f, m_use = 0.f;
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ls[4] = {0.f, 0.f, 0.f, 0.f};
     float pf[32];
-    bf16x8 pb[2][2];
     // operand of MFMA step i: even i -> QK step i/2 (k = i/4, kb = (i/2)&1), odd i -> PV step
     // i/2 (db = (i/2)/4, kb = ((i/2)>>1)&1, s2 = (i/2)&1)
     auto operand = [&](int i) -> bf16x8 {
@@ -297,6 +336,15 @@ void attn_kernel(AttnArgs a) {
       const int db = st >> 2, kbb = (st >> 1) & 1, s2 = st & 1;
       return *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
     };
+    auto prob = [&](int e, float mu) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -mu));
+      pf[e] = p;
+      ls[e & 3] += p;
+      if (e & 1) {
+        pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
+        pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
+      }
+    };
     bf16x8 opq[4];
 #pragma unroll
     for (int i = 0; i < 3; ++i) opq[i] = operand(i);
@@ -306,68 +354,69 @@ void attn_kernel(AttnArgs a) {
       const int st = i >> 1;
       if ((i & 1) == 0) {
         const int k = st >> 1, kbb = st & 1;
-        s_nxt[kbb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], qf[k], s_nxt[kbb], 0, 0, 0);
+        s_nxt[kbb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], qf[k], k == 0 ? zero16 : s_nxt[kbb], 0, 0, 0);
       } else {
         const int db = st >> 2, kbb = (st >> 1) & 1, s2 = st & 1;
         oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], pprev[kbb][s2], oacc[db], 0, 0, 0);
       }
-      // softmax slice i of tile tau
-      if (i == 0) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx0 = fmaxf(mx0, s_cur[0][e]);
-      } else if (i == 1) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx1 = fmaxf(mx1, s_cur[1][e]);
-      } else if (i == 2) {
-        mx = pair_max(fmaxf(mx0, mx1)) * c2;
-        const bool raise = mx > m_run + kStale;
-        const float m_new = raise ? mx : m_run;
-        alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
-        m_run = m_new;
-        m_use = m_new == -INFINITY ? 0.f : m_new;
-      } else {
-        // slices 3..31 compute the 32 probabilities: slice i handles elements [e0, e1)
-        const int e0 = ((i - 3) * 32) / 29, e1 = ((i - 2) * 32) / 29;
-#pragma unroll
-        for (int e = e0; e < e1; ++e) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
-          asm volatile("" ::"v"(p));  // keep this slice's exp next to its MFMA
-          pf[e] = p;
-          ls[e & 3] += p;
-          asm volatile("" ::"v"(ls[e & 3]));
-          if (e & 1) {
-            pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
-            pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
-          }
-          if ((e & 7) == 7) asm volatile("" ::"v"(pb[e >> 4][(e >> 3) & 1]));
+      // softmax slice i of tile tau: probability i, assuming the tile needs no new max
+      {
+        const int e = i;
+        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
+        asm volatile("" ::"v"(p));  // keep this slice's exp next to its MFMA
+        pf[e] = p;
+        ls[e & 3] += p;
+        asm volatile("" ::"v"(ls[e & 3]));
+        if (e & 1) {
+          pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
+          pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
         }
+        if ((e & 7) == 7) asm volatile("" ::"v"(pb[e >> 4][(e >> 3) & 1]));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
-    if (__any(alpha != 1.0f)) {  // rare: some query's running max was raised
+    float lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    const bool need = !(lp <= kMaxPart) || m_run == -INFINITY;
+    if (__any(need)) {
+      // rare path: both key halves of a query take the same decision; raise the max of each
+      // such query to the tile's true max, recompute its probabilities, rescale O and l
+      const bool needq = pair_max(need ? 1.f : 0.f) > 0.f;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) mx = fmaxf(mx, s_cur[e >> 4][e & 15]);
+      mx = pair_max(mx) * c2;
+      const float m_new = needq ? fmaxf(m_run, mx) : m_run;
+      const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float mu = m_new == -INFINITY ? 0.f : m_new;  // = m_use for lanes kept
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ls[e] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) prob(e, mu);
+      lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+      m_run = m_new;
     }
+    l_run += lp;
     if (tau + 1 < ntau) {
       int tok0, key0;
       if (tile_needs_mask(tau + 1, tok0, key0)) mask_tile(s_nxt, hh, tok0, a.T, key0, lim_lane);
     }
-#pragma unroll
-    for (int kbb = 0; kbb < 2; ++kbb) s_cur[kbb] = s_nxt[kbb];
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int y = 0; y < 2; ++y) pprev[x][y] = pb[x][y];
     // K(tau+2) and V(tau) have landed; every wave is done with K(tau+1)'s and V(tau-1)'s
     // buffers (they take K(tau+3) and V(tau+1) next)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+  int tau = 0;
+  for (; tau + 1 < ntau; tau += 2) {
+    step(tau, 0, sA, sB, pA, pB);
+    step(tau + 1, 1, sB, sA, pB, pA);
   }
   // Epilogue: PV(ntau-1).
-  if (ntau > 0) {
+  auto epilogue = [&](const bf16x8 (&pprev)[2][2]) __attribute__((always_inline)) {
     const char* vl = vb_lds((ntau - 1) & 1) + lane16;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -379,6 +428,12 @@ void attn_kernel(AttnArgs a) {
               *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
           oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pprev[kbb][s2], oacc[db], 0, 0, 0);
         }
+  };
+  if (tau < ntau) {
+    step(tau, 0, sA, sB, pA, pB);
+    epilogue(pB);
+  } else if (ntau > 0) {
+    epilogue(pA);
   }
 
   const float l_tot = pair_sum(l_run);

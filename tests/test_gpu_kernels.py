@@ -127,6 +127,26 @@ def test_attention_sharp_and_scaled_logits(gpu):
         assert_attn_close(out, ref.attention(q, k, v, softmax_scale=scale))
 
 
+def test_attention_late_max_for_some_queries(gpu):
+    """Row maxima that jump late in the window for a few queries only, so inside one wave some
+    lanes keep their probabilities and others raise their max and recompute the tile."""
+    T, n = 96, 8
+    q = _rand((1, 320, 2, 128), 21, torch.float32)
+    k = _rand((1, n * T, 2, 128), 22, torch.float32)
+    v = _rand((1, n * T, 2, 128), 23, torch.float32)
+    g = torch.Generator().manual_seed(24)
+    picks = torch.randperm(320, generator=g)[:20]
+    for j, qi in enumerate(picks.tolist()):
+        key = (n - 1 - j % 3) * T + 5 * j % T  # keys in the last three frames
+        # logit ~20 log2 units above the others: the partial sum crosses 2^8
+        k[0, key, j % 2] = 0.5 * k[0, key, j % 2] + 1.2 * q[0, qi, j % 2]
+    q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    kpool, vpool, slots = _pool_from(k, v, T, torch.bfloat16, gpu)
+    out = kernels.attention_frames(q.to(gpu), kpool, vpool, slots, frame_tokens=T)
+    torch.cuda.synchronize()
+    assert_attn_close(out, ref.attention(q, k, v))
+
+
 @pytest.mark.parametrize("clean,noisy,T,per_block", [(2, 1, 100, 1), (3, 3, 64, 3), (0, 3, 50, 3),
                                                       (6, 3, 130, 3)])
 def test_chunk_causal_vs_oracle_mask(gpu, clean, noisy, T, per_block):
