@@ -43,10 +43,10 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 HBM_PEAK_GBPS = 8000.0
 # HBM bytes per steady-state attention launch (Lq 4680 x Lk 32760, H12) measured with rocprofv3
-# on `bench.py --probe`: FETCH_SIZE x2.0 (341.40 MB) + WRITE_SIZE x1.0 (14.38 MB); the scale
+# on `bench.py --probe`: FETCH_SIZE x2.0 (341.52 MB) + WRITE_SIZE x1.0 (14.38 MB); the scale
 # factors are what the same counters read for a 1 GiB device copy.  Counters cannot be read
 # from inside the process, so the figure is recorded here for the config it was measured on.
-ATTN_TRAFFIC_BYTES = {"c2": 355.78e6}
+ATTN_TRAFFIC_BYTES = {"c2": 355.89e6}
 
 
 def log(*a):
