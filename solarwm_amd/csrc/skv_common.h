@@ -32,6 +32,15 @@ void clear_error();
 template <typename T>
 struct Vec8;
 
+// Streaming (nontemporal) 16 B accesses for data touched once per launch: the byte movers use
+// them so chunk sources, pool writes and gathered frames do not displace cached K/V tiles.
+__device__ inline u32x4 ld_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ inline void st_nt(void* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 template <>
 struct Vec8<bf16> {
   u32x4 r;
@@ -41,6 +50,12 @@ struct Vec8<bf16> {
     return v;
   }
   __device__ void store(bf16* p) const { *reinterpret_cast<u32x4*>(p) = r; }
+  __device__ static Vec8 load_nt(const bf16* p) {
+    Vec8 v;
+    v.r = ld_nt(p);
+    return v;
+  }
+  __device__ void store_nt(bf16* p) const { st_nt(p, r); }
   __device__ static Vec8 zero() {
     Vec8 v;
     v.r = u32x4{0u, 0u, 0u, 0u};
@@ -67,6 +82,16 @@ struct Vec8<float> {
   __device__ void store(float* p) const {
     *reinterpret_cast<f32x4*>(p) = a;
     *reinterpret_cast<f32x4*>(p + 4) = b;
+  }
+  __device__ static Vec8 load_nt(const float* p) {
+    Vec8 v;
+    v.a = __builtin_bit_cast(f32x4, ld_nt(p));
+    v.b = __builtin_bit_cast(f32x4, ld_nt(p + 4));
+    return v;
+  }
+  __device__ void store_nt(float* p) const {
+    st_nt(p, __builtin_bit_cast(u32x4, a));
+    st_nt(p + 4, __builtin_bit_cast(u32x4, b));
   }
   __device__ static Vec8 zero() {
     Vec8 v;

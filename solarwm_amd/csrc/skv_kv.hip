@@ -5,9 +5,9 @@
 // solar/backends/wan22/runtime/modeling/causal_model.py:1054-1080, :2881-2898).  Here a frame
 // is written once into a slot and never moved again; eviction is a slot-table update on the
 // host.  Both kernels are HBM-bound byte movers: one workgroup moves one 64-token tile of one
-// (frame, batch, head); K rows move as 16 B vectors, V is transposed through LDS so the pool
-// keeps V channel-major (tokens contiguous), which is what the attention kernel's PV product
-// reads.
+// (frame, batch, head); K rows move as 16 B vectors, V is transposed in registers, 8 tokens x 8
+// channels per thread, so the pool keeps V channel-major (tokens contiguous), which is what the
+// attention kernel's PV product reads.
 #include "skv_common.h"
 
 namespace skv {
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
       const bool live = tok0 + row < a.T;
       Vec8<E> kv = live ? Vec8<E>::load(ks + src_base + (int64_t)(tok0 + row) * a.s_st + col)
                         : Vec8<E>::zero();
-      kv.store(kp + row * kHeadDim + col);
+      kv.store_nt(kp + row * kHeadDim + col);
     }
     return;
   }
@@ -77,7 +77,9 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   E* vp = static_cast<E*>(a.vpool) + slot * a.slot_stride +
           (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
   const int i = tid - 128;
-  const int db = i & 15, tb = i >> 4;  // channels db*8.., tokens tb*8..
+  // tokens tb*8.., channels db*8..: each wave instruction covers 128 B of 8 token rows on the
+  // read side and 128 B of 8 V^T rows on the write side
+  const int tb = i & 7, db = i >> 3;
   if constexpr (sizeof(E) == 2) {
     u32x4 in[8], out[8];
 #pragma unroll
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     transpose8x8_b16(in, out);
 #pragma unroll
     for (int c = 0; c < 8; ++c)
-      *reinterpret_cast<u32x4*>(vp + (int64_t)(db * 8 + c) * a.Tp + tb * 8) = out[c];
+      st_nt(vp + (int64_t)(db * 8 + c) * a.Tp + tb * 8, out[c]);
   } else {
     Vec8<E> in[8];
 #pragma unroll
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
       Vec8<E> o;
 #pragma unroll
       for (int r = 0; r < 8; ++r) o.set(r, in[r].get(c));
-      o.store(vp + (int64_t)(db * 8 + c) * a.Tp + tb * 8);
+      o.store_nt(vp + (int64_t)(db * 8 + c) * a.Tp + tb * 8);
     }
   }
 }
@@ -204,9 +206,10 @@ struct GatherArgs {
 };
 
 // grid.x = n_frames * B * H * ntiles, block = 256; E is the raw element type of the pool.
+// Threads 0-127 copy the tile's K rows (16 B vectors); threads 128-255 each read an 8-channel x
+// 8-token block of V^T and write it transposed (8 token rows of 8 channels), in registers.
 template <typename E>
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
-  __shared__ E vt[kHeadDim * (kTile + 8)];
   int wg = blockIdx.x;
   const int t = wg % a.ntiles;
   wg /= a.ntiles;
@@ -217,38 +220,46 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
   const int64_t slot = a.slots[f];
   const int tid = threadIdx.x;
   const int tok0 = t * kTile;
-  constexpr int kRow = kTile + 8;
-
-  const E* kp = static_cast<const E*>(a.kpool) + slot * a.slot_stride +
-                ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+  const int64_t obase = (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)f * a.T * a.o_st;
+  if (tid < 128) {
+    const E* kp = static_cast<const E*>(a.kpool) + slot * a.slot_stride +
+                  ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+    E* ko = static_cast<E*>(a.kout) + obase;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int c = tid + 128 * r;
+      const int row = c >> 4, col = (c & 15) * 8;
+      if (tok0 + row < a.T)
+        Vec8<E>::load_nt(kp + row * kHeadDim + col).store_nt(ko + (int64_t)(tok0 + row) * a.o_st + col);
+    }
+    return;
+  }
   const E* vp = static_cast<const E*>(a.vpool) + slot * a.slot_stride +
                 (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
-  E* ko = static_cast<E*>(a.kout) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
-          (int64_t)f * a.T * a.o_st;
-  E* vo = static_cast<E*>(a.vout) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
-          (int64_t)f * a.T * a.o_st;
-
-  // V^T tile (128 channels x 64 tokens) -> LDS
+  E* vo = static_cast<E*>(a.vout) + obase;
+  const int i = tid - 128;
+  const int tb = i & 7, db = i >> 3;  // tokens tb*8.., channels db*8..
+  const int tokb = tok0 + tb * 8;
+  if constexpr (sizeof(E) == 2) {
+    u32x4 in[8], out[8];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int c = tid + 256 * r;
-    const int d = c >> 3, tc = (c & 7) * 8;
-    Vec8<E> v = Vec8<E>::load(vp + (int64_t)d * a.Tp + tc);
+    for (int r = 0; r < 8; ++r)
+      in[r] = ld_nt(vp + (int64_t)(db * 8 + r) * a.Tp + tb * 8);
+    transpose8x8_b16(in, out);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vt[d * kRow + tc + i] = v.get(i);
-  }
-  __syncthreads();
+    for (int c = 0; c < 8; ++c)
+      if (tokb + c < a.T)
+        st_nt(vo + (int64_t)(tokb + c) * a.o_st + db * 8, out[c]);
+  } else {
+    Vec8<E> in[8];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int c = tid + 256 * r;
-    const int row = c >> 4, col = (c & 15) * 8;
-    if (tok0 + row < a.T) {
-      const int64_t oo = (int64_t)(tok0 + row) * a.o_st + col;
-      Vec8<E>::load(kp + row * kHeadDim + col).store(ko + oo);
+    for (int r = 0; r < 8; ++r) in[r] = Vec8<E>::load_nt(vp + (int64_t)(db * 8 + r) * a.Tp + tb * 8);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
       Vec8<E> o;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o.set(i, vt[(col + i) * kRow + row]);
-      o.store(vo + oo);
+      for (int r = 0; r < 8; ++r) o.set(r, in[r].get(c));
+      if (tokb + c < a.T) o.store_nt(vo + (int64_t)(tokb + c) * a.o_st + db * 8);
     }
   }
 }

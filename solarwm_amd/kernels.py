@@ -145,7 +145,7 @@ def _scales(kpool, kscale, vscale):
     return kscale.data_ptr(), vscale.data_ptr()
 
 
-def append_frames(
+def prepare_append(
     k_new: torch.Tensor,
     v_new: torch.Tensor,
     kpool: torch.Tensor,
@@ -156,8 +156,9 @@ def append_frames(
     src_frame0: int = 0,
     kscale: torch.Tensor | None = None,
     vscale: torch.Tensor | None = None,
-) -> None:
-    """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``."""
+):
+    """Validate an append once and return a zero-argument launcher that enqueues it on the stream
+    current now (repeated launches skip the Python-side checks)."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("k_new", k_new)
@@ -176,20 +177,41 @@ def append_frames(
         raise ValueError("k_new and pools must be on the same device")
     ks, vs = _scales(kpool, kscale, vscale)
     slots = _lib.int32_array(dst_slots)
-    t0 = _tic()
-    _lib.check(
-        "skv_append",
-        lib.skv_append(
-            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
-            kpool.data_ptr(), vpool.data_ptr(), ks, vs, dtype_code(kpool.dtype), n_slots, slots, n,
-            b, h, HEAD_DIM, frame_tokens, _stream(kpool.device),
-        ),
+    args = (
+        k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
+        kpool.data_ptr(), vpool.data_ptr(), ks, vs, dtype_code(kpool.dtype), n_slots, slots, n,
+        b, h, HEAD_DIM, frame_tokens, _stream(kpool.device),
     )
     moved = 2 * n * frame_tokens * b * h * HEAD_DIM * (k_new.element_size() + kpool.element_size())
-    _toc("append", t0, moved)
+
+    def launch() -> None:
+        t0 = _tic()
+        _lib.check("skv_append", lib.skv_append(*args))
+        _toc("append", t0, moved)
+
+    launch.bytes_moved = moved
+    launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots)  # keep buffers alive
+    return launch
 
 
-def gather_frames(
+def append_frames(
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    kpool: torch.Tensor,
+    vpool: torch.Tensor,
+    dst_slots: Sequence[int],
+    *,
+    frame_tokens: int,
+    src_frame0: int = 0,
+    kscale: torch.Tensor | None = None,
+    vscale: torch.Tensor | None = None,
+) -> None:
+    """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``."""
+    prepare_append(k_new, v_new, kpool, vpool, dst_slots, frame_tokens=frame_tokens,
+                   src_frame0=src_frame0, kscale=kscale, vscale=vscale)()
+
+
+def prepare_gather(
     kpool: torch.Tensor,
     vpool: torch.Tensor,
     slots: Sequence[int],
@@ -197,8 +219,9 @@ def gather_frames(
     frame_tokens: int,
     k_out: torch.Tensor | None = None,
     v_out: torch.Tensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    """Materialise pool frames ``slots`` as token-major K, V ``[B, len(slots)*T, H, D]``."""
+):
+    """Validate a gather once; return (launcher, k_out, v_out).  The launcher enqueues the gather
+    on the stream current now."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     n = len(slots)
@@ -213,18 +236,39 @@ def gather_frames(
     sb, st, sh = _token_major("k_out", k_out)
     if _token_major("v_out", v_out) != (sb, st, sh):
         raise ValueError("k_out and v_out must share strides")
-    if n == 0:
-        return k_out, v_out
-    t0 = _tic()
-    _lib.check(
-        "skv_gather",
-        lib.skv_gather(
-            kpool.data_ptr(), vpool.data_ptr(), dtype_code(kpool.dtype), n_slots,
-            _lib.int32_array(slots), n, b, h, HEAD_DIM, frame_tokens, k_out.data_ptr(),
-            v_out.data_ptr(), sb, st, sh, _stream(kpool.device),
-        ),
+    table = _lib.int32_array(slots)
+    args = (
+        kpool.data_ptr(), vpool.data_ptr(), dtype_code(kpool.dtype), n_slots, table, n, b, h,
+        HEAD_DIM, frame_tokens, k_out.data_ptr(), v_out.data_ptr(), sb, st, sh,
+        _stream(kpool.device),
     )
-    _toc("gather", t0, 2 * 2 * n * frame_tokens * b * h * HEAD_DIM * kpool.element_size())
+    moved = 2 * 2 * n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
+
+    def launch() -> None:
+        if n == 0:
+            return
+        t0 = _tic()
+        _lib.check("skv_gather", lib.skv_gather(*args))
+        _toc("gather", t0, moved)
+
+    launch.bytes_moved = moved
+    launch.keep = (kpool, vpool, k_out, v_out, table)
+    return launch, k_out, v_out
+
+
+def gather_frames(
+    kpool: torch.Tensor,
+    vpool: torch.Tensor,
+    slots: Sequence[int],
+    *,
+    frame_tokens: int,
+    k_out: torch.Tensor | None = None,
+    v_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Materialise pool frames ``slots`` as token-major K, V ``[B, len(slots)*T, H, D]``."""
+    launch, k_out, v_out = prepare_gather(kpool, vpool, slots, frame_tokens=frame_tokens,
+                                          k_out=k_out, v_out=v_out)
+    launch()
     return k_out, v_out
 
 
