@@ -504,7 +504,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_kernel<bf16,bf16>" if cfg["cache"] == "bf16" else "attn_fp8_kernel<bf16>",
+            "kernel": "skv::attn_kernel<NW, bf16, bf16> (NW = 8 at config 2)" if cfg["cache"] == "bf16" else "skv::attn_fp8_kernel<NW, bf16>",
             "achieved": round(achieved, 2),
             "peak": peak,
             "unit": "TFLOP/s",
