@@ -351,6 +351,11 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       if (i + 3 < 32) opq[(i + 3) & 3] = operand(i + 3);
+      // wave priority falls over the tile (2, 1, 0 by thirds): the wave that is ahead yields
+      // issue slots to the one behind, so both reach the tile's barrier closer together
+      if (i == 0) __builtin_amdgcn_s_setprio(2);
+      if (i == 11) __builtin_amdgcn_s_setprio(1);
+      if (i == 22) __builtin_amdgcn_s_setprio(0);
       const int st = i >> 1;
       if ((i & 1) == 0) {
         const int k = st >> 1, kbb = st & 1;
