@@ -101,6 +101,43 @@ int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_st, int64_
                   int64_t q_pos0, int64_t chunk_tokens, void* out, int64_t out_sb,
                   int64_t out_st, int64_t out_sh, skv_stream_t stream);
 
+/*
+ * RoPE on load (pre-RoPE caches, as the reference keeps them).  The reference re-ropes the
+ * visible window in float64 on every forward: sink frames at temporal positions 0.., local
+ * frames and the query chunk at window-relative positions (causal_model.py:791-876 via
+ * echorope_apply :88-197; table model.py:28-35, split causal_model.py:1855-1866: per head 22
+ * temporal, 21 height and 21 width complex pairs (2i, 2i+1)).  Here:
+ *
+ * skv_append_rope — skv_append for bf16/f32 pools that also writes K with its height/width pairs
+ * rotated (token t of a frame sits at h = t / grid_w, w = t % grid_w) into kr_pool (same layout
+ * as k_pool).  rope_hw (device, float32) holds cos, sin per (h, pair) for h < grid_h, then per
+ * (w, pair) for w < grid_w: [(grid_h + grid_w) * 21 * 2].  grid_h * grid_w == frame_tokens.
+ * k_pool / v_pool receive the raw frames exactly as skv_append writes them.
+ */
+int skv_append_rope(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
+                    int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool, void* v_pool,
+                    int pool_dtype, int n_slots, const int32_t* dst_slots /* host */,
+                    int n_frames, int batch, int heads, int head_dim, int frame_tokens,
+                    void* kr_pool, const float* rope_hw, int grid_h, int grid_w,
+                    skv_stream_t stream);
+
+/*
+ * skv_attention_rope — skv_attention (bf16 pools) over keys from kr_pool (written by
+ * skv_append_rope) with un-roped queries: the kernel rotates each query's height/width pairs
+ * (rope_hw) and, for every key frame j, its temporal pairs by the angle of (query frame f, key
+ * frame j): rope_t (device, float32) = cos, sin of (p_query[f] - p_key[j]) * theta^(-2i/44) per
+ * [f][j][i], i < 22, f < n_qframes (q_len == n_qframes * frame_tokens, query row r is frame
+ * r / T, token r % T).  Scores equal those of queries and keys roped at p_query / p_key.
+ */
+int skv_attention_rope(const void* q, int q_dtype, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                       const void* kr_pool, const void* v_pool, int pool_dtype, int n_slots,
+                       const int32_t* frame_slots /* host */, int n_frames, int batch,
+                       int heads, int head_dim, int q_len, int frame_tokens,
+                       float softmax_scale, int mask_mode, int64_t q_pos0,
+                       int64_t chunk_tokens, void* out, int64_t out_sb, int64_t out_st,
+                       int64_t out_sh, const float* rope_hw, int grid_h, int grid_w,
+                       const float* rope_t, int n_qframes, skv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

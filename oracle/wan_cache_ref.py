@@ -19,6 +19,13 @@ Pinning (tests/test_oracle.py):
 * ``memory_gather`` — index semantics checked against per-frame slicing.
 * ``fp8_fake_quant_frames`` / ``fp8_fake_quant_rows`` — compositions of the pinned
   ``fp8_quantize``; checked for block independence and exact decoding of representable values.
+* ``rope_params`` / ``wan_rope_freqs`` / ``rope_frames`` — angles against ``math.cos`` /
+  ``math.sin`` of position × theta^(-2j/d) computed independently; the temporal/height/width
+  channel split; rotation preserves each pair's norm; position 0 is the identity; scores depend
+  only on position differences (shifting every position leaves q·k unchanged).
+* ``window_relative_positions`` / ``rope_positions`` — hand-derived cases of the reference's
+  allocation (sink frames at 0.., the query chunk pinned at the window tail, capping at the
+  EchoRoPE horizon or ``rope_train_frames``, underflow errors).
 """
 
 from __future__ import annotations
@@ -113,11 +120,17 @@ def cached_self_attention(
     attn_fn: Callable[..., torch.Tensor] = attention,
     memory_k: torch.Tensor | None = None,
     memory_v: torch.Tensor | None = None,
+    rope: dict[str, Any] | None = None,
 ):
     """Returns ``(x [B, Lq, H, D], (current_end, local_end_index, cache_update_info))``.
 
     ``memory_k``/``memory_v`` ([B, M, H, D], already gathered) are placed ahead of the window,
     as the H3 memory path orders ``[bank | history | current]`` (memory_kv_attention.py:97-137).
+
+    ``rope`` (``{"freqs", "grid_hw", "use_echorope", "rope_train_frames"}``) makes ``q``/``k``
+    pre-RoPE, as the reference stores them: the cache keeps raw K and the query chunk, sink
+    frames and local frames are rotated at the positions of ``rope_positions`` before attention
+    (causal_model.py:1135-1199 with _rope_sink_local_and_query / _rope_q_and_window_k).
     """
     max_attention_size = 39600 if local_attn_size == -1 else local_attn_size * frame_seqlen
     current_end = current_start + q.shape[1]
@@ -191,21 +204,48 @@ def cached_self_attention(
         }
 
     # visible window (causal_model.py:1135-1199)
+    nb = num_new_tokens // frame_seqlen
     if sink_tokens > 0:
         local_budget = max_attention_size - sink_tokens
         active_sink = min(sink_tokens, local_end_index)
-        parts_k = [temp_k[:, :active_sink]]
-        parts_v = [temp_v[:, :active_sink]]
+        k_sink, v_sink = temp_k[:, :active_sink], temp_v[:, :active_sink]
+        k_loc, v_loc = temp_k[:, :0], temp_v[:, :0]
         if local_budget > 0:
             local_start_for_window = max(sink_tokens, local_end_index - local_budget)
-            parts_k.append(temp_k[:, local_start_for_window:local_end_index])
-            parts_v.append(temp_v[:, local_start_for_window:local_end_index])
-        k_cat = torch.cat(parts_k, dim=1)
-        v_cat = torch.cat(parts_v, dim=1)
+            k_loc = temp_k[:, local_start_for_window:local_end_index]
+            v_loc = temp_v[:, local_start_for_window:local_end_index]
+        if rope is not None:
+            pos = rope_positions(
+                num_sink_frames=active_sink // frame_seqlen, num_local_frames=k_loc.shape[1] // frame_seqlen,
+                num_new_frames=nb, use_echorope=rope["use_echorope"],
+                max_attention_size=max_attention_size, frame_seqlen=frame_seqlen,
+                table_len=rope["freqs"].shape[0], rope_train_frames=rope.get("rope_train_frames"),
+                current_start_frame=current_start // frame_seqlen, sink_branch=True)
+            q = rope_frames(q, rope["grid_hw"], range(pos["q_start"], pos["q_start"] + nb), rope["freqs"])
+            k_sink = rope_frames(k_sink, rope["grid_hw"], range(k_sink.shape[1] // frame_seqlen), rope["freqs"])
+            nl = k_loc.shape[1] // frame_seqlen
+            if nl > 0:
+                k_loc = rope_frames(k_loc, rope["grid_hw"], range(pos["local_start"], pos["local_start"] + nl),
+                                    rope["freqs"])
+        k_cat = torch.cat([k_sink, k_loc], dim=1)
+        v_cat = torch.cat([v_sink, v_loc], dim=1)
     else:
         window_start = max(0, local_end_index - max_attention_size)
         k_cat = temp_k[:, window_start:local_end_index]
         v_cat = temp_v[:, window_start:local_end_index]
+        if rope is not None:
+            nw = k_cat.shape[1] // frame_seqlen
+            pos = rope_positions(
+                num_sink_frames=0, num_local_frames=nw, num_new_frames=nb,
+                use_echorope=rope["use_echorope"], max_attention_size=max_attention_size,
+                frame_seqlen=frame_seqlen, table_len=rope["freqs"].shape[0], sink_branch=False)
+            if nw == 0:
+                raise RuntimeError("EchoRoPE attention got an empty K window")
+            q = rope_frames(q, rope["grid_hw"], range(pos["q_start"], pos["q_start"] + nb), rope["freqs"])
+            k_cat = rope_frames(k_cat, rope["grid_hw"], range(pos["local_start"], pos["local_start"] + nw),
+                                rope["freqs"])
+    if rope is not None and memory_k is not None:
+        raise NotImplementedError("RoPE with memory-bank frames is outside this restatement")
     if memory_k is not None:
         k_cat = torch.cat([memory_k.to(k_cat.dtype), k_cat], dim=1)
         v_cat = torch.cat([memory_v.to(v_cat.dtype), v_cat], dim=1)
@@ -378,3 +418,107 @@ def e4m3_decode(code: int) -> float:
     if e == 0:
         return s * m * 2.0**-9
     return s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+
+
+# ---------------------------------------------------------------------------------------------
+# RoPE for the cached path: table (model.py:28-35), Wan's temporal/height/width split
+# (causal_model.py:1855-1866), the per-frame rotation of echorope_apply (causal_model.py:88-197;
+# block_relativistic_rope :200-218 is the same transform), and the position allocation of the
+# cache branch (_window_relative_positions :656-701, _echorope_pmax_frames :703-716,
+# _rope_q_and_window_k :718-789, _rope_sink_local_and_query :791-876).
+# ---------------------------------------------------------------------------------------------
+def rope_params(max_seq_len: int, dim: int, theta: float = 10000.0) -> torch.Tensor:
+    """complex128 [max_seq_len, dim/2]: exp(i * p * theta^(-2j/dim))."""
+    assert dim % 2 == 0
+    inv = 1.0 / torch.pow(torch.tensor(theta, dtype=torch.float64),
+                          torch.arange(0, dim, 2, dtype=torch.float64) / dim)
+    ang = torch.outer(torch.arange(max_seq_len, dtype=torch.float64), inv)
+    return torch.polar(torch.ones_like(ang), ang)
+
+
+def rope_split(head_dim: int) -> tuple[int, int, int]:
+    """(temporal, height, width) complex pairs of a head: c - 2(c//3), c//3, c//3 with c = D/2."""
+    c = head_dim // 2
+    return c - 2 * (c // 3), c // 3, c // 3
+
+
+def wan_rope_freqs(head_dim: int = 128, max_seq_len: int = 1024) -> torch.Tensor:
+    """The model's table: [max_seq_len, D/2] complex, temporal | height | width parts."""
+    d = head_dim
+    return torch.cat([rope_params(max_seq_len, d - 4 * (d // 6)),
+                      rope_params(max_seq_len, 2 * (d // 6)),
+                      rope_params(max_seq_len, 2 * (d // 6))], dim=1)
+
+
+def rope_frames(x: torch.Tensor, grid_hw: tuple[int, int], temporal_pos: Sequence[int],
+                freqs: torch.Tensor) -> torch.Tensor:
+    """Rotate ``x`` [B, F*H*W, heads, D] whose frame f sits at temporal position
+    ``temporal_pos[f]`` and whose tokens are ordered (h, w) inside a frame; complex pairs
+    (x[2i], x[2i+1]) are multiplied by the table entries in float64 and the result is cast back
+    to x's dtype (echorope_apply with frame_indices)."""
+    gh, gw = grid_hw
+    B, L, n, D = x.shape
+    F = len(temporal_pos)
+    if L != F * gh * gw:
+        raise ValueError(f"rope_frames: {L} tokens != {F} frames x {gh}x{gw}")
+    ct, ch, cw = rope_split(D)
+    ft, fh, fw = freqs.split([ct, ch, cw], dim=1)
+    pos = torch.as_tensor(list(temporal_pos), dtype=torch.long)
+    if F and (int(pos.min()) < 0 or int(pos.max()) >= ft.shape[0]):
+        raise ValueError(f"temporal positions {list(temporal_pos)} outside the table")
+    f_all = torch.cat([ft[pos].view(F, 1, 1, ct).expand(F, gh, gw, ct),
+                       fh[:gh].view(1, gh, 1, ch).expand(F, gh, gw, ch),
+                       fw[:gw].view(1, 1, gw, cw).expand(F, gh, gw, cw)], dim=-1).reshape(L, 1, -1)
+    xc = torch.view_as_complex(x.to(torch.float64).reshape(B, L, n, D // 2, 2))
+    return torch.view_as_real(xc * f_all).reshape(B, L, n, D).to(x.dtype)
+
+
+def window_relative_positions(*, current_start_frame: int, num_new_frames: int,
+                              num_context_frames: int, pmax: int) -> tuple[int, int]:
+    """(q_start, local_start) of _window_relative_positions (query memory unused on this
+    path): the query block ends at min(current_start + B - 1, pmax - 1) and the context ends
+    with it."""
+    q_last = min(current_start_frame + num_new_frames - 1, pmax - 1)
+    q_start = q_last - num_new_frames + 1
+    local_start = q_last - num_context_frames + 1 if num_context_frames > 0 else q_last
+    return q_start, local_start
+
+
+def echorope_pmax_frames(*, max_attention_size: int, frame_seqlen: int, table_len: int,
+                         min_frames: int) -> int:
+    return min(max(1, int(min_frames), int(max_attention_size // max(1, frame_seqlen))), table_len)
+
+
+def rope_positions(*, num_sink_frames: int, num_local_frames: int, num_new_frames: int,
+                   use_echorope: bool, max_attention_size: int, frame_seqlen: int,
+                   table_len: int = 1024, rope_train_frames: int | None = None,
+                   current_start_frame: int = 0, sink_branch: bool = True) -> dict[str, int]:
+    """Temporal positions of the visible window and the query chunk.
+
+    ``sink_branch`` selects _rope_sink_local_and_query (a sink is configured: sink frames at
+    0..ns-1, then the local frames) or _rope_q_and_window_k (no sink: one window).  Returns
+    ``{"q_start", "local_start", "num_sink"}``; the key positions of the window in ``cat``
+    order are ``range(num_sink) + range(local_start, local_start + num_local)``.
+    """
+    nb, nl = num_new_frames, num_local_frames
+    ns = num_sink_frames if sink_branch else 0
+    pmax = echorope_pmax_frames(max_attention_size=max_attention_size, frame_seqlen=frame_seqlen,
+                                table_len=table_len, min_frames=nb)
+    if use_echorope:
+        q_start, local_start = window_relative_positions(
+            current_start_frame=max(0, ns + nl - nb), num_new_frames=nb,
+            num_context_frames=nl, pmax=pmax)
+    elif sink_branch:
+        if rope_train_frames is None:
+            q_last = ns + nl - 1
+        else:
+            q_last = min(current_start_frame + nb - 1, rope_train_frames - 1)
+        q_start = q_last - nb + 1
+        local_start = q_last - nl + 1 if nl > 0 else max(ns, q_start)
+    else:
+        q_start, local_start = nl - nb, 0
+    if q_start < 0 or local_start < 0:
+        raise ValueError(
+            f"EchoRoPE underflow while assigning positions: B={nb}, R={nl}, sink={ns}, "
+            f"q_start={q_start}, local_start={local_start}, pmax={pmax}")
+    return {"q_start": q_start, "local_start": local_start, "num_sink": ns}

@@ -7,14 +7,18 @@ Public surface (the reference's call signatures, solar/backends/wan22/runtime):
 * :func:`attend_cached`, :func:`apply_cache_updates` — cached self-attention + deferred commit
 * :func:`attention`, :func:`chunk_causal_attention` — dense drop-in attention ops
 * :mod:`solarwm_amd.kernels` — thin wrappers of the C ABI in include/solarkv.h
+* :class:`RopeConfig` — pre-RoPE caches with Wan RoPE applied on load (``rope=`` of the
+  allocator)
 """
 
 from .attention import apply_cache_updates, attend_cached, attention, chunk_causal_attention
 from .cache import CacheGeometry, CachePlan, SlotKVCache, make_kv_cache_allocator, plan_cached_forward
+from .rope import RopeConfig
 
 __all__ = [
     "CacheGeometry",
     "CachePlan",
+    "RopeConfig",
     "SlotKVCache",
     "apply_cache_updates",
     "attend_cached",

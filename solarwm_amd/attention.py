@@ -23,6 +23,7 @@ import torch
 
 from . import _lib, kernels
 from .cache import CacheUpdate, SlotKVCache
+from .rope import positions as rope_positions
 
 
 def _pack_dense(k: torch.Tensor, v: torch.Tensor, pool_dtype: torch.dtype):
@@ -144,8 +145,9 @@ def attend_cached(
 ) -> tuple[torch.Tensor, tuple[int, int, CacheUpdate]]:
     """One layer's cached self-attention (causal_model.py:1028-1235, post-projection/RoPE).
 
-    ``q``, ``k``, ``v`` are the chunk's ``[B, Lq, H, D]`` query/key/value (K already roped, as
-    stored in the cache).  The chunk is appended into staging slots, the visible window is the
+    ``q``, ``k``, ``v`` are the chunk's ``[B, Lq, H, D]`` query/key/value: post-RoPE for a cache
+    without RoPE configuration, pre-RoPE (as the reference's cache branch receives them) for a
+    cache allocated with ``rope`` (RoPE applied on load at the reference's window positions).  The chunk is appended into staging slots, the visible window is the
     reference's ``cat[sink, local]`` (including the chunk), optionally preceded by memory-bank
     frames ``memory_frames`` (bank indices, in order), and nothing in the committed cache
     changes until :func:`apply_cache_updates`.  Returns ``(out [B, Lq, H, D], (current_end,
@@ -165,18 +167,39 @@ def attend_cached(
         int(current_start), q.shape[1], sink_recache_after_switch
     )
     T = g.frame_tokens
+    rope = kv_cache.rope
+    if rope is not None and memory_frames:
+        raise NotImplementedError("memory-bank frames with RoPE on load are not supported")
     if plan.write_len > 0:
         kernels.append_frames(
             k, v, kv_cache.kpool, kv_cache.vpool, staging, frame_tokens=T,
             src_frame0=plan.roped_offset // T, kscale=kv_cache.kscale, vscale=kv_cache.vscale,
+            kr_pool=kv_cache.krpool, rope_hw=rope.hw if rope is not None else None,
+            grid_hw=rope.cfg.grid_hw if rope is not None else None,
         )
     frames = list(kv_cache.bank_slots(memory_frames)) if memory_frames else []
     frames.extend(window)
     if not frames:
         raise RuntimeError("KV-cache attention window is empty")  # causal_model.py:785-787
+    rope_args = None
+    kpool = kv_cache.kpool
+    if rope is not None:
+        # sink frames lead the window when a sink is configured (causal_model.py:1135-1156);
+        # the query chunk is whole frames (causal_model.py:737-744, :806-810)
+        nb = q.shape[1] // T
+        if nb * T != q.shape[1]:
+            raise ValueError("EchoRoPE expects the query chunk to contain whole frames")
+        sink_branch = g.sink_tokens > 0
+        ns = (plan.window[0][1] - plan.window[0][0]) // T if sink_branch and plan.window else 0
+        qpos, kpos = rope_positions(
+            rope.cfg, num_sink_frames=ns, num_local_frames=len(window) - ns, num_new_frames=nb,
+            max_attention_size=g.max_attention_size, frame_tokens=T,
+            current_start_frame=int(current_start) // T, sink_branch=sink_branch)
+        rope_args = (rope.hw, rope.cfg.grid_hw, rope.temporal(qpos, kpos))
+        kpool = kv_cache.krpool
     x = kernels.attention_frames(
-        q, kv_cache.kpool, kv_cache.vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
-        kscale=kv_cache.kscale, vscale=kv_cache.vscale, out=out,
+        q, kpool, kv_cache.vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
+        kscale=kv_cache.kscale, vscale=kv_cache.vscale, out=out, rope=rope_args,
     )
     update = kv_cache.stage(plan, temp)
     return x, (plan.current_end, plan.local_end_index, update)

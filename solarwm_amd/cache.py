@@ -28,6 +28,7 @@ from typing import Any, Iterator, Sequence
 import torch
 
 from . import kernels
+from .rope import RopeConfig, RopeTables
 
 # causal_model.py:572-574: local_attn_size == -1 means a fixed 39600-token attention budget.
 UNBOUNDED_ATTENTION_TOKENS = 39600
@@ -331,15 +332,29 @@ class SlotKVCache(Mapping):
     cache materialised by the gather kernel (for inspection; the hot path never builds it);
     ``"global_end_index"``/``"local_end_index"`` return 1-element int64 CPU tensors mirroring
     the host state.
+
+    With ``rope`` (tables shared by every layer of a model) the cache is pre-RoPE like the
+    reference's: ``k``/``v`` hold the raw frames, and ``krpool`` holds each frame's K with its
+    height/width RoPE pairs rotated, which the attention kernel reads (bf16 caches only).
     """
 
-    def __init__(self, geom: CacheGeometry, *, dtype: torch.dtype, device: torch.device | str):
+    def __init__(self, geom: CacheGeometry, *, dtype: torch.dtype, device: torch.device | str,
+                 rope: RopeTables | None = None):
         self.geom = geom
         self.dtype = dtype
         self.device = torch.device(device)
         self.kpool, self.vpool, self.kscale, self.vscale = kernels.new_pools(
             geom.n_slots, geom.batch, geom.heads, geom.frame_tokens, dtype, self.device
         )
+        self.rope = rope
+        self.krpool = None
+        if rope is not None:
+            if dtype != torch.bfloat16:
+                raise ValueError(f"RoPE on load needs a bf16 cache, got {dtype}")
+            gh, gw = rope.cfg.grid_hw
+            if gh * gw != geom.frame_tokens:
+                raise ValueError(f"RoPE grid {gh}x{gw} does not tile {geom.frame_tokens}-token frames")
+            self.krpool = torch.zeros_like(self.kpool)
         self.slots = SlotTable(geom)
 
     def reset(self) -> None:
@@ -347,6 +362,8 @@ class SlotKVCache(Mapping):
         self.slots.reset()
         self.kpool.zero_()
         self.vpool.zero_()
+        if self.krpool is not None:
+            self.krpool.zero_()
         if self.kscale is not None:
             self.kscale.zero_()
             self.vscale.zero_()
@@ -377,6 +394,8 @@ class SlotKVCache(Mapping):
 
     def write_bank(self, indices: Sequence[int], k: torch.Tensor, v: torch.Tensor) -> None:
         """Store frames of ``k``/``v`` ([B, len(indices)*T, H, D]) in memory-bank entries."""
+        if self.rope is not None:
+            raise NotImplementedError("memory-bank frames with RoPE on load are not supported")
         kernels.append_frames(
             k, v, self.kpool, self.vpool, self.bank_slots(indices),
             frame_tokens=self.geom.frame_tokens, kscale=self.kscale, vscale=self.vscale,
@@ -417,12 +436,15 @@ def make_kv_cache_allocator(
     num_frame_per_block: int = 3,
     bank_frames: int = 0,
     cache_dtype: torch.dtype | None = None,
+    rope: RopeConfig | None = None,
 ):
     """Return ``allocate_kv_cache(batch_size, *, dtype, device) -> list[SlotKVCache]``.
 
     Same signature as ``Wan5BStage2Runtime.allocate_kv_cache`` (stage2.py:1758-1817), so it can
     be injected as that runtime's ``_kv_cache_allocator``.  ``cache_dtype`` overrides the storage
     dtype (``torch.float8_e4m3fn`` for the fp8 cache); by default the model dtype is used.
+    ``rope`` makes the caches pre-RoPE (K and Q are passed un-roped and RoPE is applied on load,
+    as the reference's cache branch does); its tables are shared by all layers.
     """
     if local_attn_size <= 0:
         raise ValueError("the slot cache needs a positive local_attn_size (cache frames)")
@@ -440,6 +462,7 @@ def make_kv_cache_allocator(
             bank_frames=bank_frames,
         )
         store = dtype if cache_dtype is None else cache_dtype
-        return [SlotKVCache(geom, dtype=store, device=device) for _ in range(num_layers)]
+        tables = RopeTables(rope, device) if rope is not None else None
+        return [SlotKVCache(geom, dtype=store, device=device, rope=tables) for _ in range(num_layers)]
 
     return allocate_kv_cache

@@ -52,8 +52,18 @@ struct AttnArgs {
   float scale_log2;  // softmax_scale * log2(e)
   int mask_mode;
   int64_t q_pos0, chunk, n_keys;
+  // RoPE on load (bf16 pools; kpool is then the height/width-roped K copy): rope_hw = cos, sin
+  // per (h, pair) then per (w, pair) of the spatial pairs; rope_t = cos, sin of
+  // (p_query_frame - p_key_frame) * w_j per (query frame, key frame, temporal pair)
+  const float* rope_hw;
+  const float* rope_t;
+  int gh, gw, n_qframes;
   int32_t slots[SKV_MAX_FRAMES];
 };
+
+// Wan's split of a head's 64 complex channel pairs (2i, 2i+1): 22 temporal, 21 height, 21 width
+// (causal_model.py:1855-1866).
+constexpr int kRopeT = 22, kRopeHW = 21;
 
 // Workgroups have NW = 4 or 8 waves (128 or 256 queries); the launcher picks the shape that
 // fills the 256 CUs best (8-wave groups halve the K/V bytes staged per query).
@@ -192,7 +202,7 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
     }
 }
 
-template <int NW, typename QT, typename KT>
+template <int NW, typename QT, typename KT, bool ROPE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   constexpr int kBQ = NW * 32;
@@ -221,13 +231,64 @@ void attn_kernel(AttnArgs a) {
 
   // Q^T operand: lane (n, hh) holds q[qrow][k*16 + hh*8 .. +7] for k = 0..7.
   bf16x8 qf[8];
+  // RoPE: the query's height/width pairs are rotated once here; its temporal pairs (0..21, in
+  // qf[0..2]) are kept unrotated in qt0 and turned by (p_query - p_key) per key frame below.
+  [[maybe_unused]] bf16x8 qt0[3];
+  [[maybe_unused]] int qfi = 0;  // query frame of this lane's row
   {
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
                    (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 8;
+    if constexpr (ROPE) {
+      const int qr = qlive ? qrow : a.Lq - 1;
+      qfi = qr / a.T;
+      const int tt = qr - qfi * a.T, hq = tt / a.gw, wq = tt - hq * a.gw;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-      qf[k] = qlive ? Vec8<QT>::load(qp + k * 16).to_bf16() : Vec8<bf16>::zero().to_bf16();
+      for (int k = 0; k < 8; ++k) {
+        const Vec8<QT> x = qlive ? Vec8<QT>::load(qp + k * 16) : Vec8<QT>::zero();
+        Vec8<float> y;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y.set(e, (float)(bf16)x.get(e));
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int pr = k * 8 + hh * 4 + m;
+          if (pr < kRopeT) continue;
+          const int idx = pr < kRopeT + kRopeHW ? hq * kRopeHW + (pr - kRopeT)
+                                                : (a.gh + wq) * kRopeHW + (pr - kRopeT - kRopeHW);
+          const float c = a.rope_hw[2 * idx], sn = a.rope_hw[2 * idx + 1];
+          const float u = y.get(2 * m), v = y.get(2 * m + 1);
+          y.set(2 * m, u * c - v * sn);
+          y.set(2 * m + 1, u * sn + v * c);
+        }
+        qf[k] = y.to_bf16();
+      }
+#pragma unroll
+      for (int k = 0; k < 3; ++k) qt0[k] = qf[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        qf[k] = qlive ? Vec8<QT>::load(qp + k * 16).to_bf16() : Vec8<bf16>::zero().to_bf16();
+    }
   }
+  // RoPE: qf[0..2] <- qt0 with temporal pair p turned by the angle of (query frame, key frame j)
+  [[maybe_unused]] auto rot_q = [&](int j) {
+    const float* tb = a.rope_t + ((int64_t)qfi * a.n_frames + j) * (2 * kRopeT);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      Vec8<float> y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y.set(e, (float)qt0[k][e]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int pr = k * 8 + hh * 4 + m;
+        if (pr >= kRopeT) continue;
+        const float c = tb[2 * pr], sn = tb[2 * pr + 1];
+        const float u = y.get(2 * m), v = y.get(2 * m + 1);
+        y.set(2 * m, u * c - v * sn);
+        y.set(2 * m + 1, u * sn + v * c);
+      }
+      qf[k] = y.to_bf16();
+    }
+  };
 
   // Visibility limits (keys indexed 0..n_keys-1 in frame-list order; n_keys < 2^31).
   const int n_keys = (int)a.n_keys;
@@ -301,6 +362,7 @@ void attn_kernel(AttnArgs a) {
       *reinterpret_cast<bf16x8*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = Vec8<bf16>::zero().to_bf16();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if constexpr (ROPE) rot_q(0);
     qk_tile(kb_lds(0) + lane16, qf, s_cur);
     int tok0, key0;
     if (tile_needs_mask(0, tok0, key0)) mask_tile(s_cur, hh, tok0, a.T, key0, lim_lane);
@@ -321,6 +383,11 @@ void attn_kernel(AttnArgs a) {
     loader.issue_v(vpool + vtile_base(tau), vb_lds(cb), w);
     const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
     const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
+    if constexpr (ROPE) {
+      // QK(tau+1) below opens a new key frame: turn Q's temporal pairs for it
+      const int t1 = tau + 1;
+      if (t1 < ntau && t1 % a.ntiles_f == 0) rot_q(t1 / a.ntiles_f);
+    }
 
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ls[4] = {0.f, 0.f, 0.f, 0.f};
@@ -773,7 +840,7 @@ static int cu_count() {
 }
 
 template <int NW>
-static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, hipStream_t s) {
+static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, bool rope, hipStream_t s) {
   dim3 grid(a.n_wg), block(NW * 64);
   if (pool_dtype == SKV_FP8_E4M3) {
     if (q_dtype == SKV_BF16)
@@ -783,25 +850,32 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, hipStream_t s
     return;
   }
   const size_t lds_bytes = 2 * kTileBytes;
+  if (rope) {  // bf16 pools only (checked by the caller)
+    if (q_dtype == SKV_BF16)
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, true>), grid, block, lds_bytes, s, a);
+    else
+      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, true>), grid, block, lds_bytes, s, a);
+    return;
+  }
   if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, false>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
-    hipLaunchKernelGGL((attn_kernel<NW, bf16, float>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, float, false>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_F32 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<NW, float, bf16>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, float, bf16, false>), grid, block, lds_bytes, s, a);
   else
-    hipLaunchKernelGGL((attn_kernel<NW, float, float>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, float, float, false>), grid, block, lds_bytes, s, a);
 }
 
-extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
-                             int64_t q_sh, const void* k_pool, const void* v_pool,
-                             const float* k_scale, const float* v_scale, int pool_dtype,
-                             int n_slots, const int32_t* frame_slots, int n_frames, int batch,
-                             int heads, int head_dim, int q_len, int frame_tokens,
-                             float softmax_scale, int mask_mode, int64_t q_pos0,
-                             int64_t chunk_tokens, void* out, int64_t out_sb, int64_t out_st,
-                             int64_t out_sh, skv_stream_t stream) {
-  clear_error();
+static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
+                          int64_t q_sh, const void* k_pool, const void* v_pool,
+                          const float* k_scale, const float* v_scale, int pool_dtype,
+                          int n_slots, const int32_t* frame_slots, int n_frames, int batch,
+                          int heads, int head_dim, int q_len, int frame_tokens,
+                          float softmax_scale, int mask_mode, int64_t q_pos0,
+                          int64_t chunk_tokens, void* out, int64_t out_sb, int64_t out_st,
+                          int64_t out_sh, const float* rope_hw, int grid_h, int grid_w,
+                          const float* rope_t, int n_qframes, skv_stream_t stream) {
   if (!q || !k_pool || !v_pool || !frame_slots || !out) {
     set_error("skv_attention: null pointer argument");
     return SKV_E_ARG;
@@ -853,8 +927,27 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
               frame_tokens);
     return SKV_E_ARG;
   }
+  const bool rope = rope_t != nullptr;
+  if (rope) {
+    if (pool_dtype != SKV_BF16) {
+      set_error("skv_attention_rope: only bf16 pools are supported");
+      return SKV_E_UNSUPPORTED;
+    }
+    if (!rope_hw || grid_h <= 0 || grid_w <= 0 || (int64_t)grid_h * grid_w != frame_tokens ||
+        n_qframes <= 0 || (int64_t)n_qframes * frame_tokens != q_len) {
+      set_error("skv_attention_rope: need rope_hw, grid_h * grid_w == frame_tokens (%d x %d vs "
+                "%d) and q_len == n_qframes * frame_tokens (%d vs %d x %d)", grid_h, grid_w,
+                frame_tokens, q_len, n_qframes, frame_tokens);
+      return SKV_E_ARG;
+    }
+  }
   if (q_len == 0) return SKV_OK;
   AttnArgs a;
+  a.rope_hw = rope_hw;
+  a.rope_t = rope_t;
+  a.gh = grid_h;
+  a.gw = grid_w;
+  a.n_qframes = n_qframes;
   a.q = q;
   a.o = out;
   a.kpool = k_pool;
@@ -902,13 +995,48 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (nw == 8)
-    launch<8>(a, q_dtype, pool_dtype, s);
+    launch<8>(a, q_dtype, pool_dtype, rope, s);
   else
-    launch<4>(a, q_dtype, pool_dtype, s);
+    launch<4>(a, q_dtype, pool_dtype, rope, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("skv_attention: launch failed: %s", hipGetErrorString(e));
     return SKV_E_LAUNCH;
   }
   return SKV_OK;
+}
+
+extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
+                             int64_t q_sh, const void* k_pool, const void* v_pool,
+                             const float* k_scale, const float* v_scale, int pool_dtype,
+                             int n_slots, const int32_t* frame_slots, int n_frames, int batch,
+                             int heads, int head_dim, int q_len, int frame_tokens,
+                             float softmax_scale, int mask_mode, int64_t q_pos0,
+                             int64_t chunk_tokens, void* out, int64_t out_sb, int64_t out_st,
+                             int64_t out_sh, skv_stream_t stream) {
+  clear_error();
+  return attention_impl(q, q_dtype, q_sb, q_st, q_sh, k_pool, v_pool, k_scale, v_scale,
+                        pool_dtype, n_slots, frame_slots, n_frames, batch, heads, head_dim, q_len,
+                        frame_tokens, softmax_scale, mask_mode, q_pos0, chunk_tokens, out, out_sb,
+                        out_st, out_sh, nullptr, 0, 0, nullptr, 0, stream);
+}
+
+extern "C" int skv_attention_rope(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
+                                  int64_t q_sh, const void* kr_pool, const void* v_pool,
+                                  int pool_dtype, int n_slots, const int32_t* frame_slots,
+                                  int n_frames, int batch, int heads, int head_dim, int q_len,
+                                  int frame_tokens, float softmax_scale, int mask_mode,
+                                  int64_t q_pos0, int64_t chunk_tokens, void* out,
+                                  int64_t out_sb, int64_t out_st, int64_t out_sh,
+                                  const float* rope_hw, int grid_h, int grid_w,
+                                  const float* rope_t, int n_qframes, skv_stream_t stream) {
+  clear_error();
+  if (!rope_t) {
+    set_error("skv_attention_rope: null rope_t");
+    return SKV_E_ARG;
+  }
+  return attention_impl(q, q_dtype, q_sb, q_st, q_sh, kr_pool, v_pool, nullptr, nullptr,
+                        pool_dtype, n_slots, frame_slots, n_frames, batch, heads, head_dim, q_len,
+                        frame_tokens, softmax_scale, mask_mode, q_pos0, chunk_tokens, out, out_sb,
+                        out_st, out_sh, rope_hw, grid_h, grid_w, rope_t, n_qframes, stream);
 }

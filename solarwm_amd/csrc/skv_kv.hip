@@ -22,8 +22,35 @@ struct AppendArgs {
   float* vscale;
   int64_t slot_stride;  // elements per slot in each pool (B*H*Tp*D)
   int B, H, T, Tp, n_frames, src_frame0, ntiles;
+  // RoPE copy (bf16/fp32 pools): krpool receives K with the height/width pairs of Wan's RoPE
+  // applied (rope_hw: cos, sin per (h, pair) then per (w, pair)); nullptr = no copy
+  void* krpool;
+  const float* rope_hw;
+  int gh, gw;
   int32_t slots[SKV_MAX_APPEND_FRAMES];
 };
+
+// Wan splits a head's 64 complex channel pairs (2i, 2i+1) into 22 temporal, 21 height and 21
+// width pairs (causal_model.py:1855-1866).
+constexpr int kRopeT = 22, kRopeHW = 21;
+
+// Rotate the spatial pairs among channels [col, col+8) of token t (grid width gw): pair p in
+// [22, 43) turns by the angle of row h = t / gw, p in [43, 64) by that of column w = t % gw.
+template <typename E>
+__device__ inline void rope_spatial8(Vec8<E>& v, int col, int t, int gh, int gw, const float* tab) {
+  if (col + 8 <= 2 * kRopeT) return;
+  const int hq = t / gw, wq = t - hq * gw;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int p = col / 2 + m;
+    if (p < kRopeT) continue;
+    const int idx = p < kRopeT + kRopeHW ? hq * kRopeHW + (p - kRopeT) : (gh + wq) * kRopeHW + (p - kRopeT - kRopeHW);
+    const float c = tab[2 * idx], sn = tab[2 * idx + 1];
+    const float x = (float)v.get(2 * m), y = (float)v.get(2 * m + 1);
+    v.set(2 * m, (E)(x * c - y * sn));
+    v.set(2 * m + 1, (E)(x * sn + y * c));
+  }
+}
 
 // 8x8 transpose of 16-bit elements held as 8 rows of 4 x u32 (row r = token, word c/2 half c%2
 // = channel c): out[c].word[w] = (in[2w] half c, in[2w+1] half c).
@@ -70,6 +97,10 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
       Vec8<E> kv = live ? Vec8<E>::load(ks + src_base + (int64_t)(tok0 + row) * a.s_st + col)
                         : Vec8<E>::zero();
       kv.store_nt(kp + row * kHeadDim + col);
+      if (a.krpool) {
+        if (live) rope_spatial8(kv, col, tok0 + row, a.gh, a.gw, a.rope_hw);
+        kv.store_nt(static_cast<E*>(a.krpool) + (kp - static_cast<E*>(a.kpool)) + row * kHeadDim + col);
+      }
     }
     return;
   }
@@ -322,12 +353,12 @@ using namespace skv;
 
 static bool aligned8(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)(8 * bytes)) == 0; }
 
-extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
-                          int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool,
-                          void* v_pool, float* k_scale, float* v_scale, int pool_dtype,
-                          int n_slots, const int32_t* dst_slots, int n_frames, int batch,
-                          int heads, int head_dim, int frame_tokens, skv_stream_t stream) {
-  clear_error();
+static int append_impl(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
+                       int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool,
+                       void* v_pool, float* k_scale, float* v_scale, int pool_dtype,
+                       int n_slots, const int32_t* dst_slots, int n_frames, int batch,
+                       int heads, int head_dim, int frame_tokens, void* kr_pool,
+                       const float* rope_hw, int grid_h, int grid_w, skv_stream_t stream) {
   if (!k_new || !v_new || !k_pool || !v_pool || !dst_slots) {
     set_error("skv_append: null pointer argument");
     return SKV_E_ARG;
@@ -349,6 +380,17 @@ extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, i
     set_error("skv_append: src_dtype=%d pool_dtype=%d unsupported (pool must equal src or be fp8)",
               src_dtype, pool_dtype);
     return SKV_E_UNSUPPORTED;
+  }
+  if (kr_pool) {
+    if (fp8) {
+      set_error("skv_append_rope: fp8 pools are not supported");
+      return SKV_E_UNSUPPORTED;
+    }
+    if (!rope_hw || grid_h <= 0 || grid_w <= 0 || (int64_t)grid_h * grid_w != frame_tokens) {
+      set_error("skv_append_rope: need rope_hw and grid_h * grid_w == frame_tokens (%d x %d vs %d)",
+                grid_h, grid_w, frame_tokens);
+      return SKV_E_ARG;
+    }
   }
   if (fp8 && (!k_scale || !v_scale)) {
     set_error("skv_append: fp8 pool needs k_scale and v_scale");
@@ -377,6 +419,10 @@ extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, i
   a.src_frame0 = src_frame0;
   a.ntiles = a.Tp / kTile;
   a.slot_stride = (int64_t)batch * heads * a.Tp * kHeadDim;
+  a.krpool = kr_pool;
+  a.rope_hw = rope_hw;
+  a.gh = grid_h;
+  a.gw = grid_w;
   for (int f = 0; f < n_frames; ++f) {
     if (dst_slots[f] < 0 || dst_slots[f] >= n_slots) {
       set_error("skv_append: dst_slots[%d]=%d outside [0, %d)", f, dst_slots[f], n_slots);
@@ -404,6 +450,34 @@ extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, i
     return SKV_E_LAUNCH;
   }
   return SKV_OK;
+}
+
+extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
+                          int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool,
+                          void* v_pool, float* k_scale, float* v_scale, int pool_dtype,
+                          int n_slots, const int32_t* dst_slots, int n_frames, int batch,
+                          int heads, int head_dim, int frame_tokens, skv_stream_t stream) {
+  clear_error();
+  return append_impl(k_new, v_new, src_dtype, src_sb, src_st, src_sh, src_frame0, k_pool, v_pool,
+                     k_scale, v_scale, pool_dtype, n_slots, dst_slots, n_frames, batch, heads,
+                     head_dim, frame_tokens, nullptr, nullptr, 0, 0, stream);
+}
+
+extern "C" int skv_append_rope(const void* k_new, const void* v_new, int src_dtype,
+                               int64_t src_sb, int64_t src_st, int64_t src_sh, int src_frame0,
+                               void* k_pool, void* v_pool, int pool_dtype, int n_slots,
+                               const int32_t* dst_slots, int n_frames, int batch, int heads,
+                               int head_dim, int frame_tokens, void* kr_pool,
+                               const float* rope_hw, int grid_h, int grid_w,
+                               skv_stream_t stream) {
+  clear_error();
+  if (!kr_pool) {
+    set_error("skv_append_rope: null kr_pool");
+    return SKV_E_ARG;
+  }
+  return append_impl(k_new, v_new, src_dtype, src_sb, src_st, src_sh, src_frame0, k_pool, v_pool,
+                     nullptr, nullptr, pool_dtype, n_slots, dst_slots, n_frames, batch, heads,
+                     head_dim, frame_tokens, kr_pool, rope_hw, grid_h, grid_w, stream);
 }
 
 extern "C" int skv_gather(const void* k_pool, const void* v_pool, int pool_dtype, int n_slots,

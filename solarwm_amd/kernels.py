@@ -145,6 +145,20 @@ def _scales(kpool, kscale, vscale):
     return kscale.data_ptr(), vscale.data_ptr()
 
 
+def _check_rope_hw(kr_pool, kpool, rope_hw, grid_hw, frame_tokens) -> None:
+    _require_cuda("kr_pool", kr_pool)
+    if kr_pool.shape != kpool.shape or kr_pool.dtype != kpool.dtype or not kr_pool.is_contiguous():
+        raise ValueError("kr_pool must be a contiguous tensor shaped and typed like the K pool")
+    if grid_hw is None or rope_hw is None:
+        raise ValueError("RoPE needs rope_hw and grid_hw")
+    gh, gw = int(grid_hw[0]), int(grid_hw[1])
+    if gh * gw != frame_tokens:
+        raise ValueError(f"grid {gh}x{gw} does not tile a {frame_tokens}-token frame")
+    _require_cuda("rope_hw", rope_hw)
+    if rope_hw.dtype != torch.float32 or rope_hw.numel() != (gh + gw) * 21 * 2 or not rope_hw.is_contiguous():
+        raise ValueError(f"rope_hw must be contiguous float32 with {(gh + gw) * 42} entries")
+
+
 def prepare_append(
     k_new: torch.Tensor,
     v_new: torch.Tensor,
@@ -156,9 +170,16 @@ def prepare_append(
     src_frame0: int = 0,
     kscale: torch.Tensor | None = None,
     vscale: torch.Tensor | None = None,
+    kr_pool: torch.Tensor | None = None,
+    rope_hw: torch.Tensor | None = None,
+    grid_hw: tuple[int, int] | None = None,
 ):
     """Validate an append once and return a zero-argument launcher that enqueues it on the stream
-    current now (repeated launches skip the Python-side checks)."""
+    current now (repeated launches skip the Python-side checks).
+
+    With ``kr_pool`` (same shape and dtype as ``kpool``), the frames' K is also written there
+    with the height/width pairs of RoPE applied (``rope_hw`` from ``rope.spatial_table``,
+    ``grid_hw`` = the frame's patch grid)."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("k_new", k_new)
@@ -177,20 +198,33 @@ def prepare_append(
         raise ValueError("k_new and pools must be on the same device")
     ks, vs = _scales(kpool, kscale, vscale)
     slots = _lib.int32_array(dst_slots)
-    args = (
-        k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
-        kpool.data_ptr(), vpool.data_ptr(), ks, vs, dtype_code(kpool.dtype), n_slots, slots, n,
-        b, h, HEAD_DIM, frame_tokens, _stream(kpool.device),
-    )
     moved = 2 * n * frame_tokens * b * h * HEAD_DIM * (k_new.element_size() + kpool.element_size())
+    if kr_pool is None:
+        fn_name = "skv_append"
+        args = (
+            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
+            kpool.data_ptr(), vpool.data_ptr(), ks, vs, dtype_code(kpool.dtype), n_slots, slots,
+            n, b, h, HEAD_DIM, frame_tokens, _stream(kpool.device),
+        )
+    else:
+        _check_rope_hw(kr_pool, kpool, rope_hw, grid_hw, frame_tokens)
+        fn_name = "skv_append_rope"
+        args = (
+            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
+            kpool.data_ptr(), vpool.data_ptr(), dtype_code(kpool.dtype), n_slots, slots, n, b, h,
+            HEAD_DIM, frame_tokens, kr_pool.data_ptr(), rope_hw.data_ptr(), grid_hw[0],
+            grid_hw[1], _stream(kpool.device),
+        )
+        moved += n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
+    fn = getattr(lib, fn_name)
 
     def launch() -> None:
         t0 = _tic()
-        _lib.check("skv_append", lib.skv_append(*args))
+        _lib.check(fn_name, fn(*args))
         _toc("append", t0, moved)
 
     launch.bytes_moved = moved
-    launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots)  # keep buffers alive
+    launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots, kr_pool, rope_hw)
     return launch
 
 
@@ -205,10 +239,15 @@ def append_frames(
     src_frame0: int = 0,
     kscale: torch.Tensor | None = None,
     vscale: torch.Tensor | None = None,
+    kr_pool: torch.Tensor | None = None,
+    rope_hw: torch.Tensor | None = None,
+    grid_hw: tuple[int, int] | None = None,
 ) -> None:
-    """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``."""
+    """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``
+    (and, with ``kr_pool``, K with its height/width RoPE pairs rotated into ``kr_pool``)."""
     prepare_append(k_new, v_new, kpool, vpool, dst_slots, frame_tokens=frame_tokens,
-                   src_frame0=src_frame0, kscale=kscale, vscale=vscale)()
+                   src_frame0=src_frame0, kscale=kscale, vscale=vscale, kr_pool=kr_pool,
+                   rope_hw=rope_hw, grid_hw=grid_hw)()
 
 
 def prepare_gather(
@@ -286,8 +325,13 @@ def attention_frames(
     q_pos0: int = 0,
     chunk_tokens: int = 0,
     out: torch.Tensor | None = None,
+    rope: tuple[torch.Tensor, tuple[int, int], torch.Tensor] | None = None,
 ) -> torch.Tensor:
-    """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D]."""
+    """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D].
+
+    ``rope = (rope_hw, grid_hw, rope_t)``: ``q`` is pre-RoPE and ``kpool`` is the height/width
+    roped K copy; the kernel ropes the queries (``rope_t`` from ``rope.temporal_table`` with one
+    row per query frame and one column per entry of ``frame_slots``)."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("q", q)
@@ -307,15 +351,36 @@ def attention_frames(
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
     ks, vs = _scales(kpool, kscale, vscale)
     t0 = _tic()
-    _lib.check(
-        "skv_attention",
-        lib.skv_attention(
-            q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(), ks,
-            vs, dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots), len(frame_slots),
-            b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode, q_pos0, chunk_tokens,
-            out.data_ptr(), osb, ost, osh, _stream(q.device),
-        ),
-    )
+    if rope is None:
+        _lib.check(
+            "skv_attention",
+            lib.skv_attention(
+                q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(),
+                ks, vs, dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots),
+                len(frame_slots), b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode,
+                q_pos0, chunk_tokens, out.data_ptr(), osb, ost, osh, _stream(q.device),
+            ),
+        )
+    else:
+        rope_hw, grid_hw, rope_t = rope
+        _check_rope_hw(kpool, kpool, rope_hw, grid_hw, frame_tokens)
+        nq = q.shape[1] // frame_tokens
+        _require_cuda("rope_t", rope_t)
+        if (q.shape[1] != nq * frame_tokens or rope_t.dtype != torch.float32
+                or tuple(rope_t.shape) != (nq, len(frame_slots), 22, 2) or not rope_t.is_contiguous()):
+            raise ValueError(
+                f"rope_t must be contiguous float32 [{nq}, {len(frame_slots)}, 22, 2] and q whole "
+                f"frames (got {tuple(rope_t.shape)}, Lq={q.shape[1]})")
+        _lib.check(
+            "skv_attention_rope",
+            lib.skv_attention_rope(
+                q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(),
+                dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots), len(frame_slots),
+                b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode, q_pos0, chunk_tokens,
+                out.data_ptr(), osb, ost, osh, rope_hw.data_ptr(), int(grid_hw[0]),
+                int(grid_hw[1]), rope_t.data_ptr(), nq, _stream(q.device),
+            ),
+        )
     # algorithmic FLOPs: QKᵀ and PV over every key (masking is not discounted)
     _toc("attention", t0, 4.0 * b * h * q.shape[1] * len(frame_slots) * frame_tokens * HEAD_DIM)
     return out

@@ -78,3 +78,37 @@ def test_python_wrapper_raises_valueerror():
         _lib.check("skv_append", _lib.SKV_E_ARG)
     with pytest.raises(_lib.SolarKVError):
         _lib.check("skv_append", _lib.SKV_E_LAUNCH)
+
+
+def test_signature_arity_matches_header():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, (_, argtypes) in _lib.SIGNATURES.items():
+        m = re.search(rf"\b{name}\s*\(([^)]*)\)\s*;", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(argtypes), name
+
+
+def test_rope_argument_errors_do_not_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    # fp8 pools have no RoPE copy path
+    st = lib.skv_append_rope(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, _lib.SKV_FP8_E4M3,
+                             4, _slots(0), 1, 1, 1, 128, 64, fake, fake, 8, 8, None)
+    assert st == _lib.SKV_E_UNSUPPORTED and b"fp8" in lib.skv_last_error()
+    # the spatial grid must tile the frame
+    st = lib.skv_append_rope(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, _lib.SKV_BF16,
+                             4, _slots(0), 1, 1, 1, 128, 64, fake, fake, 8, 7, None)
+    assert st == _lib.SKV_E_ARG and b"grid" in lib.skv_last_error()
+    st = lib.skv_append_rope(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, _lib.SKV_BF16,
+                             4, _slots(0), 1, 1, 1, 128, 64, None, fake, 8, 8, None)
+    assert st == _lib.SKV_E_ARG and b"kr_pool" in lib.skv_last_error()
+    args = dict(q_len=128, T=64, pool=_lib.SKV_BF16, nq=2, rope_t=fake)
+
+    def attn(**kw):
+        a = dict(args, **kw)
+        return lib.skv_attention_rope(fake, _lib.SKV_BF16, 8, 8, 8, fake, fake, a["pool"], 4,
+                                      _slots(0), 1, 1, 1, 128, a["q_len"], a["T"], 0.1, 0, 0, 0,
+                                      fake, 8, 8, 8, fake, 8, 8, a["rope_t"], a["nq"], None)
+    assert attn(pool=_lib.SKV_F32) == _lib.SKV_E_UNSUPPORTED and b"bf16" in lib.skv_last_error()
+    assert attn(nq=3) == _lib.SKV_E_ARG and b"n_qframes" in lib.skv_last_error()
+    assert attn(rope_t=None) == _lib.SKV_E_ARG and b"rope_t" in lib.skv_last_error()

@@ -319,3 +319,107 @@ def test_fp8_fake_quant_blocks_are_independent():
     assert torch.equal(y2[:, : 2 * T], y[:, : 2 * T])
     q = torch.tensor([[3.0, -1.5, 0.75, 0.0]])
     assert torch.equal(ref.fp8_fake_quant_rows(q), q)  # absmax 3 -> scale 3/448, all exact
+
+
+# ---- RoPE (table, split, rotation, position allocation) ---------------------------------------
+def test_rope_params_angles_match_math():
+    """Entry [p, j] of a dim-d table is exp(i * p * 10000^(-2j/d)), checked against math."""
+    for dim in (44, 42):
+        t = ref.rope_params(1024, dim)
+        for p, j in ((0, 0), (1, 0), (7, 3), (20, dim // 2 - 1), (1023, 5)):
+            ang = p * 10000.0 ** (-2.0 * j / dim)
+            assert abs(t[p, j].real - math.cos(ang)) < 1e-12 and abs(t[p, j].imag - math.sin(ang)) < 1e-12
+
+
+def test_rope_split_and_table_layout():
+    assert ref.rope_split(128) == (22, 21, 21)
+    f = ref.wan_rope_freqs(128)
+    assert f.shape == (1024, 64) and f.dtype == torch.complex128
+    assert torch.equal(f[:, :22], ref.rope_params(1024, 44))
+    assert torch.equal(f[:, 22:43], ref.rope_params(1024, 42))
+    assert torch.equal(f[:, 43:], ref.rope_params(1024, 42))
+
+
+def test_rope_frames_rotation_properties():
+    g = torch.Generator().manual_seed(3)
+    gh, gw = 3, 4
+    x = torch.randn(1, 2 * gh * gw, 2, 128, generator=g, dtype=torch.float64)
+    f = ref.wan_rope_freqs()
+    y = ref.rope_frames(x, (gh, gw), [0, 5], f)
+    pair_norm = lambda t: t.reshape(*t.shape[:-1], 64, 2).pow(2).sum(-1)
+    assert torch.allclose(pair_norm(y), pair_norm(x), atol=1e-12)  # rotations
+    assert torch.allclose(y[:, 0], x[:, 0], atol=0)  # frame 0, token (0, 0): identity
+    # token (h=2, w=1) of frame 1 (temporal position 5): pair 0 turns by 5 rad, pair 22 + j by
+    # 2 * 10000^(-2j/42), pair 43 + j by 1 * 10000^(-2j/42)
+    tok = gh * gw + 2 * gw + 1
+    for pair, ang in ((0, 5.0), (22 + 4, 2 * 10000.0 ** (-8 / 42)), (43 + 7, 1 * 10000.0 ** (-14 / 42))):
+        a, b = x[0, tok, 1, 2 * pair], x[0, tok, 1, 2 * pair + 1]
+        assert abs(y[0, tok, 1, 2 * pair] - (a * math.cos(ang) - b * math.sin(ang))) < 1e-12
+        assert abs(y[0, tok, 1, 2 * pair + 1] - (a * math.sin(ang) + b * math.cos(ang))) < 1e-12
+
+
+def test_rope_scores_depend_on_position_differences():
+    """q.k after RoPE is unchanged when every temporal position shifts by the same amount."""
+    g = torch.Generator().manual_seed(4)
+    gh, gw = 2, 3
+    q = torch.randn(1, gh * gw, 1, 128, generator=g, dtype=torch.float64)
+    k = torch.randn(1, 3 * gh * gw, 1, 128, generator=g, dtype=torch.float64)
+    f = ref.wan_rope_freqs()
+    s0 = ref.rope_frames(q, (gh, gw), [9], f)[0, :, 0] @ ref.rope_frames(k, (gh, gw), [0, 4, 9], f)[0, :, 0].T
+    s1 = ref.rope_frames(q, (gh, gw), [19], f)[0, :, 0] @ ref.rope_frames(k, (gh, gw), [10, 14, 19], f)[0, :, 0].T
+    assert torch.allclose(s0, s1, atol=1e-9)
+    s2 = ref.rope_frames(q, (gh, gw), [19], f)[0, :, 0] @ ref.rope_frames(k, (gh, gw), [10, 15, 19], f)[0, :, 0].T
+    assert not torch.allclose(s0, s2, atol=1e-6)  # a different gap changes the scores
+
+
+@pytest.mark.parametrize("kw,want", [
+    # config-2 steady state, EchoRoPE: sink at 0, local frames 1..20, the chunk at 18..20
+    (dict(num_sink_frames=1, num_local_frames=20, num_new_frames=3, use_echorope=True), (18, 1)),
+    # first chunk: the chunk is frames 0..2 (sink 0, local 1..2)
+    (dict(num_sink_frames=1, num_local_frames=2, num_new_frames=3, use_echorope=True), (0, 1)),
+    # window longer than the EchoRoPE horizon (21 frames): the tail is pinned at 20
+    (dict(num_sink_frames=1, num_local_frames=26, num_new_frames=3, use_echorope=True), (18, -6)),
+    # block-relative without rope_train_frames: physical positions of the window
+    (dict(num_sink_frames=1, num_local_frames=20, num_new_frames=3, use_echorope=False), (18, 1)),
+    # block-relative with rope_train_frames=12: positions freeze at the training horizon
+    (dict(num_sink_frames=1, num_local_frames=9, num_new_frames=3, use_echorope=False,
+          rope_train_frames=12, current_start_frame=40), (9, 3)),
+    # no sink (one window): EchoRoPE puts the window at 0.., the chunk at its tail
+    (dict(num_sink_frames=0, num_local_frames=7, num_new_frames=3, use_echorope=True, sink_branch=False), (4, 0)),
+])
+def test_rope_positions_cases(kw, want):
+    kw = dict(kw, max_attention_size=21 * 1560, frame_seqlen=1560)
+    if want[1] < 0:
+        with pytest.raises(ValueError, match="underflow"):
+            ref.rope_positions(**kw)
+        return
+    pos = ref.rope_positions(**kw)
+    assert (pos["q_start"], pos["local_start"]) == want
+
+
+def test_cached_attention_rope_wiring():
+    """The rope option ropes the query chunk and the visible frames at rope_positions' slots;
+    the cache itself keeps raw K (causal_model.py:1135-1199)."""
+    g = torch.Generator().manual_seed(5)
+    T, gh, gw, H = 12, 3, 4, 2
+    f = ref.wan_rope_freqs()
+    rope = {"freqs": f, "grid_hw": (gh, gw), "use_echorope": True}
+    cache = ref.allocate_kv_cache(num_layers=1, batch_size=1, cache_tokens=5 * T, num_heads=H,
+                                  head_dim=128, dtype=torch.float32)[0]
+    for chunk in range(4):
+        q, k, v = (torch.randn(1, 2 * T, H, 128, generator=g) for _ in range(3))
+        kw = dict(current_start=chunk * 2 * T, frame_seqlen=T, sink_size=1, local_attn_size=5)
+        x, (cur_end, loc_end, info) = ref.cached_self_attention(q, k, v, cache, rope=rope, **kw)
+        # explicit: window frames of the updated temp cache, roped at sink 0 / local / query tail
+        x_raw, _ = ref.cached_self_attention(q, k, v, cache, attn_fn=lambda a, b, c: (a, b, c), **kw)
+        qq, kk, vv = x_raw
+        nf = kk.shape[1] // T
+        pos = ref.rope_positions(num_sink_frames=1, num_local_frames=nf - 1, num_new_frames=2,
+                                 use_echorope=True, max_attention_size=5 * T, frame_seqlen=T)
+        kpos = [0] + list(range(pos["local_start"], pos["local_start"] + nf - 1))
+        want = ref.attention(ref.rope_frames(qq, (gh, gw), [pos["q_start"], pos["q_start"] + 1], f),
+                             ref.rope_frames(kk, (gh, gw), kpos, f), vv)
+        assert torch.equal(x, want)
+        assert kpos[-1] == pos["q_start"] + 1  # the chunk's own keys share the queries' slots
+        ref.apply_cache_updates([cache], [(0, (cur_end, loc_end, info))])
+    assert not torch.equal(cache["k"], ref.rope_frames(cache["k"][:, :5 * T], (gh, gw), range(5), f))
