@@ -28,12 +28,14 @@ import time
 
 CONFIGS = {
     "c2": dict(workload="wan2.1-1.3b", layers=30, heads=12, T=1560, chunk_f=3, cap_f=21,
-               sink_f=1, chunks=27, batch=1, cache="bf16"),
+               sink_f=1, chunks=27, batch=1, cache="bf16", grid=(30, 52)),
     "c3": dict(workload="wan2.2-5b", layers=30, heads=24, T=880, chunk_f=3, cap_f=21,
-               sink_f=1, chunks=40, batch=1, cache="bf16"),
+               sink_f=1, chunks=40, batch=1, cache="bf16", grid=(22, 40)),
     "c5": dict(workload="wan2.1-1.3b fp8-e4m3 kv, 4 streams", layers=30, heads=12, T=1560,
-               chunk_f=3, cap_f=21, sink_f=1, chunks=27, batch=4, cache="fp8"),
+               chunk_f=3, cap_f=21, sink_f=1, chunks=27, batch=4, cache="fp8", grid=(30, 52)),
 }
+# grid: the latent patch grid of one frame (480x832 video -> 60x104 latent -> 2x2 patches; the
+# 5B model's 16x VAE: 704x1280 -> 44x80 -> 22x40), used by the pre-RoPE (RoPE on load) legs
 # config 4: 33B-class memory path (one GPU holds one layer's 256-slot bank: 8.4 GB; all 48
 # layers would need 403 GB)
 C4 = dict(workload="33b-class memory path", layers=48, heads=40, T=1560, chunk_f=3, cap_f=21,
@@ -72,16 +74,17 @@ def make_inputs(cfg, device, seed=1234, outliers=False):
     return out
 
 
-def make_caches(cfg, device):
+def make_caches(cfg, device, rope=False):
     import torch
 
-    from solarwm_amd import make_kv_cache_allocator
+    from solarwm_amd import RopeConfig, make_kv_cache_allocator
 
     alloc = make_kv_cache_allocator(
         num_layers=cfg["layers"], num_heads=cfg["heads"], head_dim=128,
         frame_sequence_length=cfg["T"], local_attn_size=cfg["cap_f"], sink_size=cfg["sink_f"],
         num_frame_per_block=cfg["chunk_f"],
         cache_dtype=torch.float8_e4m3fn if cfg["cache"] == "fp8" else None,
+        rope=RopeConfig(grid_hw=cfg["grid"]) if rope else None,
     )
     return alloc(cfg["batch"], dtype=torch.bfloat16, device=device)
 
@@ -135,12 +138,52 @@ def run_ours(cfg, inputs, caches, chunk_ids):
                 apply_cache_updates(caches, infos)
 
 
-def reference_gpu_step(cfg, inputs, dense, chunk_ids):
+def _ref_rope_frames(x, grid, positions, freqs):
+    """The reference's window RoPE of one part of the window (echorope_apply,
+    causal_model.py:88-197): float64 complex multiply by the table rows of each frame's temporal
+    position and each token's (h, w), cast back to x's dtype."""
+    import torch
+
+    gh, gw = grid
+    B, L, n, D = x.shape
+    F = len(positions)
+    ct, ch, cw = 22, 21, 21
+    ft, fh, fw = freqs.split([ct, ch, cw], dim=1)
+    pos = torch.tensor(list(positions), device=x.device)
+    f_all = torch.cat([ft[pos].view(F, 1, 1, ct).expand(F, gh, gw, ct),
+                       fh[:gh].view(1, gh, 1, ch).expand(F, gh, gw, ch),
+                       fw[:gw].view(1, 1, gw, cw).expand(F, gh, gw, cw)], dim=-1).reshape(L, 1, -1)
+    xc = torch.view_as_complex(x.to(torch.float64).reshape(B, L, n, D // 2, 2))
+    return torch.view_as_real(xc * f_all).reshape(B, L, n, D).to(x.dtype)
+
+
+def _ref_freqs(device):
+    """Wan's complex RoPE table (model.py:28-35, causal_model.py:1855-1866) on the GPU."""
+    import torch
+
+    def params(dim):
+        inv = 1.0 / torch.pow(torch.tensor(10000.0, dtype=torch.float64),
+                              torch.arange(0, dim, 2, dtype=torch.float64) / dim)
+        ang = torch.outer(torch.arange(1024, dtype=torch.float64), inv)
+        return torch.polar(torch.ones_like(ang), ang)
+
+    return torch.cat([params(44), params(42), params(42)], dim=1).to(device)
+
+
+def reference_gpu_step(cfg, inputs, dense, chunk_ids, rope=False):
     """The reference's per-layer op sequence on the GPU with PyTorch-ROCm: clone the cache,
     memmove the non-sink window, slice-assign the chunk, cat sink|local, SDPA; deferred commit
-    repeats memmove + assign (causal_model.py:1028-1226, :2856-2921)."""
+    repeats memmove + assign (causal_model.py:1028-1226, :2856-2921).  With ``rope`` the cache
+    is pre-RoPE and the sink, local window and queries are re-roped in float64 every pass
+    (_rope_sink_local_and_query, causal_model.py:791-876)."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from solarwm_amd import RopeConfig
+    from solarwm_amd.rope import positions as rope_positions
+
+    freqs = _ref_freqs(inputs[0][0].device) if rope else None
+    rcfg = RopeConfig(grid_hw=cfg["grid"]) if rope else None
 
     T, Lq = cfg["T"], cfg["chunk_f"] * cfg["T"]
     sink = cfg["sink_f"] * T
@@ -169,11 +212,20 @@ def reference_gpu_step(cfg, inputs, dense, chunk_ids):
                 tv[:, ls:nle] = v
                 a_s = min(sink, nle)
                 lsw = max(sink, nle - (cap - sink))
-                kc = torch.cat([tk[:, :a_s], tk[:, lsw:nle]], dim=1)
+                k_sink, k_loc, qr = tk[:, :a_s], tk[:, lsw:nle], q
+                if rope:
+                    qpos, kpos = rope_positions(
+                        rcfg, num_sink_frames=a_s // T, num_local_frames=(nle - lsw) // T,
+                        num_new_frames=Lq // T, max_attention_size=cap, frame_tokens=T,
+                        current_start_frame=cs // T, sink_branch=True)
+                    qr = _ref_rope_frames(q, cfg["grid"], qpos, freqs)
+                    k_sink = _ref_rope_frames(k_sink, cfg["grid"], kpos[: a_s // T], freqs)
+                    k_loc = _ref_rope_frames(k_loc, cfg["grid"], kpos[a_s // T :], freqs)
+                kc = torch.cat([k_sink, k_loc], dim=1)
                 vc = torch.cat([tv[:, :a_s], tv[:, lsw:nle]], dim=1)
                 with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                     x = torch.nn.functional.scaled_dot_product_attention(
-                        q.transpose(1, 2).contiguous(), kc.transpose(1, 2).contiguous(),
+                        qr.transpose(1, 2).contiguous(), kc.transpose(1, 2).contiguous(),
                         vc.transpose(1, 2).contiguous(),
                     ).transpose(1, 2).contiguous()
                 ups.append((layer, ev, ro, ls, nle, ce, k, v))
@@ -316,24 +368,64 @@ def probe(cfg, device, iters=20):
     log(f"[probe] copy 1 GiB x3, append x{iters} ({Lq} tokens), attention x{iters} (Lq {Lq}, Lk {n * T})")
 
 
-def steady_state(name, device, fill=7, timed=3):
-    """Configs 3 and 5: fill the 21-frame window (chunks 0..fill-1, untimed), then time `timed`
-    steady-state chunks (4 none + 1 commit passes over all layers)."""
+def steady_state(name, device, fill=7, timed=3, rope=False):
+    """Configs 3 and 5 (and config 2 with RoPE on load): fill the 21-frame window (chunks
+    0..fill-1, untimed), then time `timed` steady-state chunks (4 none + 1 commit passes over all
+    layers)."""
     import torch
 
     cfg = CONFIGS[name]
     inputs = make_inputs(cfg, device, outliers=cfg["cache"] == "fp8")
-    caches = make_caches(cfg, device)
+    caches = make_caches(cfg, device, rope=rope)
     run_ours(cfg, inputs, caches, range(fill))
     st = timed_rollout(cfg, inputs, caches, range(fill, fill + timed))
     st["workload"] = (
         f"{cfg['workload']}: {cfg['layers']} layers, H{cfg['heads']}xD128, {cfg['T']} tok/frame, "
         f"Lq {cfg['chunk_f'] * cfg['T']}, window {cfg['cap_f'] * cfg['T']} keys, batch "
-        f"{cfg['batch']}, {cfg['cache']} cache; chunks {fill}..{fill + timed - 1} (steady state)"
+        f"{cfg['batch']}, {cfg['cache']} cache{', pre-RoPE cache (RoPE on load)' if rope else ''}; "
+        f"chunks {fill}..{fill + timed - 1} (steady state)"
     )
     del inputs, caches
     torch.cuda.empty_cache()
     return st
+
+
+def c2_rope(device, fill=7, timed=2):
+    """Config 2 with a pre-RoPE cache, as the reference keeps it: ours (RoPE applied on load by
+    the kernels) against the reference op sequence that re-ropes the window in float64 every
+    pass, both over steady-state chunks."""
+    import torch
+
+    ours = steady_state("c2", device, fill=fill, timed=timed, rope=True)
+    cfg = CONFIGS["c2"]
+    inputs = make_inputs(cfg, device)
+    T = cfg["T"]
+    # the reference's caches start full (global = local end = the 21-frame window), the state
+    # after `fill` chunks; the timed chunks then evict and re-rope exactly as in steady state
+    full = cfg["cap_f"] * T
+    dense = [
+        {"k": torch.zeros(cfg["batch"], full, cfg["heads"], 128, dtype=torch.bfloat16, device=device),
+         "v": torch.zeros(cfg["batch"], full, cfg["heads"], 128, dtype=torch.bfloat16, device=device),
+         "g": fill * cfg["chunk_f"] * T, "l": full}
+        for _ in range(cfg["layers"])
+    ]
+    reference_gpu_step(cfg, inputs, dense, range(fill, fill + 1), rope=True)  # warm
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reference_gpu_step(cfg, inputs, dense, range(fill + 1, fill + 1 + timed), rope=True)
+    torch.cuda.synchronize()
+    rfps = cfg["chunk_f"] * timed / (time.perf_counter() - t0)
+    del dense, inputs
+    torch.cuda.empty_cache()
+    return {
+        "frames_per_s": round(ours["frames_per_s"], 4),
+        "attn_tflops": round(ours["attn_tflops"], 1),
+        "attn_avg_ms": round(ours["attn_avg_ms"], 4),
+        "reference_gpu_frames_per_s": round(rfps, 4),
+        "speedup": round(ours["frames_per_s"] / rfps, 3),
+        "workload": ours["workload"],
+        "note": "reference = the same op sequence with its float64 window re-rope per pass",
+    }
 
 
 def c5_quality(device):
@@ -579,6 +671,9 @@ def main():
             r = steady_state(name, dev)
             aux[name] = {k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in r.items()}
             log(f"[bench] aux {name}: {aux[name]}")
+        log("[bench] aux c2 with RoPE on load")
+        aux["c2_rope"] = c2_rope(dev)
+        log(f"[bench] aux c2_rope: {aux['c2_rope']}")
         log("[bench] aux c5: fp8 vs bf16 quality")
         aux["c5"]["quality"] = c5_quality(dev)
         log(f"[bench] aux c5 quality: {aux['c5']['quality']}")
