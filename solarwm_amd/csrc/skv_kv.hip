@@ -141,6 +141,141 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   }
 }
 
+// fp8 append with the frame held on chip (bf16 sources, Tp <= 64 * kFp8OnChip): one
+// 1024-thread workgroup per (frame, batch, head, K|V); thread t owns chunk j = 16 B of row
+// 64 j + t / 16, channels (t % 16) * 8 .. +8.  Every chunk of the frame is loaded at once (one
+// HBM read, all loads in flight): the first kFp8RegChunks into registers, the rest straight into
+// LDS (buffer_load ... lds, 16 KB per chunk).  The workgroup reduces the absmax and the codes
+// come from the hardware e4m3 convert, which on clamped inputs gives exactly the
+// round-to-nearest-even codes of f32_to_e4m3.  V^T tiles go through a double-buffered LDS tile
+// (one barrier per tile).
+constexpr int kFp8RegChunks = 18;
+constexpr int kFp8LdsChunks = 7;
+constexpr int kFp8OnChip = kFp8RegChunks + kFp8LdsChunks;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ inline uint32_t e4m3x4(float a, float b, float c, float d) {
+  int v = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, v, true);
+  return (uint32_t)v;
+}
+
+__device__ inline u32x2 quant8(const u32x4& r, float inv) {
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(r[i] << 16);
+    f[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = fminf(fmaxf(f[i] * inv, -448.0f), 448.0f);
+  return u32x2{e4m3x4(f[0], f[1], f[2], f[3]), e4m3x4(f[4], f[5], f[6], f[7])};
+}
+
+// |x| of a bf16 is its bits & 0x7fff, and non-negative bf16 order as integers: the absmax runs
+// on packed 16-bit integer maxima (no unpacking to fp32, which would double the live state)
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ inline u16x2 absmax8(const u32x4& r, u16x2 m) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, r[i] & 0x7fff7fffu));
+  return m;
+}
+
+__global__ __launch_bounds__(1024) void append_fp8_reg_kernel(AppendArgs a) {
+  constexpr int kRowT = kTile + 4;  // V^T tile row: 64 tokens + 4 bytes of skew
+  constexpr int kChunkBytes = 1024 * 16;
+  __shared__ float red[32];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kFp8LdsChunks * kChunkBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vt8[2][kHeadDim * kRowT];
+  int wg = blockIdx.x;
+  const int is_v = wg & 1;
+  wg >>= 1;
+  const int h = wg % a.H;
+  wg /= a.H;
+  const int b = wg % a.B;
+  const int f = wg / a.B;
+  const int64_t slot = a.slots[f];
+  const int tid = threadIdx.x;
+  const int rr = tid >> 4, col = (tid & 15) * 8;
+  const bf16* src = static_cast<const bf16*>(is_v ? a.vsrc : a.ksrc) + (int64_t)b * a.s_sb +
+                    (int64_t)h * a.s_sh + (int64_t)(a.src_frame0 + f) * a.T * a.s_st;
+  // one buffer descriptor per frame: the lane's byte offset is a single VGPR (no 64-bit
+  // address per load); the host guarantees the frame spans < 2^31 bytes.  Rows >= T are never
+  // loaded (their register chunks are zero, their LDS chunks are masked on read).
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, 0x7fffffff, 0x00020000);
+  const uint32_t lane_off = (uint32_t)(rr * a.s_st + col) * 2u;
+  const uint32_t row_step = (uint32_t)(kTile * a.s_st) * 2u;
+  const int nt = a.ntiles;
+  uint8_t* my_stage = stage + tid * 16;
+#pragma unroll
+  for (int c = 0; c < kFp8LdsChunks; ++c) {
+    const int j = kFp8RegChunks + c;
+    if (j < nt && kTile * j + rr < a.T)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (lds_void_t*)(stage + c * kChunkBytes + (tid >> 6) * 1024), 16,
+          lane_off + j * row_step, 0, 0, 0);
+  }
+  u32x4 r[kFp8RegChunks];
+#pragma unroll
+  for (int j = 0; j < kFp8RegChunks; ++j) {
+    r[j] = u32x4{0u, 0u, 0u, 0u};
+    if (j < nt && kTile * j + rr < a.T)
+      r[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off + j * row_step, 0, 0));
+  }
+  // chunk j of this thread wherever it lives, zero for rows >= T
+  auto chunk = [&](int j) -> u32x4 {
+    if (j < kFp8RegChunks) return r[j];
+    return (kTile * j + rr < a.T) ? *reinterpret_cast<const u32x4*>(my_stage + (j - kFp8RegChunks) * kChunkBytes)
+                                  : u32x4{0u, 0u, 0u, 0u};
+  };
+  u16x2 mm = {0, 0};
+#pragma unroll
+  for (int j = 0; j < kFp8RegChunks; ++j) mm = absmax8(r[j], mm);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS chunks have landed
+#pragma unroll
+  for (int j = kFp8RegChunks; j < kFp8OnChip; ++j)
+    if (j < nt) mm = absmax8(chunk(j), mm);
+  float m = __uint_as_float((uint32_t)(mm[0] > mm[1] ? mm[0] : mm[1]) << 16);
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  if (tid < 64) {
+    float x = tid < 16 ? red[tid] : 0.f;
+    for (int off = 8; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    if (tid == 0) red[16] = x;
+  }
+  __syncthreads();
+  const float amax = red[16];
+  const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+  if (tid == 0) {
+    float* sc = is_v ? a.vscale : a.kscale;
+    sc[(slot * a.B + b) * a.H + h] = amax / 448.0f;
+  }
+  uint8_t* pool = static_cast<uint8_t*>(is_v ? a.vpool : a.kpool) + slot * a.slot_stride +
+                  (int64_t)(b * a.H + h) * a.Tp * kHeadDim;
+  if (!is_v) {
+#pragma unroll
+    for (int j = 0; j < kFp8OnChip; ++j)
+      if (j < nt)  // rows T..Tp-1 hold zeros -> code 0
+        *reinterpret_cast<u32x2*>(pool + (int64_t)(kTile * j + rr) * kHeadDim + col) = quant8(chunk(j), inv);
+    return;
+  }
+  const int d = tid >> 3, tc = (tid & 7) * 8;
+#pragma unroll
+  for (int j = 0; j < kFp8OnChip; ++j) {
+    if (j >= nt) break;
+    uint8_t* buf = vt8[j & 1];
+    const u32x2 q = quant8(chunk(j), inv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) buf[(col + i) * kRowT + rr] = (uint8_t)(q[i >> 2] >> (8 * (i & 3)));
+    __syncthreads();  // buf[j & 1] complete; every read of it two tiles ago is done
+    const uint32_t* rd = reinterpret_cast<const uint32_t*>(buf + d * kRowT + tc);
+    *reinterpret_cast<u32x2*>(pool + (int64_t)d * a.Tp + kTile * j + tc) = u32x2{rd[0], rd[1]};
+  }
+}
+
 // fp8 append: one workgroup per (frame, batch, head, K|V).  Pass 1 reduces absmax over the
 // frame's T x 128 values; pass 2 re-reads them (L2/MALL resident), quantises with
 // inv = 448 / absmax and stores e4m3fn codes (V transposed through LDS).
@@ -433,7 +568,11 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fp8) {
     dim3 grid(n_frames * batch * heads * 2);
-    if (src_dtype == SKV_BF16)
+    const bool reg_path = src_dtype == SKV_BF16 && a.ntiles <= kFp8OnChip &&
+                          (int64_t)a.Tp * src_st * 2 < ((int64_t)1 << 31);
+    if (reg_path)
+      hipLaunchKernelGGL(append_fp8_reg_kernel, grid, dim3(1024), 0, s, a);
+    else if (src_dtype == SKV_BF16)
       hipLaunchKernelGGL(append_fp8_kernel<bf16>, grid, dim3(1024), 0, s, a);
     else
       hipLaunchKernelGGL(append_fp8_kernel<float>, grid, dim3(1024), 0, s, a);

@@ -57,10 +57,15 @@ def test_append_gather_roundtrip_and_layout(gpu, dtype, B, H, T):
 
 
 @pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("B,H,T", [(1, 12, 1560), (4, 2, 390), (1, 3, 100)])
-def test_fp8_append_matches_oracle(gpu, src_dtype, B, H, T):
-    _say("fp8 append", src_dtype, B, H, T)
-    x = _rand((B, 2 * T, H, 128), seed=11, dtype=torch.float32)
+@pytest.mark.parametrize("B,H,T,wide", [(1, 12, 1560, False), (4, 2, 390, False),
+                                        (1, 3, 100, False), (2, 2, 1560, True),
+                                        (1, 2, 1700, False), (1, 2, 1153, True)])
+def test_fp8_append_matches_oracle(gpu, src_dtype, B, H, T, wide):
+    """Frames of up to 25 tiles go through the on-chip kernel (bf16 sources), longer frames and
+    f32 sources through the two-pass kernel; ``wide``: the source is a head slice of a wider
+    tensor (token stride > H * 128)."""
+    _say("fp8 append", src_dtype, B, H, T, wide)
+    x = _rand((B, 2 * T, H + 3 if wide else H, 128), seed=11, dtype=torch.float32)[:, :, :H]
     g = torch.Generator().manual_seed(12)
     outlier = torch.randperm(128, generator=g)[:2]
     x[..., outlier] *= 20.0
@@ -68,8 +73,14 @@ def test_fp8_append_matches_oracle(gpu, src_dtype, B, H, T):
     x = x.to(src_dtype)
     v = (x * -0.5).to(src_dtype)
     kpool, vpool, ks, vs = kernels.new_pools(4, B, H, T, torch.float8_e4m3fn, gpu)
-    kernels.append_frames(x.to(gpu), v.to(gpu), kpool, vpool, [2, 1], frame_tokens=T,
-                          kscale=ks, vscale=vs)
+    kpool.view(torch.uint8).fill_(0x55), vpool.view(torch.uint8).fill_(0x55)  # stale slots
+    xd, vd = x.to(gpu), v.to(gpu)
+    if wide:  # keep the head-slice strides on the device
+        xd, vd = (torch.zeros((B, 2 * T, H + 3, 128), dtype=src_dtype, device=gpu)[:, :, :H]
+                  for _ in range(2))
+        xd.copy_(x), vd.copy_(v)
+        assert xd.stride(1) == (H + 3) * 128
+    kernels.append_frames(xd, vd, kpool, vpool, [2, 1], frame_tokens=T, kscale=ks, vscale=vs)
     torch.cuda.synchronize()
     for f, s in enumerate([2, 1]):
         for src, pool, sc, vt in ((x, kpool, ks, False), (v, vpool, vs, True)):
@@ -79,6 +90,8 @@ def test_fp8_append_matches_oracle(gpu, src_dtype, B, H, T):
             got = got[..., :T].transpose(-1, -2) if vt else got[:, :, :T]
             assert torch.equal(got.view(torch.uint8), codes.view(torch.uint8)), (f, vt)
             assert torch.equal(sc[s].cpu(), scale), (f, vt)
+            pad = pool[s][..., T:] if vt else pool[s][:, :, T:]
+            assert int(pad.view(torch.uint8).count_nonzero()) == 0, (f, vt)  # rows T..Tp-1
 
 
 def _pool_from(k, v, T, dtype, device, perm_seed=0):
