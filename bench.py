@@ -74,22 +74,44 @@ def make_inputs(cfg, device, seed=1234, outliers=False):
     return out
 
 
-def make_caches(cfg, device, rope=False):
+def make_caches(cfg, device, rope=False, prope=False):
     import torch
 
-    from solarwm_amd import RopeConfig, make_kv_cache_allocator
+    from solarwm_amd import PropeConfig, RopeConfig, make_kv_cache_allocator
 
     alloc = make_kv_cache_allocator(
         num_layers=cfg["layers"], num_heads=cfg["heads"], head_dim=128,
         frame_sequence_length=cfg["T"], local_attn_size=cfg["cap_f"], sink_size=cfg["sink_f"],
         num_frame_per_block=cfg["chunk_f"],
         cache_dtype=torch.float8_e4m3fn if cfg["cache"] == "fp8" else None,
-        rope=RopeConfig(grid_hw=cfg["grid"]) if rope else None,
+        rope=RopeConfig(grid_hw=cfg["grid"]) if rope or prope else None,
+        prope=PropeConfig() if prope else None,
     )
     return alloc(cfg["batch"], dtype=torch.bfloat16, device=device)
 
 
-def timed_rollout(cfg, inputs, caches, chunk_ids):
+def camera_trajectory(cfg, frames, device, seed=11):
+    """Per-latent-frame cameras [B, F, 4, 4] / [B, F, 3, 3] (float32): a slow pan (yaw up to
+    ~0.05 rad per frame) with a forward walk, and the data path's intrinsics
+    (data.py:516-530: fx = 969.7/1920, fy = 969.7/1080, principal point 0.5)."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    B = cfg["batch"]
+    yaw = torch.cumsum(torch.rand(B, frames, generator=g, dtype=torch.float64) * 0.05, dim=1)
+    v = torch.zeros(B, frames, 4, 4, dtype=torch.float64)
+    v[..., 0, 0], v[..., 0, 2] = yaw.cos(), yaw.sin()
+    v[..., 2, 0], v[..., 2, 2] = -yaw.sin(), yaw.cos()
+    v[..., 1, 1] = v[..., 3, 3] = 1.0
+    v[..., 2, 3] = -0.1 * torch.arange(frames, dtype=torch.float64)
+    k = torch.zeros(B, frames, 3, 3, dtype=torch.float64)
+    k[..., 0, 0], k[..., 1, 1] = 969.6969696969696 / 1920.0, 969.6969696969696 / 1080.0
+    k[..., 0, 2] = k[..., 1, 2] = 0.5
+    k[..., 2, 2] = 1.0
+    return v.float().to(device), k.float().to(device)
+
+
+def timed_rollout(cfg, inputs, caches, chunk_ids, cams=None):
     """Run chunks with HIP events around every launch; returns the measured figures."""
     import torch
 
@@ -98,7 +120,7 @@ def timed_rollout(cfg, inputs, caches, chunk_ids):
     with kernels.timed_launches() as tm:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        run_ours(cfg, inputs, caches, chunk_ids)
+        run_ours(cfg, inputs, caches, chunk_ids, cams)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     n_attn, attn_ms, attn_flops = tm.summary("attention")
@@ -122,20 +144,26 @@ def timed_rollout(cfg, inputs, caches, chunk_ids):
     }
 
 
-def run_ours(cfg, inputs, caches, chunk_ids):
-    from solarwm_amd import apply_cache_updates, attend_cached
+def run_ours(cfg, inputs, caches, chunk_ids, cams=None):
+    """Our path over chunks; ``cams`` (per-frame viewmats, K) stages one fused-PRoPE camera
+    pass per forward for all layers."""
+    from solarwm_amd import apply_cache_updates, attend_cached, commit_camera_cache, stage_camera_cache
 
     Lq = cfg["chunk_f"] * cfg["T"]
     outs = [None] * cfg["layers"]
     for c in chunk_ids:
         for policy in PASSES:
             infos = []
+            cp = None
+            if cams is not None:
+                cp = stage_camera_cache(caches, cams[0], cams[1], c * Lq, Lq, per_frame=True)
             for layer, (q, k, v) in enumerate(inputs):
-                x, upd = attend_cached(q, k, v, caches[layer], c * Lq, out=outs[layer])
+                x, upd = attend_cached(q, k, v, caches[layer], c * Lq, out=outs[layer], camera=cp)
                 outs[layer] = x
                 infos.append((layer, upd))
             if policy != "none":
                 apply_cache_updates(caches, infos)
+                commit_camera_cache(cp)
 
 
 def _ref_rope_frames(x, grid, positions, freqs):
@@ -170,12 +198,51 @@ def _ref_freqs(device):
     return torch.cat([params(44), params(42), params(42)], dim=1).to(device)
 
 
-def reference_gpu_step(cfg, inputs, dense, chunk_ids, rope=False):
+def _ref_projection(viewmats, ks):
+    """The reference's per-token PRoPE matrices in float32 (camera_prope.py:206-231,
+    :307-338): P = lift(K_norm) V, P⁻¹ = V⁻¹ lift(K_norm⁻¹)."""
+    import torch
+
+    kn = torch.zeros_like(ks)
+    kn[..., 0, 0], kn[..., 1, 1], kn[..., 2, 2] = ks[..., 0, 0], ks[..., 1, 1], 1.0
+    lift = torch.zeros(ks.shape[:-2] + (4, 4), dtype=ks.dtype, device=ks.device)
+    lift[..., :3, :3] = kn
+    lift[..., 3, 3] = 1.0
+    kinv = torch.zeros_like(ks)
+    kinv[..., 0, 0], kinv[..., 1, 1], kinv[..., 2, 2] = 1.0 / kn[..., 0, 0], 1.0 / kn[..., 1, 1], 1.0
+    lift_inv = torch.zeros_like(lift)
+    lift_inv[..., :3, :3] = kinv
+    lift_inv[..., 3, 3] = 1.0
+    rt = viewmats[..., :3, :3].transpose(-1, -2)
+    vinv = torch.zeros_like(viewmats)
+    vinv[..., :3, :3] = rt
+    vinv[..., :3, 3] = -torch.einsum("...ij,...j->...i", rt, viewmats[..., :3, 3])
+    vinv[..., 3, 3] = 1.0
+    p = torch.einsum("...ij,...jk->...ik", lift, viewmats)
+    return p, torch.einsum("...ij,...jk->...ik", vinv, lift_inv)
+
+
+def _ref_tiled(feats, mats):
+    """_apply_tiled_projmat's per-ray branch (camera_prope.py:234-256) on [B, L, H, D]:
+    matrix cast to the features' dtype, one 4x4 per token over every 4-channel group."""
+    import torch
+
+    B, L, H, D = feats.shape
+    f = feats.transpose(1, 2).reshape(B, H, L, D // 4, 4)
+    out = torch.einsum("btij,bntpj->bntpi", mats.to(feats.dtype), f)
+    return out.reshape(B, H, L, D).transpose(1, 2)
+
+
+def reference_gpu_step(cfg, inputs, dense, chunk_ids, rope=False, cams=None):
     """The reference's per-layer op sequence on the GPU with PyTorch-ROCm: clone the cache,
     memmove the non-sink window, slice-assign the chunk, cat sink|local, SDPA; deferred commit
     repeats memmove + assign (causal_model.py:1028-1226, :2856-2921).  With ``rope`` the cache
     is pre-RoPE and the sink, local window and queries are re-roped in float64 every pass
-    (_rope_sink_local_and_query, causal_model.py:791-876)."""
+    (_rope_sink_local_and_query, causal_model.py:791-876).  With ``cams`` (per-frame viewmats, K)
+    the fused PRoPE mode runs too: the camera cache is staged once per forward
+    (causal_model.py:1948-2066: clone, roll, write) and every layer builds per-token P / P⁻¹ of
+    its window and applies them with bf16 einsums (causal_model.py:1170-1199 ->
+    camera_prope.py:93-256)."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
@@ -192,6 +259,22 @@ def reference_gpu_step(cfg, inputs, dense, chunk_ids, rope=False):
         cs = c * Lq
         for policy in PASSES:
             ups = []
+            if cams is not None:
+                st0 = dense[0]
+                cv = cams[0][:, cs // T : cs // T + Lq // T].repeat_interleave(T, dim=1)
+                ck = cams[1][:, cs // T : cs // T + Lq // T].repeat_interleave(T, dim=1)
+                tcv, tck = st0["cv"].clone(), st0["ck"].clone()
+                ge, le = st0["g"], st0["l"]
+                if cs + Lq > ge and Lq + le > cap:
+                    ev = Lq + le - cap
+                    ro = le - ev - sink
+                    nle = le + cs + Lq - ge - ev
+                    tcv[:, sink : sink + ro] = tcv[:, sink + ev : sink + ev + ro].clone()
+                    tck[:, sink : sink + ro] = tck[:, sink + ev : sink + ev + ro].clone()
+                else:
+                    nle = le + cs + Lq - ge
+                tcv[:, nle - Lq : nle] = cv
+                tck[:, nle - Lq : nle] = ck
             for layer, (q, k, v) in enumerate(inputs):
                 st = dense[layer]
                 ge, le = st["g"], st["l"]
@@ -223,11 +306,20 @@ def reference_gpu_step(cfg, inputs, dense, chunk_ids, rope=False):
                     k_loc = _ref_rope_frames(k_loc, cfg["grid"], kpos[a_s // T :], freqs)
                 kc = torch.cat([k_sink, k_loc], dim=1)
                 vc = torch.cat([tv[:, :a_s], tv[:, lsw:nle]], dim=1)
+                if cams is not None:
+                    wv = torch.cat([tcv[:, :a_s], tcv[:, lsw:nle]], dim=1)
+                    wk = torch.cat([tck[:, :a_s], tck[:, lsw:nle]], dim=1)
+                    p_q, _ = _ref_projection(cv, ck)
+                    _, p_kinv = _ref_projection(wv, wk)
+                    qr = _ref_tiled(qr, p_q.transpose(-1, -2))
+                    kc, vc = _ref_tiled(kc, p_kinv), _ref_tiled(vc, p_kinv)
                 with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                     x = torch.nn.functional.scaled_dot_product_attention(
                         qr.transpose(1, 2).contiguous(), kc.transpose(1, 2).contiguous(),
                         vc.transpose(1, 2).contiguous(),
                     ).transpose(1, 2).contiguous()
+                if cams is not None:
+                    x = _ref_tiled(x, p_q)
                 ups.append((layer, ev, ro, ls, nle, ce, k, v))
                 del x
             if policy != "none":
@@ -239,6 +331,9 @@ def reference_gpu_step(cfg, inputs, dense, chunk_ids, rope=False):
                     st["k"][:, ls:nle] = k
                     st["v"][:, ls:nle] = v
                     st["g"], st["l"] = ce, nle
+                if cams is not None:
+                    dense[0]["cv"].copy_(tcv)
+                    dense[0]["ck"].copy_(tck)
 
 
 def cpu_baseline(cfg):
@@ -368,7 +463,7 @@ def probe(cfg, device, iters=20):
     log(f"[probe] copy 1 GiB x3, append x{iters} ({Lq} tokens), attention x{iters} (Lq {Lq}, Lk {n * T})")
 
 
-def steady_state(name, device, fill=7, timed=3, rope=False):
+def steady_state(name, device, fill=7, timed=3, rope=False, prope=False):
     """Configs 3 and 5 (and config 2 with RoPE on load): fill the 21-frame window (chunks
     0..fill-1, untimed), then time `timed` steady-state chunks (4 none + 1 commit passes over all
     layers)."""
@@ -376,13 +471,15 @@ def steady_state(name, device, fill=7, timed=3, rope=False):
 
     cfg = CONFIGS[name]
     inputs = make_inputs(cfg, device, outliers=cfg["cache"] == "fp8")
-    caches = make_caches(cfg, device, rope=rope)
-    run_ours(cfg, inputs, caches, range(fill))
-    st = timed_rollout(cfg, inputs, caches, range(fill, fill + timed))
+    caches = make_caches(cfg, device, rope=rope, prope=prope)
+    cams = camera_trajectory(cfg, (fill + timed) * cfg["chunk_f"], device) if prope else None
+    run_ours(cfg, inputs, caches, range(fill), cams)
+    st = timed_rollout(cfg, inputs, caches, range(fill, fill + timed), cams)
     st["workload"] = (
         f"{cfg['workload']}: {cfg['layers']} layers, H{cfg['heads']}xD128, {cfg['T']} tok/frame, "
         f"Lq {cfg['chunk_f'] * cfg['T']}, window {cfg['cap_f'] * cfg['T']} keys, batch "
-        f"{cfg['batch']}, {cfg['cache']} cache{', pre-RoPE cache (RoPE on load)' if rope else ''}; "
+        f"{cfg['batch']}, {cfg['cache']} cache{', pre-RoPE cache (RoPE on load)' if rope else ''}"
+        f"{', pre-RoPE camera-aware cache (RoPE + fused PRoPE on load)' if prope else ''}; "
         f"chunks {fill}..{fill + timed - 1} (steady state)"
     )
     del inputs, caches
@@ -390,13 +487,15 @@ def steady_state(name, device, fill=7, timed=3, rope=False):
     return st
 
 
-def c2_rope(device, fill=7, timed=2):
+def c2_rope(device, fill=7, timed=2, prope=False):
     """Config 2 with a pre-RoPE cache, as the reference keeps it: ours (RoPE applied on load by
     the kernels) against the reference op sequence that re-ropes the window in float64 every
-    pass, both over steady-state chunks."""
+    pass, both over steady-state chunks.  ``prope``: the fused-PRoPE camera mode on top
+    (one camera per latent frame, a slow pan), against the reference's per-layer per-token
+    camera matrices and bf16 einsums."""
     import torch
 
-    ours = steady_state("c2", device, fill=fill, timed=timed, rope=True)
+    ours = steady_state("c2", device, fill=fill, timed=timed, rope=True, prope=prope)
     cfg = CONFIGS["c2"]
     inputs = make_inputs(cfg, device)
     T = cfg["T"]
@@ -409,10 +508,16 @@ def c2_rope(device, fill=7, timed=2):
          "g": fill * cfg["chunk_f"] * T, "l": full}
         for _ in range(cfg["layers"])
     ]
-    reference_gpu_step(cfg, inputs, dense, range(fill, fill + 1), rope=True)  # warm
+    cams = None
+    if prope:
+        cams = camera_trajectory(cfg, (fill + 1 + timed) * cfg["chunk_f"], device)
+        # camera cache rows of the full window: valid matrices (frame 0's camera)
+        dense[0]["cv"] = cams[0][:, :1].expand(-1, full, -1, -1).contiguous()
+        dense[0]["ck"] = cams[1][:, :1].expand(-1, full, -1, -1).contiguous()
+    reference_gpu_step(cfg, inputs, dense, range(fill, fill + 1), rope=True, cams=cams)  # warm
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    reference_gpu_step(cfg, inputs, dense, range(fill + 1, fill + 1 + timed), rope=True)
+    reference_gpu_step(cfg, inputs, dense, range(fill + 1, fill + 1 + timed), rope=True, cams=cams)
     torch.cuda.synchronize()
     rfps = cfg["chunk_f"] * timed / (time.perf_counter() - t0)
     del dense, inputs
@@ -424,7 +529,8 @@ def c2_rope(device, fill=7, timed=2):
         "reference_gpu_frames_per_s": round(rfps, 4),
         "speedup": round(ours["frames_per_s"] / rfps, 3),
         "workload": ours["workload"],
-        "note": "reference = the same op sequence with its float64 window re-rope per pass",
+        "note": ("reference = the same op sequence with its float64 window re-rope per pass"
+                 + (" and per-layer per-token PRoPE matrices applied by bf16 einsums" if prope else "")),
     }
 
 
@@ -674,6 +780,8 @@ def main():
         log("[bench] aux c2 with RoPE on load")
         aux["c2_rope"] = c2_rope(dev)
         log(f"[bench] aux c2_rope: {aux['c2_rope']}")
+        aux["c2_prope"] = c2_rope(dev, prope=True)
+        log(f"[bench] aux c2_prope: {aux['c2_prope']}")
         log("[bench] aux c5: fp8 vs bf16 quality")
         aux["c5"]["quality"] = c5_quality(dev)
         log(f"[bench] aux c5 quality: {aux['c5']['quality']}")

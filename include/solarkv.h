@@ -138,6 +138,48 @@ int skv_attention_rope(const void* q, int q_dtype, int64_t q_sb, int64_t q_st, i
                        int64_t out_sh, const float* rope_hw, int grid_h, int grid_w,
                        const float* rope_t, int n_qframes, skv_stream_t stream);
 
+/*
+ * Fused PRoPE on top of RoPE on load (camera-conditioned caches).  The reference's fused mode
+ * keeps raw K/V plus a camera cache with the same token layout, re-ropes the window and then
+ * applies PRoPE: q' = P_qᵀ q, k' = P_k⁻¹ k, v' = P_k⁻¹ v on every group of 4 head channels
+ * (P = lift(K_norm) · viewmat of the token's camera), attends, and maps the output back with P_q
+ * (causal_model.py:585-651, :1170-1199 → camera_prope.py:93-261; camera cache
+ * causal_model.py:1948-2075).  Cameras are per latent frame (the data path expands one camera
+ * per frame to every token, data.py:516-530).  Matrices are row-major 4x4 float32.
+ *
+ * skv_append_prope — skv_append_rope (bf16 pools) that also applies P_k⁻¹ of each written frame's
+ * camera, kv_xform[f][b] (device, [n_frames][batch][16]): kx_pool receives K with its
+ * height/width pairs rotated and then P_k⁻¹ on channel groups 11..31 (channels 44..127; groups
+ * 0..10 hold temporal pairs and stay raw), vx_pool receives P_k⁻¹ v on every group (V layout).
+ * k_pool / v_pool receive the raw frames exactly as skv_append writes them.
+ */
+int skv_append_prope(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
+                     int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool, void* v_pool,
+                     int pool_dtype, int n_slots, const int32_t* dst_slots /* host */,
+                     int n_frames, int batch, int heads, int head_dim, int frame_tokens,
+                     void* kx_pool, void* vx_pool, const float* rope_hw, int grid_h, int grid_w,
+                     const float* kv_xform, skv_stream_t stream);
+
+/*
+ * skv_attention_prope — skv_attention_rope over kx_pool / vx_pool (written by skv_append_prope)
+ * with un-roped queries; frame_tokens >= 64.  Device tables, for query frame f of stream b and
+ * key frame j of the list:
+ *   q_xform_t [b][j][f][11][16]  W = R_k(p_k)ᵀ (P_q P_k⁻¹)ᵀ R_q(p_q) per temporal group g < 11,
+ *                                R = the group's two temporal RoPE rotations (angles p·θ^(-2i/44))
+ *   q_xform_s [b][f][16]         P_qᵀ, applied to the spatial groups after their RoPE rotation
+ *   out_xform [b][f][16]         P_q, applied to every group of the output
+ * Scores equal those of the reference's RoPE-then-PRoPE queries and keys; the output is P_q o.
+ */
+int skv_attention_prope(const void* q, int q_dtype, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                        const void* kx_pool, const void* vx_pool, int pool_dtype, int n_slots,
+                        const int32_t* frame_slots /* host */, int n_frames, int batch,
+                        int heads, int head_dim, int q_len, int frame_tokens,
+                        float softmax_scale, int mask_mode, int64_t q_pos0,
+                        int64_t chunk_tokens, void* out, int64_t out_sb, int64_t out_st,
+                        int64_t out_sh, const float* rope_hw, int grid_h, int grid_w,
+                        const float* q_xform_t, const float* q_xform_s, const float* out_xform,
+                        int n_qframes, skv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -121,6 +121,7 @@ def cached_self_attention(
     memory_k: torch.Tensor | None = None,
     memory_v: torch.Tensor | None = None,
     rope: dict[str, Any] | None = None,
+    prope: dict[str, Any] | None = None,
 ):
     """Returns ``(x [B, Lq, H, D], (current_end, local_end_index, cache_update_info))``.
 
@@ -131,6 +132,11 @@ def cached_self_attention(
     pre-RoPE, as the reference stores them: the cache keeps raw K and the query chunk, sink
     frames and local frames are rotated at the positions of ``rope_positions`` before attention
     (causal_model.py:1135-1199 with _rope_sink_local_and_query / _rope_q_and_window_k).
+
+    ``prope`` (``{"q_viewmats", "q_ks", "kv_viewmats", "kv_ks"}`` plus optional ``"transform"``
+    and ``"emulate_bf16"``) applies fused PRoPE after RoPE (causal_model.py:1170-1199): query
+    cameras are the chunk's [B, Lq, ...] tensors, key cameras the staged camera cache
+    [B, cache_tokens, ...] of ``prope_ref.stage_fused_camera_cache``, cut to the window rows.
     """
     max_attention_size = 39600 if local_attn_size == -1 else local_attn_size * frame_seqlen
     current_end = current_start + q.shape[1]
@@ -210,10 +216,12 @@ def cached_self_attention(
         active_sink = min(sink_tokens, local_end_index)
         k_sink, v_sink = temp_k[:, :active_sink], temp_v[:, :active_sink]
         k_loc, v_loc = temp_k[:, :0], temp_v[:, :0]
+        window = [(0, active_sink)]
         if local_budget > 0:
             local_start_for_window = max(sink_tokens, local_end_index - local_budget)
             k_loc = temp_k[:, local_start_for_window:local_end_index]
             v_loc = temp_v[:, local_start_for_window:local_end_index]
+            window.append((local_start_for_window, local_end_index))
         if rope is not None:
             pos = rope_positions(
                 num_sink_frames=active_sink // frame_seqlen, num_local_frames=k_loc.shape[1] // frame_seqlen,
@@ -231,6 +239,7 @@ def cached_self_attention(
         v_cat = torch.cat([v_sink, v_loc], dim=1)
     else:
         window_start = max(0, local_end_index - max_attention_size)
+        window = [(window_start, local_end_index)]
         k_cat = temp_k[:, window_start:local_end_index]
         v_cat = temp_v[:, window_start:local_end_index]
         if rope is not None:
@@ -251,6 +260,18 @@ def cached_self_attention(
         v_cat = torch.cat([memory_v.to(v_cat.dtype), v_cat], dim=1)
     if k_cat.shape[1] == 0:
         raise RuntimeError("KV-cache attention window is empty")
+    if prope is not None:
+        if memory_k is not None:
+            raise NotImplementedError("PRoPE with memory-bank frames is outside this restatement")
+        from . import prope_ref
+
+        x = prope_ref.fused_prope_attention(
+            q, k_cat, v_cat, q_viewmats=prope["q_viewmats"], q_ks=prope["q_ks"],
+            kv_viewmats=prope_ref.visible_cameras(prope["kv_viewmats"], window),
+            kv_ks=prope_ref.visible_cameras(prope["kv_ks"], window), attn_fn=attn_fn,
+            transform=prope.get("transform", "linear"),
+            emulate_bf16=prope.get("emulate_bf16", False))
+        return x, (current_end, local_end_index, info)
     x = attn_fn(q, k_cat, v_cat)
     return x, (current_end, local_end_index, info)
 

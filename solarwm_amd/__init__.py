@@ -9,21 +9,29 @@ Public surface (the reference's call signatures, solar/backends/wan22/runtime):
 * :mod:`solarwm_amd.kernels` — thin wrappers of the C ABI in include/solarkv.h
 * :class:`RopeConfig` — pre-RoPE caches with Wan RoPE applied on load (``rope=`` of the
   allocator)
+* :class:`PropeConfig`, :func:`stage_camera_cache` — fused PRoPE camera transforms on the same
+  caches (``prope=`` of the allocator; one camera pass per forward, ``camera=`` of
+  :func:`attend_cached`)
 """
 
 from .attention import apply_cache_updates, attend_cached, attention, chunk_causal_attention
 from .cache import CacheGeometry, CachePlan, SlotKVCache, make_kv_cache_allocator, plan_cached_forward
+from .prope import PropeConfig, commit_camera_cache, drop_camera_cache, stage_camera_cache
 from .rope import RopeConfig
 
 __all__ = [
     "CacheGeometry",
     "CachePlan",
+    "PropeConfig",
     "RopeConfig",
     "SlotKVCache",
     "apply_cache_updates",
     "attend_cached",
     "attention",
     "chunk_causal_attention",
+    "commit_camera_cache",
+    "drop_camera_cache",
     "make_kv_cache_allocator",
     "plan_cached_forward",
+    "stage_camera_cache",
 ]

@@ -59,6 +59,17 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _i32p, _i32, _i32, _i32, _i32, _i32,
          _i32, _f32, _i32, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i32, _i32, _vp, _i32, _vp],
     ),
+    "skv_append_prope": (
+        _i32,
+        [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _i32, _i32p, _i32, _i32, _i32,
+         _i32, _i32, _vp, _vp, _vp, _i32, _i32, _vp, _vp],
+    ),
+    "skv_attention_prope": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _i32p, _i32, _i32, _i32, _i32, _i32,
+         _i32, _f32, _i32, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i32, _i32, _vp, _vp, _vp,
+         _i32, _vp],
+    ),
 }
 
 _lock = threading.Lock()

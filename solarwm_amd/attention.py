@@ -23,6 +23,7 @@ import torch
 
 from . import _lib, kernels
 from .cache import CacheUpdate, SlotKVCache
+from .prope import CameraPass
 from .rope import positions as rope_positions
 
 
@@ -131,6 +132,21 @@ def chunk_causal_attention(
     ).to(out_dtype)
 
 
+def window_positions(kv_cache: SlotKVCache, plan, window: Sequence[int], nb: int,
+                     current_start: int) -> tuple[list[int], list[int]]:
+    """RoPE temporal positions (query frames, key frames in window order) of one cached forward:
+    sink frames lead the window when a sink is configured (causal_model.py:1135-1156) and the
+    query chunk is whole frames (causal_model.py:737-744, :806-810)."""
+    g = kv_cache.geom
+    T = g.frame_tokens
+    sink_branch = g.sink_tokens > 0
+    ns = (plan.window[0][1] - plan.window[0][0]) // T if sink_branch and plan.window else 0
+    return rope_positions(
+        kv_cache.rope.cfg, num_sink_frames=ns, num_local_frames=len(window) - ns,
+        num_new_frames=nb, max_attention_size=g.max_attention_size, frame_tokens=T,
+        current_start_frame=int(current_start) // T, sink_branch=sink_branch)
+
+
 def attend_cached(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -142,15 +158,19 @@ def attend_cached(
     memory_frames: Sequence[int] | None = None,
     softmax_scale: float | None = None,
     out: torch.Tensor | None = None,
+    camera: CameraPass | None = None,
 ) -> tuple[torch.Tensor, tuple[int, int, CacheUpdate]]:
     """One layer's cached self-attention (causal_model.py:1028-1235, post-projection/RoPE).
 
     ``q``, ``k``, ``v`` are the chunk's ``[B, Lq, H, D]`` query/key/value: post-RoPE for a cache
     without RoPE configuration, pre-RoPE (as the reference's cache branch receives them) for a
-    cache allocated with ``rope`` (RoPE applied on load at the reference's window positions).  The chunk is appended into staging slots, the visible window is the
-    reference's ``cat[sink, local]`` (including the chunk), optionally preceded by memory-bank
-    frames ``memory_frames`` (bank indices, in order), and nothing in the committed cache
-    changes until :func:`apply_cache_updates`.  Returns ``(out [B, Lq, H, D], (current_end,
+    cache allocated with ``rope`` (RoPE applied on load at the reference's window positions).
+    The chunk is appended into staging slots, the visible window is the reference's
+    ``cat[sink, local]`` (including the chunk), optionally preceded by memory-bank frames
+    ``memory_frames`` (bank indices, in order), and nothing in the committed cache changes until
+    :func:`apply_cache_updates`.  ``camera`` (from ``prope.stage_camera_cache``, once per forward
+    for all layers) applies fused PRoPE after RoPE (causal_model.py:1170-1199) and returns the
+    output mapped back by the query cameras.  Returns ``(out [B, Lq, H, D], (current_end,
     local_end_index, update))``.
     """
     g = kv_cache.geom
@@ -170,36 +190,47 @@ def attend_cached(
     rope = kv_cache.rope
     if rope is not None and memory_frames:
         raise NotImplementedError("memory-bank frames with RoPE on load are not supported")
+    if camera is not None:
+        if kv_cache.camera is None or camera.camera is not kv_cache.camera:
+            raise ValueError("camera pass was staged for a different cache (allocate with prope=)")
+        if (camera.current_start != int(current_start) or camera.num_new_tokens != q.shape[1]
+                or camera.staging != tuple(staging) or camera.window != tuple(window)):
+            raise RuntimeError("camera pass does not match this layer's forward (stage it once per "
+                               "forward, before the layers, with the same current_start and chunk)")
+    elif kv_cache.camera is not None and kv_cache.camera.active:
+        raise ValueError("this cache holds camera-conditioned history: pass camera= "
+                         "(prope.stage_camera_cache) for every forward")
     if plan.write_len > 0:
         kernels.append_frames(
             k, v, kv_cache.kpool, kv_cache.vpool, staging, frame_tokens=T,
             src_frame0=plan.roped_offset // T, kscale=kv_cache.kscale, vscale=kv_cache.vscale,
             kr_pool=kv_cache.krpool, rope_hw=rope.hw if rope is not None else None,
             grid_hw=rope.cfg.grid_hw if rope is not None else None,
+            vr_pool=kv_cache.vrpool if camera is not None else None,
+            kv_xform=camera.kv_xform if camera is not None else None,
         )
     frames = list(kv_cache.bank_slots(memory_frames)) if memory_frames else []
     frames.extend(window)
     if not frames:
         raise RuntimeError("KV-cache attention window is empty")  # causal_model.py:785-787
-    rope_args = None
-    kpool = kv_cache.kpool
+    rope_args = prope_args = None
+    kpool, vpool = kv_cache.kpool, kv_cache.vpool
     if rope is not None:
-        # sink frames lead the window when a sink is configured (causal_model.py:1135-1156);
-        # the query chunk is whole frames (causal_model.py:737-744, :806-810)
         nb = q.shape[1] // T
         if nb * T != q.shape[1]:
             raise ValueError("EchoRoPE expects the query chunk to contain whole frames")
-        sink_branch = g.sink_tokens > 0
-        ns = (plan.window[0][1] - plan.window[0][0]) // T if sink_branch and plan.window else 0
-        qpos, kpos = rope_positions(
-            rope.cfg, num_sink_frames=ns, num_local_frames=len(window) - ns, num_new_frames=nb,
-            max_attention_size=g.max_attention_size, frame_tokens=T,
-            current_start_frame=int(current_start) // T, sink_branch=sink_branch)
-        rope_args = (rope.hw, rope.cfg.grid_hw, rope.temporal(qpos, kpos))
         kpool = kv_cache.krpool
+        if camera is not None:
+            prope_args = (rope.hw, rope.cfg.grid_hw, camera.q_xform_t, camera.q_xform_s,
+                          camera.out_xform)
+            vpool = kv_cache.vrpool
+        else:
+            qpos, kpos = window_positions(kv_cache, plan, window, nb, int(current_start))
+            rope_args = (rope.hw, rope.cfg.grid_hw, rope.temporal(qpos, kpos))
     x = kernels.attention_frames(
-        q, kpool, kv_cache.vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
+        q, kpool, vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
         kscale=kv_cache.kscale, vscale=kv_cache.vscale, out=out, rope=rope_args,
+        prope=prope_args,
     )
     update = kv_cache.stage(plan, temp)
     return x, (plan.current_end, plan.local_end_index, update)

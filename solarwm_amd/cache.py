@@ -28,6 +28,7 @@ from typing import Any, Iterator, Sequence
 import torch
 
 from . import kernels
+from .prope import CameraCache, PropeConfig
 from .rope import RopeConfig, RopeTables
 
 # causal_model.py:572-574: local_attn_size == -1 means a fixed 39600-token attention budget.
@@ -336,10 +337,16 @@ class SlotKVCache(Mapping):
     With ``rope`` (tables shared by every layer of a model) the cache is pre-RoPE like the
     reference's: ``k``/``v`` hold the raw frames, and ``krpool`` holds each frame's K with its
     height/width RoPE pairs rotated, which the attention kernel reads (bf16 caches only).
+
+    With ``camera`` (one ``CameraCache`` shared by every layer of a model, fused PRoPE) ``krpool``
+    also carries each frame's P⁻¹ on its spatial channel groups once a camera pass wrote it, and
+    ``vrpool`` holds P⁻¹ v; layer 0 answers the reference's ``"_fused_prope_camera_metadata"``
+    key (``{"viewmats": [B, cache_tokens, 4, 4], "K": [B, cache_tokens, 3, 3]}``).
     """
 
     def __init__(self, geom: CacheGeometry, *, dtype: torch.dtype, device: torch.device | str,
-                 rope: RopeTables | None = None):
+                 rope: RopeTables | None = None, camera: CameraCache | None = None,
+                 camera_owner: bool = False):
         self.geom = geom
         self.dtype = dtype
         self.device = torch.device(device)
@@ -355,6 +362,15 @@ class SlotKVCache(Mapping):
             if gh * gw != geom.frame_tokens:
                 raise ValueError(f"RoPE grid {gh}x{gw} does not tile {geom.frame_tokens}-token frames")
             self.krpool = torch.zeros_like(self.kpool)
+        self.camera = camera
+        self.camera_owner = camera_owner
+        self.vrpool = None
+        if camera is not None:
+            if rope is None:
+                raise ValueError("fused PRoPE needs a pre-RoPE cache (rope=)")
+            if gh * gw < kernels.TILE:
+                raise ValueError(f"fused PRoPE needs frames of at least {kernels.TILE} tokens")
+            self.vrpool = torch.zeros_like(self.vpool)
         self.slots = SlotTable(geom)
 
     def reset(self) -> None:
@@ -364,6 +380,10 @@ class SlotKVCache(Mapping):
         self.vpool.zero_()
         if self.krpool is not None:
             self.krpool.zero_()
+        if self.vrpool is not None:
+            self.vrpool.zero_()
+        if self.camera is not None and self.camera_owner:
+            self.camera.reset()
         if self.kscale is not None:
             self.kscale.zero_()
             self.vscale.zero_()
@@ -407,7 +427,21 @@ class SlotKVCache(Mapping):
             self.kpool, self.vpool, self.table, frame_tokens=self.geom.frame_tokens
         )
 
+    def camera_metadata(self) -> dict[str, torch.Tensor]:
+        """The reference's shared camera cache rows (causal_model.py:2005-2019), materialised
+        from the per-slot cameras through the slot table."""
+        idx = torch.tensor(self.table, dtype=torch.long, device=self.camera.device)
+        T = self.geom.frame_tokens
+        view = self.camera.viewmats.index_select(0, idx).transpose(0, 1)  # [B, frames, 4, 4]
+        ks = self.camera.ks.index_select(0, idx).transpose(0, 1)
+        return {"viewmats": view.repeat_interleave(T, dim=1), "K": ks.repeat_interleave(T, dim=1)}
+
+    def _has_camera_key(self) -> bool:
+        return self.camera is not None and self.camera_owner and self.camera.active
+
     def __getitem__(self, key: str) -> Any:
+        if key == "_fused_prope_camera_metadata" and self._has_camera_key():
+            return self.camera_metadata()
         if key == "k":
             return self.logical_kv()[0]
         if key == "v":
@@ -419,10 +453,13 @@ class SlotKVCache(Mapping):
         raise KeyError(key)
 
     def __iter__(self) -> Iterator[str]:
-        return iter(("k", "v", "global_end_index", "local_end_index"))
+        keys = ("k", "v", "global_end_index", "local_end_index")
+        if self._has_camera_key():
+            keys += ("_fused_prope_camera_metadata",)
+        return iter(keys)
 
     def __len__(self) -> int:
-        return 4
+        return 5 if self._has_camera_key() else 4
 
 
 def make_kv_cache_allocator(
@@ -437,6 +474,7 @@ def make_kv_cache_allocator(
     bank_frames: int = 0,
     cache_dtype: torch.dtype | None = None,
     rope: RopeConfig | None = None,
+    prope: PropeConfig | None = None,
 ):
     """Return ``allocate_kv_cache(batch_size, *, dtype, device) -> list[SlotKVCache]``.
 
@@ -444,7 +482,10 @@ def make_kv_cache_allocator(
     be injected as that runtime's ``_kv_cache_allocator``.  ``cache_dtype`` overrides the storage
     dtype (``torch.float8_e4m3fn`` for the fp8 cache); by default the model dtype is used.
     ``rope`` makes the caches pre-RoPE (K and Q are passed un-roped and RoPE is applied on load,
-    as the reference's cache branch does); its tables are shared by all layers.
+    as the reference's cache branch does); its tables are shared by all layers.  ``prope`` (with
+    ``rope``) makes the caches camera-aware for the fused PRoPE mode: one camera cache shared by
+    all layers (exposed on layer 0, as the reference keeps it), staged per forward with
+    ``prope.stage_camera_cache``.
     """
     if local_attn_size <= 0:
         raise ValueError("the slot cache needs a positive local_attn_size (cache frames)")
@@ -463,6 +504,10 @@ def make_kv_cache_allocator(
         )
         store = dtype if cache_dtype is None else cache_dtype
         tables = RopeTables(rope, device) if rope is not None else None
-        return [SlotKVCache(geom, dtype=store, device=device, rope=tables) for _ in range(num_layers)]
+        if prope is not None and rope is None:
+            raise ValueError("fused PRoPE needs a pre-RoPE cache: pass rope= as well")
+        camera = CameraCache(geom.n_slots, batch_size, device, prope) if prope is not None else None
+        return [SlotKVCache(geom, dtype=store, device=device, rope=tables, camera=camera,
+                            camera_owner=(i == 0)) for i in range(num_layers)]
 
     return allocate_kv_cache

@@ -58,12 +58,36 @@ struct AttnArgs {
   const float* rope_hw;
   const float* rope_t;
   int gh, gw, n_qframes;
+  // PRoPE (camera transforms, applied after RoPE) on the same path; every matrix is a row-major
+  // 4x4 acting on one group of 4 consecutive head channels:
+  //   pq_t [B][n_frames][n_qframes][11][16]: W = R_k^T (P_q P_k^-1)^T R_q per temporal group
+  //        (applied to the raw query; R = that group's temporal RoPE rotation at p_key / p_query)
+  //   pq_s [B][n_qframes][16]: P_q^T, applied to the query's spatial groups after their RoPE
+  //   pq_o [B][n_qframes][16]: P_q, applied to every group of the output
+  const float* pq_t;
+  const float* pq_s;
+  const float* pq_o;
   int32_t slots[SKV_MAX_FRAMES];
 };
 
 // Wan's split of a head's 64 complex channel pairs (2i, 2i+1): 22 temporal, 21 height, 21 width
 // (causal_model.py:1855-1866).
 constexpr int kRopeT = 22, kRopeHW = 21;
+constexpr int kGroupsT = kRopeT / 2;  // PRoPE groups (4 channels) holding temporal pairs only
+// PRoPE: the W matrices of one key frame for the workgroup's query frames (at most 5 when
+// frame_tokens >= 64) are staged in LDS behind the K/V tiles, double-buffered by frame parity.
+constexpr int kWPair = kGroupsT * 16 * 4;  // bytes of W per (query frame, key frame)
+constexpr int kWMaxQF = 5;
+constexpr int kWBuf = 4096;                // >= kWMaxQF * kWPair, whole 1 KB wave chunks
+static_assert(kWMaxQF * kWPair <= kWBuf, "W buffer too small");
+
+// y[4g .. 4g+4) <- m (row-major 4x4) x y[4g .. 4g+4)
+__device__ inline void xform4(Vec8<float>& y, int g, const float* m) {
+  const float x0 = y.get(4 * g), x1 = y.get(4 * g + 1), x2 = y.get(4 * g + 2), x3 = y.get(4 * g + 3);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    y.set(4 * g + i, fmaf(m[4 * i], x0, fmaf(m[4 * i + 1], x1, fmaf(m[4 * i + 2], x2, m[4 * i + 3] * x3))));
+}
 
 // Workgroups have NW = 4 or 8 waves (128 or 256 queries); the launcher picks the shape that
 // fills the 256 CUs best (8-wave groups halve the K/V bytes staged per query).
@@ -202,7 +226,7 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
     }
 }
 
-template <int NW, typename QT, typename KT, bool ROPE>
+template <int NW, typename QT, typename KT, int RM>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   constexpr int kBQ = NW * 32;
@@ -231,14 +255,16 @@ void attn_kernel(AttnArgs a) {
 
   // Q^T operand: lane (n, hh) holds q[qrow][k*16 + hh*8 .. +7] for k = 0..7.
   bf16x8 qf[8];
-  // RoPE: the query's height/width pairs are rotated once here; its temporal pairs (0..21, in
-  // qf[0..2]) are kept unrotated in qt0 and turned by (p_query - p_key) per key frame below.
+  // RM = 0: Q as given.  RM = 1 (RoPE): the query's height/width pairs are rotated once here;
+  // its temporal pairs (0..21, in qf[0..2]) are kept unrotated in qt0 and turned by
+  // (p_query - p_key) per key frame below.  RM = 2 (RoPE + PRoPE): as RM = 1, the spatial
+  // groups then take P_q^T, and the temporal groups take the per-key-frame matrix W below.
   [[maybe_unused]] bf16x8 qt0[3];
   [[maybe_unused]] int qfi = 0;  // query frame of this lane's row
   {
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
                    (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 8;
-    if constexpr (ROPE) {
+    if constexpr (RM > 0) {
       const int qr = qlive ? qrow : a.Lq - 1;
       qfi = qr / a.T;
       const int tt = qr - qfi * a.T, hq = tt / a.gw, wq = tt - hq * a.gw;
@@ -259,6 +285,12 @@ void attn_kernel(AttnArgs a) {
           y.set(2 * m, u * c - v * sn);
           y.set(2 * m + 1, u * sn + v * c);
         }
+        if constexpr (RM == 2) {
+          const float* ps = a.pq_s + ((int64_t)b * a.n_qframes + qfi) * 16;
+#pragma unroll
+          for (int gg = 0; gg < 2; ++gg)
+            if (4 * k + 2 * hh + gg >= kGroupsT) xform4(y, gg, ps);
+        }
         qf[k] = y.to_bf16();
       }
 #pragma unroll
@@ -269,8 +301,55 @@ void attn_kernel(AttnArgs a) {
         qf[k] = qlive ? Vec8<QT>::load(qp + k * 16).to_bf16() : Vec8<bf16>::zero().to_bf16();
     }
   }
-  // RoPE: qf[0..2] <- qt0 with temporal pair p turned by the angle of (query frame, key frame j)
+  // PRoPE: W of key frame j for query frames [qf_lo, qf_lo + count) -> LDS buffer j & 1 (waves
+  // 0..3 move 1 KB each with direct global->LDS loads; completion is awaited with the tiles')
+  [[maybe_unused]] const int qf_lo = q0 / a.T;
+  [[maybe_unused]] auto issue_w = [&](int j) {
+    if constexpr (RM == 2) {
+      const int count = (min(q0 + kBQ, a.Lq) - 1) / a.T - qf_lo + 1;
+      const int off = w * 1024 + lane * 16;
+      if (w < kWBuf / 1024 && off < count * kWPair) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.pq_t, (short)0, 0x7fffffff, 0x00020000);
+        const uint32_t so = (uint32_t)((((int64_t)b * a.n_frames + j) * a.n_qframes + qf_lo) * kWPair);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (lds_void_t*)(lds + 2 * kTileBytes + (j & 1) * kWBuf + w * 1024), 16, off, so, 0, 0);
+      }
+    }
+  };
+  // qf[0..2] <- qt0 with the temporal pairs turned by the angle of (query frame, key frame j)
+  // (RM = 1), or with each temporal group multiplied by that pair's W (RM = 2)
   [[maybe_unused]] auto rot_q = [&](int j) {
+    if constexpr (RM == 2) {
+      // W of (this lane's query frame, key frame j), staged in LDS by issue_w; one group's
+      // rows are live at a time (this runs inside the main loop, where registers are scarce)
+      const float* wt = reinterpret_cast<const float*>(lds + 2 * kTileBytes + (j & 1) * kWBuf) +
+                        (qfi - qf_lo) * (kGroupsT * 16);
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+          const int g = 4 * k + 2 * hh + gg;
+          if (g >= kGroupsT) continue;
+          // an opaque copy keeps the loop-invariant bf16 -> fp32 conversion here instead of
+          // hoisted out of the main loop (24 live floats there would spill)
+          bf16x8 t = qt0[k];
+          asm volatile("" : "+v"(t));
+          float x[4], r[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = (float)t[4 * gg + e];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float4 m = *reinterpret_cast<const float4*>(wt + g * 16 + 4 * i);
+            r[i] = fmaf(m.x, x[0], fmaf(m.y, x[1], fmaf(m.z, x[2], m.w * x[3])));
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qf[k][4 * gg + e] = (bf16)r[e];
+          asm volatile("" ::: "memory");
+        }
+      }
+      return;
+    }
     const float* tb = a.rope_t + ((int64_t)qfi * a.n_frames + j) * (2 * kRopeT);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
@@ -357,12 +436,16 @@ void attn_kernel(AttnArgs a) {
   if (ntau > 0) {
     loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
     if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
+    if constexpr (RM == 2) {
+      issue_w(0);
+      if (ntau > 1 && a.ntiles_f == 1) issue_w(1);
+    }
 #pragma unroll
     for (int r = 0; r < 16 / NW; ++r)
       *reinterpret_cast<bf16x8*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = Vec8<bf16>::zero().to_bf16();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if constexpr (ROPE) rot_q(0);
+    if constexpr (RM > 0) rot_q(0);
     qk_tile(kb_lds(0) + lane16, qf, s_cur);
     int tok0, key0;
     if (tile_needs_mask(0, tok0, key0)) mask_tile(s_cur, hh, tok0, a.T, key0, lim_lane);
@@ -381,9 +464,13 @@ void attn_kernel(AttnArgs a) {
                   bf16x8 (&pprev)[2][2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
     if (tau + 2 < ntau) loader.issue_k(kpool + tile_base(tau + 2), kb_lds(cb), w);
     loader.issue_v(vpool + vtile_base(tau), vb_lds(cb), w);
+    if constexpr (RM == 2) {
+      // W for the frame tile tau+2 opens (rot_q reads it at the start of step tau+1)
+      if (tau + 2 < ntau && (tau + 2) % a.ntiles_f == 0) issue_w((tau + 2) / a.ntiles_f);
+    }
     const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
     const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
-    if constexpr (ROPE) {
+    if constexpr (RM > 0) {
       // QK(tau+1) below opens a new key frame: turn Q's temporal pairs for it
       const int t1 = tau + 1;
       if (t1 < ntau && t1 % a.ntiles_f == 0) rot_q(t1 / a.ntiles_f);
@@ -513,13 +600,24 @@ void attn_kernel(AttnArgs a) {
   if (qlive) {
     QT* op = static_cast<QT*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
              (int64_t)qrow * a.o_st;
+    // lane (n, hh) holds channels db*32 + g*8 + hh*4 .. +3 of its query: whole PRoPE groups
+    [[maybe_unused]] const float* po = nullptr;
+    if constexpr (RM == 2) po = a.pq_o + ((int64_t)b * a.n_qframes + qfi) * 16;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = db * 32 + g * 8 + hh * 4;
-        store4<QT>(op + d0, oacc[db][g * 4 + 0] * inv, oacc[db][g * 4 + 1] * inv,
-                   oacc[db][g * 4 + 2] * inv, oacc[db][g * 4 + 3] * inv);
+        float x0 = oacc[db][g * 4 + 0] * inv, x1 = oacc[db][g * 4 + 1] * inv;
+        float x2 = oacc[db][g * 4 + 2] * inv, x3 = oacc[db][g * 4 + 3] * inv;
+        if constexpr (RM == 2) {
+          const float y0 = fmaf(po[0], x0, fmaf(po[1], x1, fmaf(po[2], x2, po[3] * x3)));
+          const float y1 = fmaf(po[4], x0, fmaf(po[5], x1, fmaf(po[6], x2, po[7] * x3)));
+          const float y2 = fmaf(po[8], x0, fmaf(po[9], x1, fmaf(po[10], x2, po[11] * x3)));
+          const float y3 = fmaf(po[12], x0, fmaf(po[13], x1, fmaf(po[14], x2, po[15] * x3)));
+          x0 = y0, x1 = y1, x2 = y2, x3 = y3;
+        }
+        store4<QT>(op + d0, x0, x1, x2, x3);
       }
   }
 }
@@ -840,7 +938,7 @@ static int cu_count() {
 }
 
 template <int NW>
-static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, bool rope, hipStream_t s) {
+static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipStream_t s) {
   dim3 grid(a.n_wg), block(NW * 64);
   if (pool_dtype == SKV_FP8_E4M3) {
     if (q_dtype == SKV_BF16)
@@ -850,21 +948,29 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, bool rope, hi
     return;
   }
   const size_t lds_bytes = 2 * kTileBytes;
-  if (rope) {  // bf16 pools only (checked by the caller)
+  if (rm == 2) {  // bf16 pools, frame_tokens >= 64 (checked by the caller)
+    const size_t lds_w = lds_bytes + 2 * kWBuf;
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, true>), grid, block, lds_bytes, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 2>), grid, block, lds_w, s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, true>), grid, block, lds_bytes, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 2>), grid, block, lds_w, s, a);
+    return;
+  }
+  if (rm == 1) {  // bf16 pools only (checked by the caller)
+    if (q_dtype == SKV_BF16)
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 1>), grid, block, lds_bytes, s, a);
+    else
+      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1>), grid, block, lds_bytes, s, a);
     return;
   }
   if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, false>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
-    hipLaunchKernelGGL((attn_kernel<NW, bf16, float, false>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, float, 0>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_F32 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<NW, float, bf16, false>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0>), grid, block, lds_bytes, s, a);
   else
-    hipLaunchKernelGGL((attn_kernel<NW, float, float, false>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, float, float, 0>), grid, block, lds_bytes, s, a);
 }
 
 static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
@@ -875,7 +981,8 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
                           float softmax_scale, int mask_mode, int64_t q_pos0,
                           int64_t chunk_tokens, void* out, int64_t out_sb, int64_t out_st,
                           int64_t out_sh, const float* rope_hw, int grid_h, int grid_w,
-                          const float* rope_t, int n_qframes, skv_stream_t stream) {
+                          const float* rope_t, int n_qframes, const float* pq_t,
+                          const float* pq_s, const float* pq_o, skv_stream_t stream) {
   if (!q || !k_pool || !v_pool || !frame_slots || !out) {
     set_error("skv_attention: null pointer argument");
     return SKV_E_ARG;
@@ -927,7 +1034,20 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
               frame_tokens);
     return SKV_E_ARG;
   }
-  const bool rope = rope_t != nullptr;
+  const bool prope = pq_t != nullptr;
+  const bool rope = rope_t != nullptr || prope;
+  if (prope && (!pq_s || !pq_o)) {
+    set_error("skv_attention_prope: need q_xform_t, q_xform_s and out_xform");
+    return SKV_E_ARG;
+  }
+  if (prope && (int64_t)batch * n_frames * n_qframes * kWPair >= ((int64_t)1 << 31)) {
+    set_error("skv_attention_prope: q_xform_t exceeds 2^31 bytes");
+    return SKV_E_ARG;
+  }
+  if (prope && frame_tokens < kTile) {
+    set_error("skv_attention_prope: frame_tokens=%d < %d unsupported", frame_tokens, kTile);
+    return SKV_E_UNSUPPORTED;
+  }
   if (rope) {
     if (pool_dtype != SKV_BF16) {
       set_error("skv_attention_rope: only bf16 pools are supported");
@@ -945,6 +1065,9 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   AttnArgs a;
   a.rope_hw = rope_hw;
   a.rope_t = rope_t;
+  a.pq_t = pq_t;
+  a.pq_s = pq_s;
+  a.pq_o = pq_o;
   a.gh = grid_h;
   a.gw = grid_w;
   a.n_qframes = n_qframes;
@@ -994,10 +1117,11 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     a.slots[j] = frame_slots[j];
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rm = prope ? 2 : rope ? 1 : 0;
   if (nw == 8)
-    launch<8>(a, q_dtype, pool_dtype, rope, s);
+    launch<8>(a, q_dtype, pool_dtype, rm, s);
   else
-    launch<4>(a, q_dtype, pool_dtype, rope, s);
+    launch<4>(a, q_dtype, pool_dtype, rm, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("skv_attention: launch failed: %s", hipGetErrorString(e));
@@ -1018,7 +1142,8 @@ extern "C" int skv_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q
   return attention_impl(q, q_dtype, q_sb, q_st, q_sh, k_pool, v_pool, k_scale, v_scale,
                         pool_dtype, n_slots, frame_slots, n_frames, batch, heads, head_dim, q_len,
                         frame_tokens, softmax_scale, mask_mode, q_pos0, chunk_tokens, out, out_sb,
-                        out_st, out_sh, nullptr, 0, 0, nullptr, 0, stream);
+                        out_st, out_sh, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, nullptr,
+                        stream);
 }
 
 extern "C" int skv_attention_rope(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
@@ -1038,5 +1163,28 @@ extern "C" int skv_attention_rope(const void* q, int q_dtype, int64_t q_sb, int6
   return attention_impl(q, q_dtype, q_sb, q_st, q_sh, kr_pool, v_pool, nullptr, nullptr,
                         pool_dtype, n_slots, frame_slots, n_frames, batch, heads, head_dim, q_len,
                         frame_tokens, softmax_scale, mask_mode, q_pos0, chunk_tokens, out, out_sb,
-                        out_st, out_sh, rope_hw, grid_h, grid_w, rope_t, n_qframes, stream);
+                        out_st, out_sh, rope_hw, grid_h, grid_w, rope_t, n_qframes, nullptr,
+                        nullptr, nullptr, stream);
+}
+
+extern "C" int skv_attention_prope(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
+                                   int64_t q_sh, const void* kx_pool, const void* vx_pool,
+                                   int pool_dtype, int n_slots, const int32_t* frame_slots,
+                                   int n_frames, int batch, int heads, int head_dim, int q_len,
+                                   int frame_tokens, float softmax_scale, int mask_mode,
+                                   int64_t q_pos0, int64_t chunk_tokens, void* out,
+                                   int64_t out_sb, int64_t out_st, int64_t out_sh,
+                                   const float* rope_hw, int grid_h, int grid_w,
+                                   const float* q_xform_t, const float* q_xform_s,
+                                   const float* out_xform, int n_qframes, skv_stream_t stream) {
+  clear_error();
+  if (!q_xform_t) {
+    set_error("skv_attention_prope: null q_xform_t");
+    return SKV_E_ARG;
+  }
+  return attention_impl(q, q_dtype, q_sb, q_st, q_sh, kx_pool, vx_pool, nullptr, nullptr,
+                        pool_dtype, n_slots, frame_slots, n_frames, batch, heads, head_dim, q_len,
+                        frame_tokens, softmax_scale, mask_mode, q_pos0, chunk_tokens, out, out_sb,
+                        out_st, out_sh, rope_hw, grid_h, grid_w, nullptr, n_qframes, q_xform_t,
+                        q_xform_s, out_xform, stream);
 }

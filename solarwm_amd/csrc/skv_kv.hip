@@ -27,6 +27,11 @@ struct AppendArgs {
   void* krpool;
   const float* rope_hw;
   int gh, gw;
+  // PRoPE (needs krpool): kv_xf [n_frames][B][16] = P^-1 (row-major 4x4) of each written frame's
+  // camera; krpool's spatial channel groups (44..127, after their RoPE) and every group of
+  // vrpool (V, laid out as vpool) receive P^-1 x per group of 4 channels
+  void* vrpool;
+  const float* kv_xf;
   int32_t slots[SKV_MAX_APPEND_FRAMES];
 };
 
@@ -36,8 +41,7 @@ constexpr int kRopeT = 22, kRopeHW = 21;
 
 // Rotate the spatial pairs among channels [col, col+8) of token t (grid width gw): pair p in
 // [22, 43) turns by the angle of row h = t / gw, p in [43, 64) by that of column w = t % gw.
-template <typename E>
-__device__ inline void rope_spatial8(Vec8<E>& v, int col, int t, int gh, int gw, const float* tab) {
+__device__ inline void rope_spatial8(Vec8<float>& v, int col, int t, int gh, int gw, const float* tab) {
   if (col + 8 <= 2 * kRopeT) return;
   const int hq = t / gw, wq = t - hq * gw;
 #pragma unroll
@@ -46,10 +50,34 @@ __device__ inline void rope_spatial8(Vec8<E>& v, int col, int t, int gh, int gw,
     if (p < kRopeT) continue;
     const int idx = p < kRopeT + kRopeHW ? hq * kRopeHW + (p - kRopeT) : (gh + wq) * kRopeHW + (p - kRopeT - kRopeHW);
     const float c = tab[2 * idx], sn = tab[2 * idx + 1];
-    const float x = (float)v.get(2 * m), y = (float)v.get(2 * m + 1);
-    v.set(2 * m, (E)(x * c - y * sn));
-    v.set(2 * m + 1, (E)(x * sn + y * c));
+    const float x = v.get(2 * m), y = v.get(2 * m + 1);
+    v.set(2 * m, x * c - y * sn);
+    v.set(2 * m + 1, x * sn + y * c);
   }
+}
+
+// y[4g .. 4g+4) <- m (row-major 4x4) x y[4g .. 4g+4)
+__device__ inline void xform4(Vec8<float>& y, int g, const float* m) {
+  const float x0 = y.get(4 * g), x1 = y.get(4 * g + 1), x2 = y.get(4 * g + 2), x3 = y.get(4 * g + 3);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    y.set(4 * g + i, fmaf(m[4 * i], x0, fmaf(m[4 * i + 1], x1, fmaf(m[4 * i + 2], x2, m[4 * i + 3] * x3))));
+}
+
+template <typename E>
+__device__ inline Vec8<float> to_f32(const Vec8<E>& v) {
+  Vec8<float> y;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y.set(e, (float)v.get(e));
+  return y;
+}
+
+template <typename E>
+__device__ inline Vec8<E> from_f32(const Vec8<float>& y) {
+  Vec8<E> v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v.set(e, (E)y.get(e));
+  return v;
 }
 
 // 8x8 transpose of 16-bit elements held as 8 rows of 4 x u32 (row r = token, word c/2 half c%2
@@ -70,7 +98,8 @@ __device__ inline void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
 // 64 K rows (16 B vectors); threads 128-255 each move one 8-token x 8-channel block of V,
 // transposed in registers, so V^T rows are written as 16 B vectors without an LDS stage.
 // Rows past T are written as zeros.
-template <typename E>
+// XM: 0 = pools only, 1 = + RoPE copy of K (krpool), 2 = + PRoPE copies of K and V
+template <typename E, int XM>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   int wg = blockIdx.x;
   const int t = wg % a.ntiles;
@@ -97,8 +126,18 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
       Vec8<E> kv = live ? Vec8<E>::load(ks + src_base + (int64_t)(tok0 + row) * a.s_st + col)
                         : Vec8<E>::zero();
       kv.store_nt(kp + row * kHeadDim + col);
-      if (a.krpool) {
-        if (live) rope_spatial8(kv, col, tok0 + row, a.gh, a.gw, a.rope_hw);
+      if constexpr (XM > 0) {
+        if (live && col + 8 > 2 * kRopeT) {
+          Vec8<float> y = to_f32(kv);
+          rope_spatial8(y, col, tok0 + row, a.gh, a.gw, a.rope_hw);
+          if constexpr (XM == 2) {
+            const float* m = a.kv_xf + ((int64_t)f * a.B + b) * 16;
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg)
+              if (col + 4 * gg >= 2 * kRopeT) xform4(y, gg, m);
+          }
+          kv = from_f32<E>(y);
+        }
         kv.store_nt(static_cast<E*>(a.krpool) + (kp - static_cast<E*>(a.kpool)) + row * kHeadDim + col);
       }
     }
@@ -123,6 +162,25 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 #pragma unroll
     for (int c = 0; c < 8; ++c)
       st_nt(vp + (int64_t)(db * 8 + c) * a.Tp + tb * 8, out[c]);
+    if constexpr (XM == 2) {
+      // P^-1 per token on both channel groups, then the same transpose into vrpool (rows past
+      // T stay zero)
+      const float* m = a.kv_xf + ((int64_t)f * a.B + b) * 16;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        Vec8<bf16> x;
+        x.r = in[r];
+        Vec8<float> y = to_f32(x);
+        xform4(y, 0, m);
+        xform4(y, 1, m);
+        in[r] = from_f32<bf16>(y).r;
+      }
+      transpose8x8_b16(in, out);
+      E* vx = static_cast<E*>(a.vrpool) + (vp - static_cast<E*>(a.vpool));
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        st_nt(vx + (int64_t)(db * 8 + c) * a.Tp + tb * 8, out[c]);
+    }
   } else {
     Vec8<E> in[8];
 #pragma unroll
@@ -493,7 +551,8 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
                        void* v_pool, float* k_scale, float* v_scale, int pool_dtype,
                        int n_slots, const int32_t* dst_slots, int n_frames, int batch,
                        int heads, int head_dim, int frame_tokens, void* kr_pool,
-                       const float* rope_hw, int grid_h, int grid_w, skv_stream_t stream) {
+                       const float* rope_hw, int grid_h, int grid_w, void* vr_pool,
+                       const float* kv_xform, skv_stream_t stream) {
   if (!k_new || !v_new || !k_pool || !v_pool || !dst_slots) {
     set_error("skv_append: null pointer argument");
     return SKV_E_ARG;
@@ -527,6 +586,16 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
       return SKV_E_ARG;
     }
   }
+  if (vr_pool || kv_xform) {
+    if (!vr_pool || !kv_xform || !kr_pool) {
+      set_error("skv_append_prope: need kx_pool, vx_pool and kv_xform");
+      return SKV_E_ARG;
+    }
+    if (pool_dtype != SKV_BF16) {
+      set_error("skv_append_prope: only bf16 pools are supported");
+      return SKV_E_UNSUPPORTED;
+    }
+  }
   if (fp8 && (!k_scale || !v_scale)) {
     set_error("skv_append: fp8 pool needs k_scale and v_scale");
     return SKV_E_ARG;
@@ -558,6 +627,8 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   a.rope_hw = rope_hw;
   a.gh = grid_h;
   a.gw = grid_w;
+  a.vrpool = vr_pool;
+  a.kv_xf = kv_xform;
   for (int f = 0; f < n_frames; ++f) {
     if (dst_slots[f] < 0 || dst_slots[f] >= n_slots) {
       set_error("skv_append: dst_slots[%d]=%d outside [0, %d)", f, dst_slots[f], n_slots);
@@ -578,10 +649,19 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
       hipLaunchKernelGGL(append_fp8_kernel<float>, grid, dim3(1024), 0, s, a);
   } else {
     dim3 grid(n_frames * batch * heads * a.ntiles);
-    if (src_dtype == SKV_BF16)
-      hipLaunchKernelGGL(append_kernel<bf16>, grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(append_kernel<float>, grid, dim3(256), 0, s, a);
+    if (src_dtype == SKV_BF16) {
+      if (kv_xform)
+        hipLaunchKernelGGL((append_kernel<bf16, 2>), grid, dim3(256), 0, s, a);
+      else if (kr_pool)
+        hipLaunchKernelGGL((append_kernel<bf16, 1>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((append_kernel<bf16, 0>), grid, dim3(256), 0, s, a);
+    } else {
+      if (kr_pool)
+        hipLaunchKernelGGL((append_kernel<float, 1>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((append_kernel<float, 0>), grid, dim3(256), 0, s, a);
+    }
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -599,7 +679,7 @@ extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, i
   clear_error();
   return append_impl(k_new, v_new, src_dtype, src_sb, src_st, src_sh, src_frame0, k_pool, v_pool,
                      k_scale, v_scale, pool_dtype, n_slots, dst_slots, n_frames, batch, heads,
-                     head_dim, frame_tokens, nullptr, nullptr, 0, 0, stream);
+                     head_dim, frame_tokens, nullptr, nullptr, 0, 0, nullptr, nullptr, stream);
 }
 
 extern "C" int skv_append_rope(const void* k_new, const void* v_new, int src_dtype,
@@ -616,7 +696,26 @@ extern "C" int skv_append_rope(const void* k_new, const void* v_new, int src_dty
   }
   return append_impl(k_new, v_new, src_dtype, src_sb, src_st, src_sh, src_frame0, k_pool, v_pool,
                      nullptr, nullptr, pool_dtype, n_slots, dst_slots, n_frames, batch, heads,
-                     head_dim, frame_tokens, kr_pool, rope_hw, grid_h, grid_w, stream);
+                     head_dim, frame_tokens, kr_pool, rope_hw, grid_h, grid_w, nullptr, nullptr,
+                     stream);
+}
+
+extern "C" int skv_append_prope(const void* k_new, const void* v_new, int src_dtype,
+                                int64_t src_sb, int64_t src_st, int64_t src_sh, int src_frame0,
+                                void* k_pool, void* v_pool, int pool_dtype, int n_slots,
+                                const int32_t* dst_slots, int n_frames, int batch, int heads,
+                                int head_dim, int frame_tokens, void* kx_pool, void* vx_pool,
+                                const float* rope_hw, int grid_h, int grid_w,
+                                const float* kv_xform, skv_stream_t stream) {
+  clear_error();
+  if (!kx_pool || !vx_pool || !kv_xform) {
+    set_error("skv_append_prope: null kx_pool, vx_pool or kv_xform");
+    return SKV_E_ARG;
+  }
+  return append_impl(k_new, v_new, src_dtype, src_sb, src_st, src_sh, src_frame0, k_pool, v_pool,
+                     nullptr, nullptr, pool_dtype, n_slots, dst_slots, n_frames, batch, heads,
+                     head_dim, frame_tokens, kx_pool, rope_hw, grid_h, grid_w, vx_pool, kv_xform,
+                     stream);
 }
 
 extern "C" int skv_gather(const void* k_pool, const void* v_pool, int pool_dtype, int n_slots,

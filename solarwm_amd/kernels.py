@@ -173,13 +173,17 @@ def prepare_append(
     kr_pool: torch.Tensor | None = None,
     rope_hw: torch.Tensor | None = None,
     grid_hw: tuple[int, int] | None = None,
+    vr_pool: torch.Tensor | None = None,
+    kv_xform: torch.Tensor | None = None,
 ):
     """Validate an append once and return a zero-argument launcher that enqueues it on the stream
     current now (repeated launches skip the Python-side checks).
 
     With ``kr_pool`` (same shape and dtype as ``kpool``), the frames' K is also written there
     with the height/width pairs of RoPE applied (``rope_hw`` from ``rope.spatial_table``,
-    ``grid_hw`` = the frame's patch grid)."""
+    ``grid_hw`` = the frame's patch grid).  With ``kv_xform`` (float32 ``[n_frames, B, 4, 4]``,
+    the P⁻¹ of each written frame's camera) and ``vr_pool`` (shaped like ``vpool``), PRoPE is
+    applied too: ``kr_pool`` gets P⁻¹ on its spatial channel groups and ``vr_pool`` gets P⁻¹ v."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("k_new", k_new)
@@ -199,7 +203,26 @@ def prepare_append(
     ks, vs = _scales(kpool, kscale, vscale)
     slots = _lib.int32_array(dst_slots)
     moved = 2 * n * frame_tokens * b * h * HEAD_DIM * (k_new.element_size() + kpool.element_size())
-    if kr_pool is None:
+    if kv_xform is not None or vr_pool is not None:
+        if kr_pool is None or vr_pool is None or kv_xform is None:
+            raise ValueError("PRoPE append needs kr_pool, vr_pool and kv_xform")
+        _check_rope_hw(kr_pool, kpool, rope_hw, grid_hw, frame_tokens)
+        _require_cuda("vr_pool", vr_pool)
+        if vr_pool.shape != vpool.shape or vr_pool.dtype != vpool.dtype or not vr_pool.is_contiguous():
+            raise ValueError("vr_pool must be a contiguous tensor shaped and typed like the V pool")
+        _require_cuda("kv_xform", kv_xform)
+        if (kv_xform.dtype != torch.float32 or tuple(kv_xform.shape) != (n, b, 4, 4)
+                or not kv_xform.is_contiguous()):
+            raise ValueError(f"kv_xform must be contiguous float32 [{n}, {b}, 4, 4]")
+        fn_name = "skv_append_prope"
+        args = (
+            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
+            kpool.data_ptr(), vpool.data_ptr(), dtype_code(kpool.dtype), n_slots, slots, n, b, h,
+            HEAD_DIM, frame_tokens, kr_pool.data_ptr(), vr_pool.data_ptr(), rope_hw.data_ptr(),
+            grid_hw[0], grid_hw[1], kv_xform.data_ptr(), _stream(kpool.device),
+        )
+        moved += 2 * n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
+    elif kr_pool is None:
         fn_name = "skv_append"
         args = (
             k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
@@ -224,7 +247,8 @@ def prepare_append(
         _toc("append", t0, moved)
 
     launch.bytes_moved = moved
-    launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots, kr_pool, rope_hw)
+    launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots, kr_pool, rope_hw, vr_pool,
+                   kv_xform)
     return launch
 
 
@@ -242,12 +266,15 @@ def append_frames(
     kr_pool: torch.Tensor | None = None,
     rope_hw: torch.Tensor | None = None,
     grid_hw: tuple[int, int] | None = None,
+    vr_pool: torch.Tensor | None = None,
+    kv_xform: torch.Tensor | None = None,
 ) -> None:
     """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``
-    (and, with ``kr_pool``, K with its height/width RoPE pairs rotated into ``kr_pool``)."""
+    (and, with ``kr_pool``, K with its height/width RoPE pairs rotated into ``kr_pool``; with
+    ``kv_xform``, the PRoPE copies of ``prepare_append``)."""
     prepare_append(k_new, v_new, kpool, vpool, dst_slots, frame_tokens=frame_tokens,
                    src_frame0=src_frame0, kscale=kscale, vscale=vscale, kr_pool=kr_pool,
-                   rope_hw=rope_hw, grid_hw=grid_hw)()
+                   rope_hw=rope_hw, grid_hw=grid_hw, vr_pool=vr_pool, kv_xform=kv_xform)()
 
 
 def prepare_gather(
@@ -326,12 +353,18 @@ def attention_frames(
     chunk_tokens: int = 0,
     out: torch.Tensor | None = None,
     rope: tuple[torch.Tensor, tuple[int, int], torch.Tensor] | None = None,
+    prope: tuple[torch.Tensor, tuple[int, int], torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D].
 
     ``rope = (rope_hw, grid_hw, rope_t)``: ``q`` is pre-RoPE and ``kpool`` is the height/width
     roped K copy; the kernel ropes the queries (``rope_t`` from ``rope.temporal_table`` with one
-    row per query frame and one column per entry of ``frame_slots``)."""
+    row per query frame and one column per entry of ``frame_slots``).
+
+    ``prope = (rope_hw, grid_hw, q_xform_t, q_xform_s, out_xform)``: RoPE then PRoPE; ``kpool`` /
+    ``vpool`` are the transformed copies of a PRoPE append and the tables come from
+    ``prope.PropeTables`` (float32 ``[B, n_frames, n_qframes, 11, 4, 4]``, ``[B, n_qframes, 4,
+    4]`` twice)."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("q", q)
@@ -351,7 +384,30 @@ def attention_frames(
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
     ks, vs = _scales(kpool, kscale, vscale)
     t0 = _tic()
-    if rope is None:
+    if prope is not None:
+        rope_hw, grid_hw, xt, xs, xo = prope
+        _check_rope_hw(kpool, kpool, rope_hw, grid_hw, frame_tokens)
+        nq = q.shape[1] // frame_tokens
+        if q.shape[1] != nq * frame_tokens:
+            raise ValueError(f"PRoPE queries must be whole frames (Lq={q.shape[1]})")
+        for name, t, shape in (("q_xform_t", xt, (b, len(frame_slots), nq, 11, 4, 4)),
+                               ("q_xform_s", xs, (b, nq, 4, 4)), ("out_xform", xo, (b, nq, 4, 4))):
+            _require_cuda(name, t)
+            if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous float32 {list(shape)}, got "
+                                 f"{t.dtype} {tuple(t.shape)}")
+        _lib.check(
+            "skv_attention_prope",
+            lib.skv_attention_prope(
+                q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(),
+                dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots), len(frame_slots),
+                b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode, q_pos0, chunk_tokens,
+                out.data_ptr(), osb, ost, osh, rope_hw.data_ptr(), int(grid_hw[0]),
+                int(grid_hw[1]), xt.data_ptr(), xs.data_ptr(), xo.data_ptr(), nq,
+                _stream(q.device),
+            ),
+        )
+    elif rope is None:
         _lib.check(
             "skv_attention",
             lib.skv_attention(

@@ -112,3 +112,32 @@ def test_rope_argument_errors_do_not_launch():
     assert attn(pool=_lib.SKV_F32) == _lib.SKV_E_UNSUPPORTED and b"bf16" in lib.skv_last_error()
     assert attn(nq=3) == _lib.SKV_E_ARG and b"n_qframes" in lib.skv_last_error()
     assert attn(rope_t=None) == _lib.SKV_E_ARG and b"rope_t" in lib.skv_last_error()
+
+
+def test_prope_argument_errors_do_not_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+
+    def app(**kw):
+        a = dict(pool=_lib.SKV_BF16, kx=fake, vx=fake, xf=fake, gw=8)
+        a.update(kw)
+        return lib.skv_append_prope(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, a["pool"], 4,
+                                    _slots(0), 1, 1, 1, 128, 64, a["kx"], a["vx"], fake, 8,
+                                    a["gw"], a["xf"], None)
+    assert app(vx=None) == _lib.SKV_E_ARG and b"vx_pool" in lib.skv_last_error()
+    assert app(xf=None) == _lib.SKV_E_ARG and b"kv_xform" in lib.skv_last_error()
+    assert app(pool=_lib.SKV_F32) == _lib.SKV_E_UNSUPPORTED
+    assert app(gw=7) == _lib.SKV_E_ARG and b"grid" in lib.skv_last_error()
+
+    def attn(**kw):
+        a = dict(q_len=128, T=64, pool=_lib.SKV_BF16, nq=2, xt=fake, xs=fake, xo=fake, gh=8, gw=8)
+        a.update(kw)
+        return lib.skv_attention_prope(fake, _lib.SKV_BF16, 8, 8, 8, fake, fake, a["pool"], 4,
+                                       _slots(0), 1, 1, 1, 128, a["q_len"], a["T"], 0.1, 0, 0, 0,
+                                       fake, 8, 8, 8, fake, a["gh"], a["gw"], a["xt"], a["xs"],
+                                       a["xo"], a["nq"], None)
+    assert attn(xt=None) == _lib.SKV_E_ARG and b"q_xform_t" in lib.skv_last_error()
+    assert attn(xo=None) == _lib.SKV_E_ARG and b"out_xform" in lib.skv_last_error()
+    assert attn(pool=_lib.SKV_F32) == _lib.SKV_E_UNSUPPORTED
+    assert attn(q_len=60, T=30, gh=5, gw=6) == _lib.SKV_E_UNSUPPORTED  # frames under 64 tokens
+    assert attn(nq=3) == _lib.SKV_E_ARG and b"n_qframes" in lib.skv_last_error()
