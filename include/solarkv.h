@@ -180,6 +180,95 @@ int skv_attention_prope(const void* q, int q_dtype, int64_t q_sb, int64_t q_st, 
                         const float* q_xform_t, const float* q_xform_s, const float* out_xform,
                         int n_qframes, skv_stream_t stream);
 
+/*
+ * Commit-path fusion: the reference normalises K and Q with WanRMSNorm over each token's full
+ * H x D row before the cache write and the attention (q = norm_q(q(x)), k = norm_k(k(x)),
+ * causal_model.py:908-910; WanRMSNorm model.py:69-84: x * rsqrt(mean(x²) + eps) * weight).
+ * Here the statistic is one small pass and the scaling is folded into the append (K) and into
+ * the attention kernel's Q load, so the normalised K/Q never round-trip through HBM.
+ *
+ * skv_rms_rows — inv_rms[b * rows + t] = 1 / sqrt(mean over (h, d) of x[b][t][h][d]² + eps)
+ * (fp32) for a token-major [batch][rows][heads][head_dim] tensor (bf16 or f32).
+ */
+int skv_rms_rows(const void* x, int dtype, int64_t sb, int64_t st, int64_t sh, int batch,
+                 int rows, int heads, int head_dim, float eps, float* inv_rms /* device */,
+                 skv_stream_t stream);
+
+/*
+ * Extended append: every option of skv_append / skv_append_rope / skv_append_prope plus the
+ * RMSNorm of K.  Optional members are NULL / 0 when unused.
+ *   k_inv_rms, k_rms_stride_b, k_norm_weight: source token t of stream b is stored as
+ *     k * k_inv_rms[b * k_rms_stride_b + t] * k_norm_weight[h * head_dim + c], evaluated in fp32
+ *     and rounded once to the source dtype (the reference rounds its bf16 norm several times);
+ *     the RoPE / PRoPE copies and fp8 codes derive from that rounded value.  V is not normalised.
+ *   kr_pool, rope_hw, grid_h, grid_w: the RoPE copy of K (skv_append_rope).
+ *   vx_pool, kv_xform: the PRoPE copies (skv_append_prope; kr_pool then receives K with RoPE and
+ *     P⁻¹ on its spatial groups).
+ */
+typedef struct skv_append_desc {
+  const void* k_new;
+  const void* v_new;
+  int src_dtype;
+  int64_t src_sb, src_st, src_sh;
+  int src_frame0;
+  void* k_pool;
+  void* v_pool;
+  float* k_scale;
+  float* v_scale;
+  int pool_dtype;
+  int n_slots;
+  const int32_t* dst_slots; /* host */
+  int n_frames, batch, heads, head_dim, frame_tokens;
+  const float* k_inv_rms;
+  int64_t k_rms_stride_b;
+  const float* k_norm_weight;
+  void* kr_pool;
+  const float* rope_hw;
+  int grid_h, grid_w;
+  void* vx_pool;
+  const float* kv_xform;
+} skv_append_desc;
+
+int skv_append_ex(const skv_append_desc* desc, skv_stream_t stream);
+
+/*
+ * Extended attention: every option of skv_attention / skv_attention_rope / skv_attention_prope
+ * plus the RMSNorm of Q at load (q_inv_rms[b * q_rms_stride_b + row] * q_norm_weight[h *
+ * head_dim + c], fp32, before RoPE/PRoPE; the fp8-pool kernel rounds the normalised Q to bf16
+ * before quantising it, as the reference's bf16 norm output).  Optional members NULL / 0.
+ * rope_t selects RoPE on load, q_xform_t (with q_xform_s, out_xform) RoPE + PRoPE.
+ */
+typedef struct skv_attention_desc {
+  const void* q;
+  int q_dtype;
+  int64_t q_sb, q_st, q_sh;
+  const void* k_pool;
+  const void* v_pool;
+  const float* k_scale;
+  const float* v_scale;
+  int pool_dtype;
+  int n_slots;
+  const int32_t* frame_slots; /* host */
+  int n_frames, batch, heads, head_dim, q_len, frame_tokens;
+  float softmax_scale;
+  int mask_mode;
+  int64_t q_pos0, chunk_tokens;
+  void* out;
+  int64_t out_sb, out_st, out_sh;
+  const float* q_inv_rms;
+  int64_t q_rms_stride_b;
+  const float* q_norm_weight;
+  const float* rope_hw;
+  int grid_h, grid_w;
+  const float* rope_t;
+  int n_qframes;
+  const float* q_xform_t;
+  const float* q_xform_s;
+  const float* out_xform;
+} skv_attention_desc;
+
+int skv_attention_ex(const skv_attention_desc* desc, skv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

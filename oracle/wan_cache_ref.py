@@ -26,6 +26,11 @@ Pinning (tests/test_oracle.py):
 * ``window_relative_positions`` / ``rope_positions`` — hand-derived cases of the reference's
   allocation (sink frames at 0.., the query chunk pinned at the window tail, capping at the
   EchoRoPE horizon or ``rope_train_frames``, underflow errors).
+* ``rms_norm_f64`` / ``wan_rms_norm`` — explicit loops; a constant row c maps to
+  c / sqrt(c² + eps) · w; scale invariance; the reference's in-dtype bf16 sequence stays within
+  a few bf16 roundings of the float64 form.
+* ``cross_attention`` — the cache keeps the first context (a later context is ignored) and the
+  result is attention over the normalised cached K.
 """
 
 from __future__ import annotations
@@ -543,3 +548,45 @@ def rope_positions(*, num_sink_frames: int, num_local_frames: int, num_new_frame
             f"EchoRoPE underflow while assigning positions: B={nb}, R={nl}, sink={ns}, "
             f"q_start={q_start}, local_start={local_start}, pmax={pmax}")
     return {"q_start": q_start, "local_start": local_start, "num_sink": ns}
+
+
+# ---------------------------------------------------------------------------------------------
+# q/k RMSNorm before the cache (causal_model.py:908-910; WanRMSNorm model.py:69-84) and the
+# cached cross-attention (WanCrossAttention.forward model.py:152-184)
+# ---------------------------------------------------------------------------------------------
+def wan_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """WanRMSNorm as the reference evaluates it: ``x * rsqrt(mean(x²) + eps)`` in x's own dtype,
+    then ``.type_as(x) * weight``, over the last dimension (the token's H*D channels)."""
+    return (x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps)).type_as(x) * weight
+
+
+def rms_norm_f64(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """The same normalisation evaluated in float64."""
+    xd = x.to(torch.float64)
+    return xd * torch.rsqrt(xd.pow(2).mean(dim=-1, keepdim=True) + eps) * weight.to(torch.float64)
+
+
+def norm_heads(x: torch.Tensor, weight: torch.Tensor, eps: float, fn=rms_norm_f64) -> torch.Tensor:
+    """Apply a row norm to [B, L, H, D] over the flattened H*D channels (the reference normalises
+    the projection output [B, L, C] before ``.view(b, s, n, d)``)."""
+    b, l, h, d = x.shape
+    return fn(x.reshape(b, l, h * d), weight, eps).reshape(b, l, h, d)
+
+
+def cross_attention(q_proj: torch.Tensor, ctx_k_proj: torch.Tensor, ctx_v_proj: torch.Tensor,
+                    crossattn_cache: dict[str, Any] | None, *, norm_q: Callable, norm_k: Callable,
+                    attn_fn: Callable[..., torch.Tensor] = attention) -> torch.Tensor:
+    """WanCrossAttention.forward after the projections (model.py:152-184), context_lens None as
+    on the cached inference path (causal_model.py:2730): q = norm_q(q(x)); K/V of the context
+    are computed once into the cache (``is_init``) and reused; returns the attention output
+    [B, L1, H, D] (before ``flatten`` and ``self.o``).  Inputs are [B, L, H, D]."""
+    q = norm_q(q_proj)
+    if crossattn_cache is not None:
+        if not crossattn_cache["is_init"]:
+            crossattn_cache["is_init"] = True
+            crossattn_cache["k"] = norm_k(ctx_k_proj)
+            crossattn_cache["v"] = ctx_v_proj
+        k, v = crossattn_cache["k"], crossattn_cache["v"]
+    else:
+        k, v = norm_k(ctx_k_proj), ctx_v_proj
+    return attn_fn(q, k, v)

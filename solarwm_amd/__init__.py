@@ -12,9 +12,12 @@ Public surface (the reference's call signatures, solar/backends/wan22/runtime):
 * :class:`PropeConfig`, :func:`stage_camera_cache` — fused PRoPE camera transforms on the same
   caches (``prope=`` of the allocator; one camera pass per forward, ``camera=`` of
   :func:`attend_cached`)
+* ``norm_q=`` / ``norm_k=`` of :func:`attend_cached` — q/k RMSNorm fused into the kernels
+* :func:`make_crossattn_cache_allocator`, :func:`cross_attend` — the cross-attention K/V cache
 """
 
 from .attention import apply_cache_updates, attend_cached, attention, chunk_causal_attention
+from .crossattn import CrossAttnCache, cross_attend, make_crossattn_cache_allocator
 from .cache import CacheGeometry, CachePlan, SlotKVCache, make_kv_cache_allocator, plan_cached_forward
 from .prope import PropeConfig, commit_camera_cache, drop_camera_cache, stage_camera_cache
 from .rope import RopeConfig
@@ -22,6 +25,7 @@ from .rope import RopeConfig
 __all__ = [
     "CacheGeometry",
     "CachePlan",
+    "CrossAttnCache",
     "PropeConfig",
     "RopeConfig",
     "SlotKVCache",
@@ -30,7 +34,9 @@ __all__ = [
     "attention",
     "chunk_causal_attention",
     "commit_camera_cache",
+    "cross_attend",
     "drop_camera_cache",
+    "make_crossattn_cache_allocator",
     "make_kv_cache_allocator",
     "plan_cached_forward",
     "stage_camera_cache",

@@ -31,6 +31,41 @@ SKV_MAX_FRAMES = 256
 # Every symbol include/solarkv.h declares, with (restype, argtypes).
 _i32, _i64, _f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)
+
+
+class AppendDesc(ctypes.Structure):
+    """``skv_append_desc`` (include/solarkv.h), field for field."""
+
+    _fields_ = [
+        ("k_new", _vp), ("v_new", _vp), ("src_dtype", _i32),
+        ("src_sb", _i64), ("src_st", _i64), ("src_sh", _i64), ("src_frame0", _i32),
+        ("k_pool", _vp), ("v_pool", _vp), ("k_scale", _vp), ("v_scale", _vp),
+        ("pool_dtype", _i32), ("n_slots", _i32), ("dst_slots", _i32p),
+        ("n_frames", _i32), ("batch", _i32), ("heads", _i32), ("head_dim", _i32),
+        ("frame_tokens", _i32),
+        ("k_inv_rms", _vp), ("k_rms_stride_b", _i64), ("k_norm_weight", _vp),
+        ("kr_pool", _vp), ("rope_hw", _vp), ("grid_h", _i32), ("grid_w", _i32),
+        ("vx_pool", _vp), ("kv_xform", _vp),
+    ]
+
+
+class AttentionDesc(ctypes.Structure):
+    """``skv_attention_desc`` (include/solarkv.h), field for field."""
+
+    _fields_ = [
+        ("q", _vp), ("q_dtype", _i32), ("q_sb", _i64), ("q_st", _i64), ("q_sh", _i64),
+        ("k_pool", _vp), ("v_pool", _vp), ("k_scale", _vp), ("v_scale", _vp),
+        ("pool_dtype", _i32), ("n_slots", _i32), ("frame_slots", _i32p),
+        ("n_frames", _i32), ("batch", _i32), ("heads", _i32), ("head_dim", _i32),
+        ("q_len", _i32), ("frame_tokens", _i32),
+        ("softmax_scale", _f32), ("mask_mode", _i32), ("q_pos0", _i64), ("chunk_tokens", _i64),
+        ("out", _vp), ("out_sb", _i64), ("out_st", _i64), ("out_sh", _i64),
+        ("q_inv_rms", _vp), ("q_rms_stride_b", _i64), ("q_norm_weight", _vp),
+        ("rope_hw", _vp), ("grid_h", _i32), ("grid_w", _i32), ("rope_t", _vp), ("n_qframes", _i32),
+        ("q_xform_t", _vp), ("q_xform_s", _vp), ("out_xform", _vp),
+    ]
+
+
 SIGNATURES: dict[str, tuple] = {
     "skv_version": (_i32, []),
     "skv_last_error": (ctypes.c_char_p, []),
@@ -70,6 +105,12 @@ SIGNATURES: dict[str, tuple] = {
          _i32, _f32, _i32, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i32, _i32, _vp, _vp, _vp,
          _i32, _vp],
     ),
+    "skv_rms_rows": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp],
+    ),
+    "skv_append_ex": (_i32, [ctypes.POINTER(AppendDesc), _vp]),
+    "skv_attention_ex": (_i32, [ctypes.POINTER(AttentionDesc), _vp]),
 }
 
 _lock = threading.Lock()

@@ -132,6 +132,25 @@ def chunk_causal_attention(
     ).to(out_dtype)
 
 
+def norm_spec(norm, heads: int, device) -> tuple[torch.Tensor, float]:
+    """(float32 weight [H*D] on ``device``, eps) of a WanRMSNorm-like object (``.weight``,
+    ``.eps``) or a ``(weight, eps)`` pair."""
+    if isinstance(norm, tuple):
+        weight, eps = norm
+    else:
+        weight, eps = norm.weight, norm.eps
+    w = weight.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if w.numel() != heads * kernels.HEAD_DIM:
+        raise ValueError(f"norm weight has {w.numel()} entries, expected {heads * kernels.HEAD_DIM}")
+    return w, float(eps)
+
+
+def _row_norm(x: torch.Tensor, norm, heads: int):
+    """(inv_rms [B, L], weight) of ``x`` for the kernels' fused RMSNorm."""
+    w, eps = norm_spec(norm, heads, x.device)
+    return kernels.rms_rows(x, eps), w
+
+
 def window_positions(kv_cache: SlotKVCache, plan, window: Sequence[int], nb: int,
                      current_start: int) -> tuple[list[int], list[int]]:
     """RoPE temporal positions (query frames, key frames in window order) of one cached forward:
@@ -159,6 +178,8 @@ def attend_cached(
     softmax_scale: float | None = None,
     out: torch.Tensor | None = None,
     camera: CameraPass | None = None,
+    norm_q=None,
+    norm_k=None,
 ) -> tuple[torch.Tensor, tuple[int, int, CacheUpdate]]:
     """One layer's cached self-attention (causal_model.py:1028-1235, post-projection/RoPE).
 
@@ -170,8 +191,11 @@ def attend_cached(
     ``memory_frames`` (bank indices, in order), and nothing in the committed cache changes until
     :func:`apply_cache_updates`.  ``camera`` (from ``prope.stage_camera_cache``, once per forward
     for all layers) applies fused PRoPE after RoPE (causal_model.py:1170-1199) and returns the
-    output mapped back by the query cameras.  Returns ``(out [B, Lq, H, D], (current_end,
-    local_end_index, update))``.
+    output mapped back by the query cameras.  ``norm_q`` / ``norm_k`` (the layer's WanRMSNorm
+    modules, or ``(weight, eps)``) take the raw projections: K is normalised inside the append
+    and Q at the attention kernel's load, the reference's ``norm_q(q(x))`` / ``norm_k(k(x))``
+    (causal_model.py:908-910) without a round trip through HBM.  Returns ``(out [B, Lq, H, D],
+    (current_end, local_end_index, update))``.
     """
     g = kv_cache.geom
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
@@ -208,6 +232,7 @@ def attend_cached(
             grid_hw=rope.cfg.grid_hw if rope is not None else None,
             vr_pool=kv_cache.vrpool if camera is not None else None,
             kv_xform=camera.kv_xform if camera is not None else None,
+            k_norm=_row_norm(k, norm_k, g.heads) if norm_k is not None else None,
         )
     frames = list(kv_cache.bank_slots(memory_frames)) if memory_frames else []
     frames.extend(window)
@@ -230,7 +255,7 @@ def attend_cached(
     x = kernels.attention_frames(
         q, kpool, vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
         kscale=kv_cache.kscale, vscale=kv_cache.vscale, out=out, rope=rope_args,
-        prope=prope_args,
+        prope=prope_args, q_norm=_row_norm(q, norm_q, g.heads) if norm_q is not None else None,
     )
     update = kv_cache.stage(plan, temp)
     return x, (plan.current_end, plan.local_end_index, update)

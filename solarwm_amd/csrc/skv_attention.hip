@@ -67,6 +67,11 @@ struct AttnArgs {
   const float* pq_t;
   const float* pq_s;
   const float* pq_o;
+  // RMSNorm of Q at load (the reference's norm_q): row r of stream b is scaled by
+  // q_rms[b * q_rms_sb + r] and channel h*D + c by q_w[h*D + c] (fp32); nullptr = Q as given
+  const float* q_rms;
+  int64_t q_rms_sb;
+  const float* q_w;
   int32_t slots[SKV_MAX_FRAMES];
 };
 
@@ -264,6 +269,9 @@ void attn_kernel(AttnArgs a) {
   {
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
                    (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 8;
+    // RMSNorm factor of this row (0 for dead rows) and its channel weights
+    const float qn = a.q_rms && qlive ? a.q_rms[(int64_t)b * a.q_rms_sb + qrow] : 0.f;
+    const float* qw = a.q_w + h * kHeadDim + hh * 8;
     if constexpr (RM > 0) {
       const int qr = qlive ? qrow : a.Lq - 1;
       qfi = qr / a.T;
@@ -272,8 +280,13 @@ void attn_kernel(AttnArgs a) {
       for (int k = 0; k < 8; ++k) {
         const Vec8<QT> x = qlive ? Vec8<QT>::load(qp + k * 16) : Vec8<QT>::zero();
         Vec8<float> y;
+        if (a.q_rms) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y.set(e, (float)(bf16)x.get(e));
+          for (int e = 0; e < 8; ++e) y.set(e, (float)x.get(e) * qn * qw[k * 16 + e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y.set(e, (float)(bf16)x.get(e));
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const int pr = k * 8 + hh * 4 + m;
@@ -295,6 +308,15 @@ void attn_kernel(AttnArgs a) {
       }
 #pragma unroll
       for (int k = 0; k < 3; ++k) qt0[k] = qf[k];
+    } else if (a.q_rms) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const Vec8<QT> x = qlive ? Vec8<QT>::load(qp + k * 16) : Vec8<QT>::zero();
+        Vec8<float> y;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y.set(e, (float)x.get(e) * qn * qw[k * 16 + e]);
+        qf[k] = y.to_bf16();
+      }
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
@@ -693,11 +715,18 @@ void attn_fp8_kernel(AttnArgs a) {
     float qv[64];
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
                    (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 64;
+    const float qn = a.q_rms && qlive ? a.q_rms[(int64_t)b * a.q_rms_sb + qrow] : 0.f;
+    const float* qw = a.q_w + h * kHeadDim + hh * 64;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       Vec8<QT> v = qlive ? Vec8<QT>::load(qp + c * 8) : Vec8<QT>::zero();
+      if (a.q_rms) {  // normalised Q in bf16, as the reference's norm_q output
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qv[c * 8 + j] = (float)(bf16)v.get(j);  // bf16 rounding first
+        for (int j = 0; j < 8; ++j) qv[c * 8 + j] = (float)(bf16)((float)v.get(j) * qn * qw[c * 8 + j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qv[c * 8 + j] = (float)(bf16)v.get(j);  // bf16 rounding first
+      }
     }
     float amax = 0.f;
 #pragma unroll
@@ -982,7 +1011,9 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
                           int64_t chunk_tokens, void* out, int64_t out_sb, int64_t out_st,
                           int64_t out_sh, const float* rope_hw, int grid_h, int grid_w,
                           const float* rope_t, int n_qframes, const float* pq_t,
-                          const float* pq_s, const float* pq_o, skv_stream_t stream) {
+                          const float* pq_s, const float* pq_o, skv_stream_t stream,
+                          const float* q_inv_rms = nullptr, int64_t q_rms_sb = 0,
+                          const float* q_norm_weight = nullptr) {
   if (!q || !k_pool || !v_pool || !frame_slots || !out) {
     set_error("skv_attention: null pointer argument");
     return SKV_E_ARG;
@@ -1034,6 +1065,14 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
               frame_tokens);
     return SKV_E_ARG;
   }
+  if ((q_inv_rms == nullptr) != (q_norm_weight == nullptr)) {
+    set_error("skv_attention_ex: Q RMSNorm needs both q_inv_rms and q_norm_weight");
+    return SKV_E_ARG;
+  }
+  if (q_inv_rms && q_rms_sb < q_len) {
+    set_error("skv_attention_ex: q_rms_stride_b=%lld < q_len=%d", (long long)q_rms_sb, q_len);
+    return SKV_E_ARG;
+  }
   const bool prope = pq_t != nullptr;
   const bool rope = rope_t != nullptr || prope;
   if (prope && (!pq_s || !pq_o)) {
@@ -1068,6 +1107,9 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   a.pq_t = pq_t;
   a.pq_s = pq_s;
   a.pq_o = pq_o;
+  a.q_rms = q_inv_rms;
+  a.q_rms_sb = q_rms_sb;
+  a.q_w = q_norm_weight;
   a.gh = grid_h;
   a.gw = grid_w;
   a.n_qframes = n_qframes;
@@ -1187,4 +1229,27 @@ extern "C" int skv_attention_prope(const void* q, int q_dtype, int64_t q_sb, int
                         frame_tokens, softmax_scale, mask_mode, q_pos0, chunk_tokens, out, out_sb,
                         out_st, out_sh, rope_hw, grid_h, grid_w, nullptr, n_qframes, q_xform_t,
                         q_xform_s, out_xform, stream);
+}
+
+extern "C" int skv_attention_ex(const skv_attention_desc* d, skv_stream_t stream) {
+  clear_error();
+  if (!d) {
+    set_error("skv_attention_ex: null descriptor");
+    return SKV_E_ARG;
+  }
+  if (d->rope_t && d->q_xform_t) {
+    set_error("skv_attention_ex: give rope_t (RoPE) or q_xform_t (RoPE + PRoPE), not both");
+    return SKV_E_ARG;
+  }
+  if (d->pool_dtype == SKV_FP8_E4M3 && (d->rope_t || d->q_xform_t)) {
+    set_error("skv_attention_ex: RoPE / PRoPE need bf16 pools");
+    return SKV_E_UNSUPPORTED;
+  }
+  return attention_impl(d->q, d->q_dtype, d->q_sb, d->q_st, d->q_sh, d->k_pool, d->v_pool,
+                        d->k_scale, d->v_scale, d->pool_dtype, d->n_slots, d->frame_slots,
+                        d->n_frames, d->batch, d->heads, d->head_dim, d->q_len, d->frame_tokens,
+                        d->softmax_scale, d->mask_mode, d->q_pos0, d->chunk_tokens, d->out,
+                        d->out_sb, d->out_st, d->out_sh, d->rope_hw, d->grid_h, d->grid_w,
+                        d->rope_t, d->n_qframes, d->q_xform_t, d->q_xform_s, d->out_xform, stream,
+                        d->q_inv_rms, d->q_rms_stride_b, d->q_norm_weight);
 }

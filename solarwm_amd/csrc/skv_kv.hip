@@ -32,8 +32,24 @@ struct AppendArgs {
   // vrpool (V, laid out as vpool) receive P^-1 x per group of 4 channels
   void* vrpool;
   const float* kv_xf;
+  // RMSNorm of K (the reference's norm_k before the cache write): source token t of stream b
+  // is scaled by krms[b * krms_sb + t] (1 / RMS over the token's H x D row) and channel
+  // h*D + c by kw[h*D + c], in fp32, then rounded once to the source dtype; nullptr = raw K
+  const float* krms;
+  int64_t krms_sb;
+  const float* kw;
   int32_t slots[SKV_MAX_APPEND_FRAMES];
 };
+
+// K row [col, col+8) of source token `tok` (stream b, head h) through RMSNorm: x * rms * w,
+// fp32 products, one rounding to E (the value the raw pool stores and everything derives from)
+template <typename E>
+__device__ inline void norm8(Vec8<E>& v, const AppendArgs& a, int b, int h, int64_t tok, int col) {
+  const float r = a.krms[(int64_t)b * a.krms_sb + tok];
+  const float* w = a.kw + h * kHeadDim + col;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v.set(e, (E)((float)v.get(e) * r * w[e]));
+}
 
 // Wan splits a head's 64 complex channel pairs (2i, 2i+1) into 22 temporal, 21 height and 21
 // width pairs (causal_model.py:1855-1866).
@@ -125,6 +141,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
       const bool live = tok0 + row < a.T;
       Vec8<E> kv = live ? Vec8<E>::load(ks + src_base + (int64_t)(tok0 + row) * a.s_st + col)
                         : Vec8<E>::zero();
+      if (a.krms && live) norm8(kv, a, b, h, (int64_t)(a.src_frame0 + f) * a.T + tok0 + row, col);
       kv.store_nt(kp + row * kHeadDim + col);
       if constexpr (XM > 0) {
         if (live && col + 8 > 2 * kRopeT) {
@@ -282,11 +299,26 @@ __global__ __launch_bounds__(1024) void append_fp8_reg_kernel(AppendArgs a) {
     if (j < nt && kTile * j + rr < a.T)
       r[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off + j * row_step, 0, 0));
   }
-  // chunk j of this thread wherever it lives, zero for rows >= T
+  const bool knorm = !is_v && a.krms;
+  const int64_t tok_base = (int64_t)(a.src_frame0 + f) * a.T;
+  auto normed = [&](u32x4 x, int row) -> u32x4 {
+    Vec8<bf16> v;
+    v.r = x;
+    norm8(v, a, b, h, tok_base + row, col);
+    return v.r;
+  };
+  if (knorm) {
+#pragma unroll
+    for (int j = 0; j < kFp8RegChunks; ++j)
+      if (j < nt && kTile * j + rr < a.T) r[j] = normed(r[j], kTile * j + rr);
+  }
+  // chunk j of this thread wherever it lives (normalised K), zero for rows >= T
   auto chunk = [&](int j) -> u32x4 {
     if (j < kFp8RegChunks) return r[j];
-    return (kTile * j + rr < a.T) ? *reinterpret_cast<const u32x4*>(my_stage + (j - kFp8RegChunks) * kChunkBytes)
-                                  : u32x4{0u, 0u, 0u, 0u};
+    const int row = kTile * j + rr;
+    if (row >= a.T) return u32x4{0u, 0u, 0u, 0u};
+    const u32x4 x = *reinterpret_cast<const u32x4*>(my_stage + (j - kFp8RegChunks) * kChunkBytes);
+    return knorm ? normed(x, row) : x;
   };
   u16x2 mm = {0, 0};
 #pragma unroll
@@ -361,12 +393,16 @@ __global__ __launch_bounds__(1024) void append_fp8_kernel(AppendArgs a) {
   const E* src = static_cast<const E*>(is_v ? a.vsrc : a.ksrc);
   src += (int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)(a.src_frame0 + f) * a.T * a.s_st;
 
+  const bool knorm = !is_v && a.krms;
+  const int64_t tok_base = (int64_t)(a.src_frame0 + f) * a.T;
   // Pass 1: absmax over T rows x 16 vec8.
   float m = 0.f;
   const int nvec = a.T * 16;
   for (int c = tid; c < nvec; c += 1024) {
     const int row = c >> 4, col = (c & 15) * 8;
-    m = absval8(Vec8<E>::load(src + (int64_t)row * a.s_st + col), m);
+    Vec8<E> x = Vec8<E>::load(src + (int64_t)row * a.s_st + col);
+    if (knorm) norm8(x, a, b, h, tok_base + row, col);
+    m = absval8(x, m);
   }
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -392,6 +428,7 @@ __global__ __launch_bounds__(1024) void append_fp8_kernel(AppendArgs a) {
     const int row = c >> 4, col = (c & 15) * 8;
     const bool live = t0 + row < a.T;
     Vec8<E> v = live ? Vec8<E>::load(src + (int64_t)(t0 + row) * a.s_st + col) : Vec8<E>::zero();
+    if (knorm && live) norm8(v, a, b, h, tok_base + t0 + row, col);
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -416,6 +453,38 @@ __global__ __launch_bounds__(1024) void append_fp8_kernel(AppendArgs a) {
       __syncthreads();
     }
   }
+}
+
+// Inverse RMS of each token's H x D row (WanRMSNorm's statistic, model.py:69-84):
+// out[b * rows + t] = 1 / sqrt(mean(x^2) + eps) in fp32.  One wave per token: lane l sums the
+// squares of 8-element chunks l, l+64, ... of the row (chunk c = head c / 16, channels
+// (c % 16) * 8 .. +8), then the wave reduces.
+struct RmsArgs {
+  const void* x;
+  int64_t sb, st, sh;
+  int B, rows, H;
+  float eps;
+  float* out;
+};
+
+template <typename E>
+__global__ __launch_bounds__(256) void rms_rows_kernel(RmsArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.B * a.rows) return;  // whole waves
+  const int b = row / a.rows, t = row - b * a.rows;
+  const int lane = threadIdx.x & 63;
+  const E* base = static_cast<const E*>(a.x) + (int64_t)b * a.sb + (int64_t)t * a.st;
+  float s = 0.f;
+  for (int c = lane; c < a.H * 16; c += 64) {
+    const Vec8<E> v = Vec8<E>::load(base + (int64_t)(c >> 4) * a.sh + (c & 15) * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (float)v.get(e);
+      s = fmaf(x, x, s);
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) a.out[row] = 1.0f / sqrtf(s / (float)(a.H * kHeadDim) + a.eps);
 }
 
 struct GatherArgs {
@@ -552,7 +621,9 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
                        int n_slots, const int32_t* dst_slots, int n_frames, int batch,
                        int heads, int head_dim, int frame_tokens, void* kr_pool,
                        const float* rope_hw, int grid_h, int grid_w, void* vr_pool,
-                       const float* kv_xform, skv_stream_t stream) {
+                       const float* kv_xform, skv_stream_t stream,
+                       const float* k_inv_rms = nullptr, int64_t rms_sb = 0,
+                       const float* k_norm_weight = nullptr) {
   if (!k_new || !v_new || !k_pool || !v_pool || !dst_slots) {
     set_error("skv_append: null pointer argument");
     return SKV_E_ARG;
@@ -600,6 +671,15 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
     set_error("skv_append: fp8 pool needs k_scale and v_scale");
     return SKV_E_ARG;
   }
+  if ((k_inv_rms == nullptr) != (k_norm_weight == nullptr)) {
+    set_error("skv_append_ex: K RMSNorm needs both k_inv_rms and k_norm_weight");
+    return SKV_E_ARG;
+  }
+  if (k_inv_rms && rms_sb < (int64_t)(src_frame0 + n_frames) * frame_tokens) {
+    set_error("skv_append_ex: k_rms_stride_b=%lld is shorter than the source frames",
+              (long long)rms_sb);
+    return SKV_E_ARG;
+  }
   const int esz = src_dtype == SKV_F32 ? 4 : 2;
   if (src_sb % 8 || src_st % 8 || src_sh % 8 || !aligned8(k_new, esz) || !aligned8(v_new, esz)) {
     set_error("skv_append: source strides/pointers must be multiples of 8 elements");
@@ -629,6 +709,9 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   a.gw = grid_w;
   a.vrpool = vr_pool;
   a.kv_xf = kv_xform;
+  a.krms = k_inv_rms;
+  a.krms_sb = rms_sb;
+  a.kw = k_norm_weight;
   for (int f = 0; f < n_frames; ++f) {
     if (dst_slots[f] < 0 || dst_slots[f] >= n_slots) {
       set_error("skv_append: dst_slots[%d]=%d outside [0, %d)", f, dst_slots[f], n_slots);
@@ -716,6 +799,66 @@ extern "C" int skv_append_prope(const void* k_new, const void* v_new, int src_dt
                      nullptr, nullptr, pool_dtype, n_slots, dst_slots, n_frames, batch, heads,
                      head_dim, frame_tokens, kx_pool, rope_hw, grid_h, grid_w, vx_pool, kv_xform,
                      stream);
+}
+
+extern "C" int skv_append_ex(const skv_append_desc* d, skv_stream_t stream) {
+  clear_error();
+  if (!d) {
+    set_error("skv_append_ex: null descriptor");
+    return SKV_E_ARG;
+  }
+  if (d->kr_pool == nullptr && (d->vx_pool || d->kv_xform)) {
+    set_error("skv_append_ex: PRoPE copies need kr_pool");
+    return SKV_E_ARG;
+  }
+  return append_impl(d->k_new, d->v_new, d->src_dtype, d->src_sb, d->src_st, d->src_sh,
+                     d->src_frame0, d->k_pool, d->v_pool, d->k_scale, d->v_scale, d->pool_dtype,
+                     d->n_slots, d->dst_slots, d->n_frames, d->batch, d->heads, d->head_dim,
+                     d->frame_tokens, d->kr_pool, d->rope_hw, d->grid_h, d->grid_w, d->vx_pool,
+                     d->kv_xform, stream, d->k_inv_rms, d->k_rms_stride_b, d->k_norm_weight);
+}
+
+extern "C" int skv_rms_rows(const void* x, int dtype, int64_t sb, int64_t st, int64_t sh,
+                            int batch, int rows, int heads, int head_dim, float eps,
+                            float* inv_rms, skv_stream_t stream) {
+  clear_error();
+  if (!x || !inv_rms) {
+    set_error("skv_rms_rows: null pointer argument");
+    return SKV_E_ARG;
+  }
+  if (head_dim != kHeadDim) {
+    set_error("skv_rms_rows: head_dim=%d unsupported (built for %d)", head_dim, kHeadDim);
+    return SKV_E_UNSUPPORTED;
+  }
+  if (batch <= 0 || rows < 0 || heads <= 0 || !(eps >= 0.f)) {
+    set_error("skv_rms_rows: bad sizes (batch=%d rows=%d heads=%d eps=%g)", batch, rows, heads,
+              (double)eps);
+    return SKV_E_ARG;
+  }
+  if (!(dtype == SKV_BF16 || dtype == SKV_F32)) {
+    set_error("skv_rms_rows: dtype=%d unsupported", dtype);
+    return SKV_E_UNSUPPORTED;
+  }
+  const int esz = dtype == SKV_F32 ? 4 : 2;
+  if (sb % 8 || st % 8 || sh % 8 || !aligned8(x, esz)) {
+    set_error("skv_rms_rows: strides/pointer must be multiples of 8 elements");
+    return SKV_E_ARG;
+  }
+  if (rows == 0) return SKV_OK;
+  RmsArgs a{x, sb, st, sh, batch, rows, heads, eps, inv_rms};
+  const int64_t n = (int64_t)batch * rows;
+  dim3 grid((unsigned)((n + 3) / 4));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SKV_BF16)
+    hipLaunchKernelGGL(rms_rows_kernel<bf16>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(rms_rows_kernel<float>, grid, dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("skv_rms_rows: launch failed: %s", hipGetErrorString(e));
+    return SKV_E_LAUNCH;
+  }
+  return SKV_OK;
 }
 
 extern "C" int skv_gather(const void* k_pool, const void* v_pool, int pool_dtype, int n_slots,

@@ -12,6 +12,7 @@ with ``Tp = ceil(T / 64) * 64`` and zero padding rows.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from contextlib import contextmanager
 from typing import Sequence
@@ -159,6 +160,39 @@ def _check_rope_hw(kr_pool, kpool, rope_hw, grid_hw, frame_tokens) -> None:
         raise ValueError(f"rope_hw must be contiguous float32 with {(gh + gw) * 42} entries")
 
 
+def rms_rows(x: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Inverse RMS of every token's H x D row of ``x`` [B, L, H, D]: float32 [B, L] with
+    ``1 / sqrt(mean(x²) + eps)`` (WanRMSNorm's statistic, model.py:69-84)."""
+    lib = _lib.load()
+    sb, st, sh = _token_major("x", x)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"x dtype {x.dtype} unsupported (float32 or bfloat16)")
+    b, l, h, _ = x.shape
+    if out is None:
+        out = torch.empty((b, l), dtype=torch.float32, device=x.device)
+    if out.dtype != torch.float32 or tuple(out.shape) != (b, l) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous float32 [{b}, {l}]")
+    _lib.check("skv_rms_rows", lib.skv_rms_rows(
+        x.data_ptr(), dtype_code(x.dtype), sb, st, sh, b, l, h, HEAD_DIM, float(eps),
+        out.data_ptr(), _stream(x.device)))
+    return out
+
+
+def _norm_args(name: str, norm, batch: int, rows: int, heads: int, device):
+    """Validate ``(inv_rms [B, >= rows] float32, weight [H*D] float32)``."""
+    inv, w = norm
+    _require_cuda(f"{name} inv_rms", inv)
+    _require_cuda(f"{name} weight", w)
+    if (inv.dtype != torch.float32 or inv.dim() != 2 or inv.shape[0] != batch or inv.shape[1] < rows
+            or inv.stride(1) != 1):
+        raise ValueError(f"{name} inv_rms must be float32 [{batch}, >= {rows}] with unit row stride")
+    if w.dtype != torch.float32 or w.numel() != heads * HEAD_DIM or not w.is_contiguous():
+        raise ValueError(f"{name} weight must be contiguous float32 with {heads * HEAD_DIM} entries")
+    if inv.device != device or w.device != device:
+        raise ValueError(f"{name} tensors must be on {device}")
+    return inv.data_ptr(), inv.stride(0), w.data_ptr()
+
+
 def prepare_append(
     k_new: torch.Tensor,
     v_new: torch.Tensor,
@@ -175,6 +209,7 @@ def prepare_append(
     grid_hw: tuple[int, int] | None = None,
     vr_pool: torch.Tensor | None = None,
     kv_xform: torch.Tensor | None = None,
+    k_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
 ):
     """Validate an append once and return a zero-argument launcher that enqueues it on the stream
     current now (repeated launches skip the Python-side checks).
@@ -183,7 +218,9 @@ def prepare_append(
     with the height/width pairs of RoPE applied (``rope_hw`` from ``rope.spatial_table``,
     ``grid_hw`` = the frame's patch grid).  With ``kv_xform`` (float32 ``[n_frames, B, 4, 4]``,
     the P⁻¹ of each written frame's camera) and ``vr_pool`` (shaped like ``vpool``), PRoPE is
-    applied too: ``kr_pool`` gets P⁻¹ on its spatial channel groups and ``vr_pool`` gets P⁻¹ v."""
+    applied too: ``kr_pool`` gets P⁻¹ on its spatial channel groups and ``vr_pool`` gets P⁻¹ v.
+    ``k_norm = (inv_rms, weight)`` stores RMS-normalised K (``rms_rows`` of ``k_new`` and the
+    norm's float32 weight); every copy and fp8 code derives from the normalised value."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("k_new", k_new)
@@ -239,6 +276,23 @@ def prepare_append(
             grid_hw[1], _stream(kpool.device),
         )
         moved += n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
+    if k_norm is not None:
+        # the same append through the descriptor entry point, with the RMSNorm of K
+        rms_p, rms_sb, w_p = _norm_args("k_norm", k_norm, b, (src_frame0 + n) * frame_tokens, h,
+                                        kpool.device)
+        desc = _lib.AppendDesc(
+            k_new=k_new.data_ptr(), v_new=v_new.data_ptr(), src_dtype=dtype_code(k_new.dtype),
+            src_sb=sb, src_st=st, src_sh=sh, src_frame0=src_frame0, k_pool=kpool.data_ptr(),
+            v_pool=vpool.data_ptr(), k_scale=ks, v_scale=vs, pool_dtype=dtype_code(kpool.dtype),
+            n_slots=n_slots, dst_slots=slots, n_frames=n, batch=b, heads=h, head_dim=HEAD_DIM,
+            frame_tokens=frame_tokens, k_inv_rms=rms_p, k_rms_stride_b=rms_sb, k_norm_weight=w_p,
+            kr_pool=kr_pool.data_ptr() if kr_pool is not None else None,
+            rope_hw=rope_hw.data_ptr() if kr_pool is not None else None,
+            grid_h=grid_hw[0] if kr_pool is not None else 0,
+            grid_w=grid_hw[1] if kr_pool is not None else 0,
+            vx_pool=vr_pool.data_ptr() if kv_xform is not None else None,
+            kv_xform=kv_xform.data_ptr() if kv_xform is not None else None)
+        fn_name, args = "skv_append_ex", (ctypes.byref(desc), _stream(kpool.device))
     fn = getattr(lib, fn_name)
 
     def launch() -> None:
@@ -248,7 +302,7 @@ def prepare_append(
 
     launch.bytes_moved = moved
     launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots, kr_pool, rope_hw, vr_pool,
-                   kv_xform)
+                   kv_xform, k_norm, args)
     return launch
 
 
@@ -268,13 +322,15 @@ def append_frames(
     grid_hw: tuple[int, int] | None = None,
     vr_pool: torch.Tensor | None = None,
     kv_xform: torch.Tensor | None = None,
+    k_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> None:
     """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``
     (and, with ``kr_pool``, K with its height/width RoPE pairs rotated into ``kr_pool``; with
-    ``kv_xform``, the PRoPE copies of ``prepare_append``)."""
+    ``kv_xform``, the PRoPE copies; with ``k_norm``, RMS-normalised K — see ``prepare_append``)."""
     prepare_append(k_new, v_new, kpool, vpool, dst_slots, frame_tokens=frame_tokens,
                    src_frame0=src_frame0, kscale=kscale, vscale=vscale, kr_pool=kr_pool,
-                   rope_hw=rope_hw, grid_hw=grid_hw, vr_pool=vr_pool, kv_xform=kv_xform)()
+                   rope_hw=rope_hw, grid_hw=grid_hw, vr_pool=vr_pool, kv_xform=kv_xform,
+                   k_norm=k_norm)()
 
 
 def prepare_gather(
@@ -354,6 +410,7 @@ def attention_frames(
     out: torch.Tensor | None = None,
     rope: tuple[torch.Tensor, tuple[int, int], torch.Tensor] | None = None,
     prope: tuple[torch.Tensor, tuple[int, int], torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+    q_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D].
 
@@ -364,7 +421,10 @@ def attention_frames(
     ``prope = (rope_hw, grid_hw, q_xform_t, q_xform_s, out_xform)``: RoPE then PRoPE; ``kpool`` /
     ``vpool`` are the transformed copies of a PRoPE append and the tables come from
     ``prope.PropeTables`` (float32 ``[B, n_frames, n_qframes, 11, 4, 4]``, ``[B, n_qframes, 4,
-    4]`` twice)."""
+    4]`` twice).
+
+    ``q_norm = (inv_rms, weight)``: the kernel RMS-normalises Q at load (``rms_rows`` of ``q``
+    and the norm's float32 weight), before RoPE / PRoPE."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("q", q)
@@ -384,7 +444,38 @@ def attention_frames(
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
     ks, vs = _scales(kpool, kscale, vscale)
     t0 = _tic()
-    if prope is not None:
+    if q_norm is not None:
+        rms_p, rms_sb, w_p = _norm_args("q_norm", q_norm, b, q.shape[1], h, q.device)
+        d = _lib.AttentionDesc(
+            q=q.data_ptr(), q_dtype=dtype_code(q.dtype), q_sb=sb, q_st=st, q_sh=sh,
+            k_pool=kpool.data_ptr(), v_pool=vpool.data_ptr(), k_scale=ks, v_scale=vs,
+            pool_dtype=dtype_code(kpool.dtype), n_slots=n_slots,
+            frame_slots=_lib.int32_array(frame_slots), n_frames=len(frame_slots), batch=b, heads=h,
+            head_dim=HEAD_DIM, q_len=q.shape[1], frame_tokens=frame_tokens, softmax_scale=scale,
+            mask_mode=mask_mode, q_pos0=q_pos0, chunk_tokens=chunk_tokens, out=out.data_ptr(),
+            out_sb=osb, out_st=ost, out_sh=osh, q_inv_rms=rms_p, q_rms_stride_b=rms_sb,
+            q_norm_weight=w_p)
+        nq = q.shape[1] // frame_tokens
+        if rope is not None or prope is not None:
+            rhw, ghw = (rope or prope)[0], (rope or prope)[1]
+            _check_rope_hw(kpool, kpool, rhw, ghw, frame_tokens)
+            if q.shape[1] != nq * frame_tokens:
+                raise ValueError(f"RoPE queries must be whole frames (Lq={q.shape[1]})")
+            d.rope_hw, d.grid_h, d.grid_w, d.n_qframes = rhw.data_ptr(), int(ghw[0]), int(ghw[1]), nq
+        if rope is not None:
+            rt = rope[2]
+            if tuple(rt.shape) != (nq, len(frame_slots), 22, 2) or rt.dtype != torch.float32:
+                raise ValueError("rope_t must be float32 [n_qframes, n_frames, 22, 2]")
+            d.rope_t = rt.data_ptr()
+        if prope is not None:
+            xt, xs, xo = prope[2], prope[3], prope[4]
+            for name, t, shape in (("q_xform_t", xt, (b, len(frame_slots), nq, 11, 4, 4)),
+                                   ("q_xform_s", xs, (b, nq, 4, 4)), ("out_xform", xo, (b, nq, 4, 4))):
+                if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
+                    raise ValueError(f"{name} must be contiguous float32 {list(shape)}")
+            d.q_xform_t, d.q_xform_s, d.out_xform = xt.data_ptr(), xs.data_ptr(), xo.data_ptr()
+        _lib.check("skv_attention_ex", lib.skv_attention_ex(ctypes.byref(d), _stream(q.device)))
+    elif prope is not None:
         rope_hw, grid_hw, xt, xs, xo = prope
         _check_rope_hw(kpool, kpool, rope_hw, grid_hw, frame_tokens)
         nq = q.shape[1] // frame_tokens

@@ -141,3 +141,59 @@ def test_prope_argument_errors_do_not_launch():
     assert attn(pool=_lib.SKV_F32) == _lib.SKV_E_UNSUPPORTED
     assert attn(q_len=60, T=30, gh=5, gw=6) == _lib.SKV_E_UNSUPPORTED  # frames under 64 tokens
     assert attn(nq=3) == _lib.SKV_E_ARG and b"n_qframes" in lib.skv_last_error()
+
+
+@pytest.mark.parametrize("cname,pyname", [("skv_append_desc", "AppendDesc"),
+                                          ("skv_attention_desc", "AttentionDesc")])
+def test_descriptor_layout_matches_header(tmp_path, cname, pyname):
+    """The ctypes mirrors of the descriptor structs have the C compiler's size and offsets."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    py = getattr(_lib, pyname)
+    fields = [f for f, _ in py._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text(
+        f'#include <stdio.h>\n#include <stddef.h>\n#include "solarkv.h"\nint main(void) {{\n'
+        f'  printf("%zu\\n", sizeof({cname}));\n'
+        + "".join(f'  printf("%zu\\n", offsetof({cname}, {f}));\n' for f in fields)
+        + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(py)
+    assert got[1:] == [getattr(py, f).offset for f in fields]
+
+
+def test_extended_entry_points_reject_bad_options():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.skv_append_ex(None, None) == _lib.SKV_E_ARG
+    d = _lib.AppendDesc(k_new=fake, v_new=fake, src_dtype=_lib.SKV_BF16, src_sb=8, src_st=8,
+                        src_sh=8, k_pool=fake, v_pool=fake, pool_dtype=_lib.SKV_BF16, n_slots=4,
+                        dst_slots=_slots(0), n_frames=1, batch=1, heads=1, head_dim=128,
+                        frame_tokens=64, k_inv_rms=fake)
+    assert lib.skv_append_ex(ctypes.byref(d), None) == _lib.SKV_E_ARG  # weight missing
+    assert b"k_norm_weight" in lib.skv_last_error()
+    d.k_norm_weight, d.k_rms_stride_b = fake, 32
+    assert lib.skv_append_ex(ctypes.byref(d), None) == _lib.SKV_E_ARG  # stride too short
+    d.k_inv_rms = d.k_norm_weight = None
+    d.vx_pool = fake
+    assert lib.skv_append_ex(ctypes.byref(d), None) == _lib.SKV_E_ARG  # PRoPE without kr_pool
+    a = _lib.AttentionDesc(q=fake, q_dtype=_lib.SKV_BF16, q_sb=8, q_st=8, q_sh=8, k_pool=fake,
+                           v_pool=fake, pool_dtype=_lib.SKV_BF16, n_slots=4, frame_slots=_slots(0),
+                           n_frames=1, batch=1, heads=1, head_dim=128, q_len=64, frame_tokens=64,
+                           softmax_scale=0.1, out=fake, out_sb=8, out_st=8, out_sh=8,
+                           q_norm_weight=fake)
+    assert lib.skv_attention_ex(ctypes.byref(a), None) == _lib.SKV_E_ARG  # q_inv_rms missing
+    a.q_inv_rms, a.q_rms_stride_b = fake, 32
+    assert lib.skv_attention_ex(ctypes.byref(a), None) == _lib.SKV_E_ARG  # stride < q_len
+    a.q_rms_stride_b, a.rope_t, a.q_xform_t = 64, fake, fake
+    assert lib.skv_attention_ex(ctypes.byref(a), None) == _lib.SKV_E_ARG  # both RoPE modes
+    st = lib.skv_rms_rows(fake, _lib.SKV_BF16, 8, 8, 8, 1, 4, 1, 64, 1e-6, fake, None)
+    assert st == _lib.SKV_E_UNSUPPORTED
+    st = lib.skv_rms_rows(fake, _lib.SKV_BF16, 8, 8, 8, 1, 4, 1, 128, -1.0, fake, None)
+    assert st == _lib.SKV_E_ARG

@@ -423,3 +423,48 @@ def test_cached_attention_rope_wiring():
         assert kpos[-1] == pos["q_start"] + 1  # the chunk's own keys share the queries' slots
         ref.apply_cache_updates([cache], [(0, (cur_end, loc_end, info))])
     assert not torch.equal(cache["k"], ref.rope_frames(cache["k"][:, :5 * T], (gh, gw), range(5), f))
+
+
+# --- RMSNorm and cached cross-attention -------------------------------------------------------
+def test_rms_norm_loops_and_closed_forms():
+    g = torch.Generator().manual_seed(40)
+    x = torch.randn(2, 3, 16, generator=g, dtype=torch.float64)
+    w = torch.rand(16, generator=g, dtype=torch.float64) + 0.5
+    got = ref.rms_norm_f64(x, w, 1e-6)
+    for b in range(2):
+        for t in range(3):
+            ms = sum(float(x[b, t, c]) ** 2 for c in range(16)) / 16
+            for c in range(16):
+                assert abs(float(got[b, t, c]) - float(x[b, t, c]) / math.sqrt(ms + 1e-6) * float(w[c])) < 1e-12
+    c = torch.full((1, 1, 8), -3.0, dtype=torch.float64)
+    assert torch.allclose(ref.rms_norm_f64(c, torch.ones(8, dtype=torch.float64), 0.5),
+                          torch.full_like(c, -3.0 / math.sqrt(9.5)))
+    # scale invariance (eps negligible)
+    assert torch.allclose(ref.rms_norm_f64(7.0 * x, w, 1e-12), ref.rms_norm_f64(x, w, 1e-12), atol=1e-12)
+
+
+def test_reference_bf16_rms_norm_near_f64():
+    """The reference's in-dtype bf16 evaluation (about four roundings) stays within 2^-6 relative
+    of the float64 form."""
+    g = torch.Generator().manual_seed(41)
+    x = (torch.randn(2, 64, 1536, generator=g) * 3).bfloat16()
+    w = (torch.rand(1536, generator=g) + 0.5).bfloat16()
+    got = ref.wan_rms_norm(x, w, 1e-6).double()
+    want = ref.rms_norm_f64(x, w, 1e-6)
+    assert float(((got - want).abs() / want.abs().clamp_min(1e-3)).max()) < 2.0**-6
+
+
+def test_cross_attention_cache_keeps_first_context():
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(1, 5, 2, 16, generator=g, dtype=torch.float64)
+    k1, v1 = (torch.randn(1, 7, 2, 16, generator=g, dtype=torch.float64) for _ in range(2))
+    k2, v2 = (torch.randn(1, 7, 2, 16, generator=g, dtype=torch.float64) for _ in range(2))
+    w = torch.rand(32, generator=g, dtype=torch.float64) + 0.5
+    nq = nk = lambda x: ref.norm_heads(x, w, 1e-6)
+    att = lambda a, b, c: ref.attention(a, b, c, round_inputs_to_bf16=False)
+    cache = {"k": None, "v": None, "is_init": False}
+    x1 = ref.cross_attention(q, k1, v1, cache, norm_q=nq, norm_k=nk, attn_fn=att)
+    x2 = ref.cross_attention(q, k2, v2, cache, norm_q=nq, norm_k=nk, attn_fn=att)
+    assert cache["is_init"] and torch.equal(x1, x2)
+    assert torch.allclose(x1, att(nq(q), nk(k1), v1))
+    assert not torch.allclose(x1, ref.cross_attention(q, k2, v2, None, norm_q=nq, norm_k=nk, attn_fn=att))
