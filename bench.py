@@ -534,6 +534,83 @@ def c2_rope(device, fill=7, timed=2, prope=False):
     }
 
 
+def commit_path(device, iters=20):
+    """Config 2, one layer in steady state: what q/k RMSNorm (causal_model.py:908-910) costs on
+    our path (norms folded into the append and the attention Q load, plus two inverse-RMS
+    passes) against the reference's in-dtype bf16 norm_q + norm_k (WanRMSNorm, model.py:69-84)
+    on the same tensors; and cross-attention over the cached 512-token text context (ours: the
+    attention kernel with Q normalised at load; reference: norm_q + flash SDPA over the cached
+    K/V, model.py:152-184)."""
+    from types import SimpleNamespace
+
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from solarwm_amd import attend_cached, cross_attend, make_crossattn_cache_allocator
+
+    cfg = dict(CONFIGS["c2"], layers=1)
+    T, Lq, H = cfg["T"], cfg["chunk_f"] * cfg["T"], cfg["heads"]
+    inputs = make_inputs(cfg, device)
+    q, k, v = inputs[0]
+    g = torch.Generator(device=device).manual_seed(3)
+    norm = [SimpleNamespace(weight=(torch.rand(H * 128, generator=g, device=device) + 0.5).bfloat16(),
+                            eps=1e-6) for _ in range(2)]
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters * 1e3  # us
+
+    caches = make_caches(cfg, device)
+    run_ours(cfg, inputs, caches, range(7))
+    start = 7 * Lq
+    plain = timed(lambda: attend_cached(q, k, v, caches[0], start))
+    fused = timed(lambda: attend_cached(q, k, v, caches[0], start, norm_q=norm[0], norm_k=norm[1]))
+
+    def ref_norms():
+        for x, n in ((q, norm[0]), (k, norm[1])):
+            xf = x.reshape(cfg["batch"], Lq, H * 128)
+            (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + n.eps)).type_as(xf) * n.weight
+
+    ref_norm = timed(ref_norms)
+    del caches
+    xc = make_crossattn_cache_allocator(num_layers=1, num_heads=H, head_dim=128)(
+        cfg["batch"], dtype=torch.bfloat16, device=device)[0]
+    ck = torch.randn(cfg["batch"], 512, H, 128, generator=g, device=device, dtype=torch.bfloat16)
+    cv = torch.randn_like(ck)
+    cross_attend(q, ck, cv, xc, norm_q=norm[0], norm_k=norm[1])
+    ours_x = timed(lambda: cross_attend(q, None, None, xc, norm_q=norm[0]))
+    kt, vt = ck.transpose(1, 2).contiguous(), cv.transpose(1, 2).contiguous()
+
+    def ref_cross():
+        qf = q.reshape(cfg["batch"], Lq, H * 128)
+        qn = ((qf * torch.rsqrt(qf.pow(2).mean(dim=-1, keepdim=True) + 1e-6)).type_as(qf)
+              * norm[0].weight).view(cfg["batch"], Lq, H, 128)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            torch.nn.functional.scaled_dot_product_attention(qn.transpose(1, 2).contiguous(), kt, vt)
+
+    ref_x = timed(ref_cross)
+    del inputs, xc
+    torch.cuda.empty_cache()
+    return {
+        "layer_pass_us": round(plain, 1),
+        "layer_pass_with_qk_norm_us": round(fused, 1),
+        "our_qk_norm_cost_us": round(fused - plain, 1),
+        "reference_qk_norm_us": round(ref_norm, 1),
+        "cross_attention_us": round(ours_x, 1),
+        "reference_cross_attention_us": round(ref_x, 1),
+        "workload": f"config 2 layer in steady state (Lq {Lq}, window {cfg['cap_f'] * T} keys, H{H}); "
+                    f"cross-attention Lq {Lq} over 512 cached context tokens",
+    }
+
+
 def c5_quality(device):
     """Config 5 cache memory and attention error: one steady-state layer pass with the fp8
     cache against the same pass with a bf16 cache (4 streams, 1% x20 outlier channels)."""
@@ -782,6 +859,8 @@ def main():
         log(f"[bench] aux c2_rope: {aux['c2_rope']}")
         aux["c2_prope"] = c2_rope(dev, prope=True)
         log(f"[bench] aux c2_prope: {aux['c2_prope']}")
+        aux["commit_path"] = commit_path(dev)
+        log(f"[bench] aux commit_path: {aux['commit_path']}")
         log("[bench] aux c5: fp8 vs bf16 quality")
         aux["c5"]["quality"] = c5_quality(dev)
         log(f"[bench] aux c5 quality: {aux['c5']['quality']}")
