@@ -237,6 +237,8 @@ int skv_append_ex(const skv_append_desc* desc, skv_stream_t stream);
  * head_dim + c], fp32, before RoPE/PRoPE; the fp8-pool kernel rounds the normalised Q to bf16
  * before quantising it, as the reference's bf16 norm output).  Optional members NULL / 0.
  * rope_t selects RoPE on load, q_xform_t (with q_xform_s, out_xform) RoPE + PRoPE.
+ * frame_lens (mask NONE only) lets frames hold fewer than frame_tokens keys, so a window can
+ * mix whole frames with spans of other lengths (the H3 prefix rows, memory_kv_attention.py).
  */
 typedef struct skv_attention_desc {
   const void* q;
@@ -265,6 +267,8 @@ typedef struct skv_attention_desc {
   const float* q_xform_t;
   const float* q_xform_s;
   const float* out_xform;
+  const int32_t* frame_lens; /* host, optional: valid keys of each listed frame (1..frame_tokens;
+                                keys past it are masked), for spans that are not whole frames */
 } skv_attention_desc;
 
 int skv_attention_ex(const skv_attention_desc* desc, skv_stream_t stream);

@@ -62,7 +62,7 @@ class AttentionDesc(ctypes.Structure):
         ("out", _vp), ("out_sb", _i64), ("out_st", _i64), ("out_sh", _i64),
         ("q_inv_rms", _vp), ("q_rms_stride_b", _i64), ("q_norm_weight", _vp),
         ("rope_hw", _vp), ("grid_h", _i32), ("grid_w", _i32), ("rope_t", _vp), ("n_qframes", _i32),
-        ("q_xform_t", _vp), ("q_xform_s", _vp), ("out_xform", _vp),
+        ("q_xform_t", _vp), ("q_xform_s", _vp), ("out_xform", _vp), ("frame_lens", _i32p),
     ]
 
 

@@ -73,6 +73,9 @@ struct AttnArgs {
   int64_t q_rms_sb;
   const float* q_w;
   int32_t slots[SKV_MAX_FRAMES];
+  // valid keys of each listed frame (T unless the caller gives ragged frames, e.g. a prefix span
+  // stored in partly filled slots); keys t >= flen[j] of frame j are masked
+  uint16_t flen[SKV_MAX_FRAMES];
 };
 
 // Wan's split of a head's 64 complex channel pairs (2i, 2i+1): 22 temporal, 21 height, 21 width
@@ -421,11 +424,12 @@ void attn_kernel(AttnArgs a) {
     return (int64_t)a.slots[j] * a.slot_stride + kbh + t * kTile;
   };
   // mask decision for tile tau (uniform): returns true if any key of the tile may be hidden
-  auto tile_needs_mask = [&](int tau, int& tok0, int& key0) -> bool {
+  auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
     tok0 = t * kTile;
     key0 = j * a.T + tok0;
-    return (tok0 + kTile > a.T) || (key0 + kTile > lim_lo);
+    tj = a.flen[j];
+    return (tok0 + kTile > tj) || (key0 + kTile > lim_lo);
   };
 
   f32x16 oacc[4];
@@ -469,8 +473,8 @@ void attn_kernel(AttnArgs a) {
     __syncthreads();
     if constexpr (RM > 0) rot_q(0);
     qk_tile(kb_lds(0) + lane16, qf, s_cur);
-    int tok0, key0;
-    if (tile_needs_mask(0, tok0, key0)) mask_tile(s_cur, hh, tok0, a.T, key0, lim_lane);
+    int tok0, key0, tj;
+    if (tile_needs_mask(0, tok0, key0, tj)) mask_tile(s_cur, hh, tok0, tj, key0, lim_lane);
     __syncthreads();  // K(0) read by every wave before its buffer takes K(2)
   }
 
@@ -583,8 +587,8 @@ void attn_kernel(AttnArgs a) {
     }
     l_run += lp;
     if (tau + 1 < ntau) {
-      int tok0, key0;
-      if (tile_needs_mask(tau + 1, tok0, key0)) mask_tile(s_nxt, hh, tok0, a.T, key0, lim_lane);
+      int tok0, key0, tj;
+      if (tile_needs_mask(tau + 1, tok0, key0, tj)) mask_tile(s_nxt, hh, tok0, tj, key0, lim_lane);
     }
     // K(tau+2) and V(tau) have landed; every wave is done with K(tau+1)'s and V(tau-1)'s
     // buffers (they take K(tau+3) and V(tau+1) next)
@@ -771,11 +775,12 @@ void attn_fp8_kernel(AttnArgs a) {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
     return vpool + (int64_t)a.slots[j] * a.slot_stride + kbh + t * kTile;
   };
-  auto tile_needs_mask = [&](int tau, int& tok0, int& key0) -> bool {
+  auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
     tok0 = t * kTile;
     key0 = j * a.T + tok0;
-    return (tok0 + kTile > a.T) || (key0 + kTile > lim_lo);
+    tj = a.flen[j];
+    return (tok0 + kTile > tj) || (key0 + kTile > lim_lo);
   };
   // wave w stages K double blocks b = w*kDpw + j (kb = b>>2, steps 2(b&3), 2(b&3)+1) and V^T
   // double blocks b (db = b>>1, kb = b&1)
@@ -845,8 +850,8 @@ void attn_fp8_kernel(AttnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     qk(kb_lds(0) + lane16, s_cur);
-    int tok0, key0;
-    if (tile_needs_mask(0, tok0, key0)) mask_tile8(s_cur, hh, tok0, a.T, key0, lim_lane);
+    int tok0, key0, tj;
+    if (tile_needs_mask(0, tok0, key0, tj)) mask_tile8(s_cur, hh, tok0, tj, key0, lim_lane);
     __syncthreads();
   }
   for (int tau = 0; tau < ntau; ++tau) {
@@ -908,8 +913,8 @@ void attn_fp8_kernel(AttnArgs a) {
         for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
     }
     if (tau + 1 < ntau) {
-      int tok0, key0;
-      if (tile_needs_mask(tau + 1, tok0, key0)) mask_tile8(s_nxt, hh, tok0, a.T, key0, lim_lane);
+      int tok0, key0, tj;
+      if (tile_needs_mask(tau + 1, tok0, key0, tj)) mask_tile8(s_nxt, hh, tok0, tj, key0, lim_lane);
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
@@ -1013,7 +1018,8 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
                           const float* rope_t, int n_qframes, const float* pq_t,
                           const float* pq_s, const float* pq_o, skv_stream_t stream,
                           const float* q_inv_rms = nullptr, int64_t q_rms_sb = 0,
-                          const float* q_norm_weight = nullptr) {
+                          const float* q_norm_weight = nullptr,
+                          const int32_t* frame_lens = nullptr) {
   if (!q || !k_pool || !v_pool || !frame_slots || !out) {
     set_error("skv_attention: null pointer argument");
     return SKV_E_ARG;
@@ -1151,12 +1157,28 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   a.q_pos0 = q_pos0;
   a.chunk = chunk_tokens > 0 ? chunk_tokens : 1;
   a.n_keys = (int64_t)n_frames * frame_tokens;
+  if (frame_lens && frame_tokens > 65535) {
+    set_error("skv_attention_ex: frame_lens need frame_tokens <= 65535");
+    return SKV_E_UNSUPPORTED;
+  }
+  bool ragged = false;
   for (int j = 0; j < n_frames; ++j) {
     if (frame_slots[j] < 0 || frame_slots[j] >= n_slots) {
       set_error("skv_attention: frame_slots[%d]=%d outside [0, %d)", j, frame_slots[j], n_slots);
       return SKV_E_ARG;
     }
     a.slots[j] = frame_slots[j];
+    const int len = frame_lens ? frame_lens[j] : frame_tokens;
+    if (len < 1 || len > frame_tokens) {
+      set_error("skv_attention_ex: frame_lens[%d]=%d outside [1, %d]", j, len, frame_tokens);
+      return SKV_E_ARG;
+    }
+    a.flen[j] = (uint16_t)len;
+    ragged |= len != frame_tokens;
+  }
+  if (ragged && mask_mode == SKV_MASK_CHUNK_CAUSAL) {
+    set_error("skv_attention_ex: the chunk-causal mask needs whole frames (no frame_lens)");
+    return SKV_E_UNSUPPORTED;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rm = prope ? 2 : rope ? 1 : 0;
@@ -1251,5 +1273,5 @@ extern "C" int skv_attention_ex(const skv_attention_desc* d, skv_stream_t stream
                         d->softmax_scale, d->mask_mode, d->q_pos0, d->chunk_tokens, d->out,
                         d->out_sb, d->out_st, d->out_sh, d->rope_hw, d->grid_h, d->grid_w,
                         d->rope_t, d->n_qframes, d->q_xform_t, d->q_xform_s, d->out_xform, stream,
-                        d->q_inv_rms, d->q_rms_stride_b, d->q_norm_weight);
+                        d->q_inv_rms, d->q_rms_stride_b, d->q_norm_weight, d->frame_lens);
 }

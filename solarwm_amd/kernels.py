@@ -411,6 +411,7 @@ def attention_frames(
     rope: tuple[torch.Tensor, tuple[int, int], torch.Tensor] | None = None,
     prope: tuple[torch.Tensor, tuple[int, int], torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     q_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
+    frame_lens: Sequence[int] | None = None,
 ) -> torch.Tensor:
     """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D].
 
@@ -424,7 +425,10 @@ def attention_frames(
     4]`` twice).
 
     ``q_norm = (inv_rms, weight)``: the kernel RMS-normalises Q at load (``rms_rows`` of ``q``
-    and the norm's float32 weight), before RoPE / PRoPE."""
+    and the norm's float32 weight), before RoPE / PRoPE.
+
+    ``frame_lens``: valid keys of each listed frame (``1..frame_tokens``), for windows that mix
+    whole frames with shorter spans; keys past a frame's length are masked (mask NONE only)."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("q", q)
@@ -444,8 +448,15 @@ def attention_frames(
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
     ks, vs = _scales(kpool, kscale, vscale)
     t0 = _tic()
-    if q_norm is not None:
-        rms_p, rms_sb, w_p = _norm_args("q_norm", q_norm, b, q.shape[1], h, q.device)
+    if q_norm is not None or frame_lens is not None:
+        rms_p = rms_sb = w_p = None
+        if q_norm is not None:
+            rms_p, rms_sb, w_p = _norm_args("q_norm", q_norm, b, q.shape[1], h, q.device)
+        flens = None
+        if frame_lens is not None:
+            if len(frame_lens) != len(frame_slots):
+                raise ValueError("frame_lens needs one entry per listed frame")
+            flens = _lib.int32_array(frame_lens)
         d = _lib.AttentionDesc(
             q=q.data_ptr(), q_dtype=dtype_code(q.dtype), q_sb=sb, q_st=st, q_sh=sh,
             k_pool=kpool.data_ptr(), v_pool=vpool.data_ptr(), k_scale=ks, v_scale=vs,
@@ -453,8 +464,8 @@ def attention_frames(
             frame_slots=_lib.int32_array(frame_slots), n_frames=len(frame_slots), batch=b, heads=h,
             head_dim=HEAD_DIM, q_len=q.shape[1], frame_tokens=frame_tokens, softmax_scale=scale,
             mask_mode=mask_mode, q_pos0=q_pos0, chunk_tokens=chunk_tokens, out=out.data_ptr(),
-            out_sb=osb, out_st=ost, out_sh=osh, q_inv_rms=rms_p, q_rms_stride_b=rms_sb,
-            q_norm_weight=w_p)
+            out_sb=osb, out_st=ost, out_sh=osh, q_inv_rms=rms_p, q_rms_stride_b=rms_sb or 0,
+            q_norm_weight=w_p, frame_lens=flens)
         nq = q.shape[1] // frame_tokens
         if rope is not None or prope is not None:
             rhw, ghw = (rope or prope)[0], (rope or prope)[1]

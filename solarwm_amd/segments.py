@@ -1,0 +1,234 @@
+"""Segmented attention on the frame-slot kernel: teacher-forcing masks, H3 chunk-list caches and
+memory-KV segments.
+
+Each of these reference paths attends query segments to unions of key spans:
+
+* the teacher-forcing block mask over ``[clean | noisy]`` tokens (causal_model.py:337-471): a
+  query chunk sees a sink, a bounded run of earlier clean chunks and (noisy) its own chunk;
+* H3's rollout window (sgf_attention.py:40-63, :236-258, :580-659): the chunk attends to
+  ``[prefix | last <= 5 committed chunks | chunk]`` with the raw chunk K/V kept per layer;
+* H3's memory-KV layout (memory_kv_attention.py:39-140): shared, bank, audio and chunk rows,
+  each with its own key spans.
+
+Here the key spans live in pool slots (frames of T tokens; spans that are not whole frames use
+partly filled slots with per-frame lengths) and each query segment is one launch of the
+attention kernel over its frame list, so no mask is materialised and masked-out blocks cost
+nothing.  The H3 rotary and camera transforms are applied by the caller (inputs are
+post-transform Q/K/V), as the reference applies them before its attention call.
+"""
+
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+
+from . import kernels
+
+_GEOM_ERR = "num_frames must be a positive multiple of num_frame_per_block"
+
+
+def teacher_forcing_frame_lists(*, num_frames: int, num_frame_per_block: int,
+                                max_prior_clean_chunks: int | None = None, sink_size: int = 0):
+    """[(first query frame, frame list)] per query chunk of ``[clean | noisy]`` frames (clean
+    frames 0..F-1, noisy F..2F-1): the union of the reference's key intervals
+    (causal_model.py:434-468) in frames, duplicates removed."""
+    F, nb = num_frames, num_frame_per_block
+    if nb <= 0 or F % nb:
+        raise ValueError(_GEOM_ERR)
+    if not 0 <= sink_size <= F or sink_size % nb:
+        raise ValueError(f"sink_size={sink_size} must be whole {nb}-frame chunks within {F} frames")
+    chunks = F // nb
+    default = max(0, chunks - 1)
+    m = default if max_prior_clean_chunks is None else int(max_prior_clean_chunks)
+    if not 0 <= m <= default:
+        raise ValueError(f"max_prior_clean_chunks must be in [0, {default}], got {m}")
+    out = []
+    for c in range(chunks):  # clean queries
+        frames = set(range(max(0, c - m) * nb if sink_size else 0, (c + 1) * nb))
+        frames |= set(range(min(sink_size, (c + 1) * nb)))
+        out.append((c * nb, sorted(frames)))
+    for c in range(chunks):  # noisy queries: never their own clean chunk
+        frames = set(range(min(sink_size, c * nb))) | set(range(max(0, c - m) * nb, c * nb))
+        frames |= set(range(F + c * nb, F + (c + 1) * nb))
+        out.append((F + c * nb, sorted(frames)))
+    return out
+
+
+def teacher_forcing_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                              num_frames: int, frame_seqlen: int, num_frame_per_block: int,
+                              max_prior_clean_chunks: int | None = None, sink_size: int = 0,
+                              softmax_scale: float | None = None) -> torch.Tensor:
+    """Attention of ``[clean | noisy]`` tokens under the teacher-forcing block mask
+    (build_teacher_forcing_block_mask + flex_attention, causal_model.py:337-471 and its
+    masked path); q/k/v are [B, 2 * num_frames * frame_seqlen, H, D] in bf16 or float32.
+    FlexAttention's padding rows (which only see themselves) are not produced."""
+    T = frame_seqlen
+    b, L, h, _ = q.shape
+    if k.shape != q.shape or v.shape != q.shape or L != 2 * num_frames * T:
+        raise ValueError(f"q/k/v must be [B, {2 * num_frames * T}, H, D] and share a shape")
+    lists = teacher_forcing_frame_lists(num_frames=num_frames, num_frame_per_block=num_frame_per_block,
+                                        max_prior_clean_chunks=max_prior_clean_chunks, sink_size=sink_size)
+    kv_dtype = k.dtype if k.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
+    kp, vp, _, _ = kernels.new_pools(2 * num_frames, b, h, T, kv_dtype, q.device)
+    kernels.append_frames(k.to(kv_dtype), v.to(kv_dtype), kp, vp, list(range(2 * num_frames)),
+                          frame_tokens=T)
+    qq = q if q.dtype in (torch.bfloat16, torch.float32) else q.to(kv_dtype)
+    out = torch.empty(qq.shape, dtype=qq.dtype, device=q.device)
+    rows = num_frame_per_block * T
+    for f0, frames in lists:
+        s = slice(f0 * T, f0 * T + rows)
+        kernels.attention_frames(qq[:, s], kp, vp, frames, frame_tokens=T,
+                                 softmax_scale=softmax_scale, out=out[:, s])
+    return out.to(q.dtype)
+
+
+class _SpanWriter:
+    """Writes token spans of any length into consecutive slots of a pool (the last slot of a span
+    partly filled); returns (slots, lengths)."""
+
+    def __init__(self, kpool: torch.Tensor, vpool: torch.Tensor, frame_tokens: int):
+        self.kpool, self.vpool, self.T = kpool, vpool, frame_tokens
+
+    def write(self, k: torch.Tensor, v: torch.Tensor, slots: Sequence[int]) -> list[int]:
+        T = self.T
+        n = k.shape[1]
+        nf = -(-n // T)
+        if nf != len(slots):
+            raise ValueError(f"a {n}-token span needs {nf} slots, got {len(slots)}")
+        if n == 0:
+            return []
+        whole = n // T
+        if whole:
+            kernels.append_frames(k, v, self.kpool, self.vpool, list(slots[:whole]), frame_tokens=T)
+        lens = [T] * whole
+        if n > whole * T:  # the tail goes through a zero-padded frame
+            rest = n - whole * T
+            pk = torch.zeros((k.shape[0], T, k.shape[2], k.shape[3]), dtype=k.dtype, device=k.device)
+            pv = torch.zeros_like(pk)
+            pk[:, :rest], pv[:, :rest] = k[:, whole * T :], v[:, whole * T :]
+            kernels.append_frames(pk, pv, self.kpool, self.vpool, [slots[whole]], frame_tokens=T)
+            lens.append(rest)
+        return lens
+
+
+class ChunkListKVCache:
+    """H3's raw chunk-list KV cache (sgf_attention.py:40-63) on frame slots: per layer, the last
+    ``window`` committed chunks of ``chunk_frames`` frames; ``history`` demands exactly the
+    chunks right before the requested one, as the reference does.  Each layer also has
+    ``span_frames`` slots for the per-forward prefix spans (text, anchor, bank, audio rows)."""
+
+    def __init__(self, *, num_layers: int, batch: int, heads: int, frame_tokens: int,
+                 chunk_frames: int = 5, window: int = 5, span_frames: int = 8,
+                 dtype: torch.dtype = torch.bfloat16, device="cuda"):
+        self.T, self.chunk_frames, self.window, self.span_frames = frame_tokens, chunk_frames, window, span_frames
+        self.n_chunk_slots = (window + 1) * chunk_frames
+        n_slots = self.n_chunk_slots + span_frames
+        self.pools = [kernels.new_pools(n_slots, batch, heads, frame_tokens, dtype, device)[:2]
+                      for _ in range(num_layers)]
+        self.entries: list[list[tuple[int, list[int]]]] = [[] for _ in range(num_layers)]
+        self.dtype = dtype
+
+    def clear(self) -> None:
+        self.entries = [[] for _ in self.entries]
+
+    def history(self, layer: int, chunk_index: int) -> list[tuple[int, list[int]]]:
+        entries = self.entries[layer]
+        expected = list(range(max(0, chunk_index - self.window), chunk_index))
+        if [e[0] for e in entries] != expected:
+            raise RuntimeError(f"H3 KV history differs at layer={layer}, chunk={chunk_index}")
+        return entries
+
+    def _staging(self, layer: int) -> list[int]:
+        used = {s for _, slots in self.entries[layer] for s in slots}
+        free = [s for s in range(self.n_chunk_slots) if s not in used]
+        return free[: self.chunk_frames]
+
+    def write_spans(self, layer: int, spans: Sequence[tuple[torch.Tensor, torch.Tensor]]):
+        """Store prefix spans (each [B, n, H, D] K and V) in this layer's span slots; returns one
+        (slots, lengths) pair per span."""
+        kp, vp = self.pools[layer]
+        w = _SpanWriter(kp, vp, self.T)
+        nxt = self.n_chunk_slots
+        out = []
+        for k, v in spans:
+            nf = -(-k.shape[1] // self.T)
+            if nxt + nf > self.n_chunk_slots + self.span_frames:
+                raise ValueError(f"prefix spans need more than the cache's {self.span_frames} span frames")
+            slots = list(range(nxt, nxt + nf))
+            out.append((slots, w.write(k, v, slots)))
+            nxt += nf
+        return out
+
+    def stage_chunk(self, layer: int, chunk_index: int, k: torch.Tensor, v: torch.Tensor):
+        """Append the chunk's raw K/V into free slots; returns (history frames, chunk slots)."""
+        hist = self.history(layer, chunk_index)
+        if k.shape[1] != self.chunk_frames * self.T:
+            raise ValueError(f"a chunk is {self.chunk_frames} frames of {self.T} tokens")
+        staging = self._staging(layer)
+        kp, vp = self.pools[layer]
+        kernels.append_frames(k, v, kp, vp, staging, frame_tokens=self.T)
+        return [s for _, slots in hist for s in slots], staging
+
+    def commit_staged(self, layer: int, chunk_index: int, staging: list[int]) -> None:
+        self.history(layer, chunk_index)
+        self.entries[layer] = [*self.entries[layer], (chunk_index, list(staging))][-self.window :]
+
+
+def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: ChunkListKVCache,
+                       layer: int, chunk_index: int, *, prefix: tuple[torch.Tensor, torch.Tensor] | None = None,
+                       commit: bool = False, softmax_scale: float | None = None) -> torch.Tensor:
+    """H3 rollout chunk attention (sgf_attention.py:236-258, :580-659): the chunk's queries over
+    ``[prefix | history chunks | chunk]``; ``commit`` keeps the chunk's raw K/V as the newest
+    history entry (the reference's ``control.cache.commit``)."""
+    frames, lens = [], []
+    if prefix is not None:
+        ((pslots, plens),) = cache.write_spans(layer, [prefix])
+        frames += pslots
+        lens += plens
+    hist, staging = cache.stage_chunk(layer, chunk_index, k, v)
+    frames += hist + staging
+    lens += [cache.T] * (len(hist) + len(staging))
+    kp, vp = cache.pools[layer]
+    out = kernels.attention_frames(q, kp, vp, frames, frame_tokens=cache.T,
+                                   softmax_scale=softmax_scale, frame_lens=lens)
+    if commit:
+        cache.commit_staged(layer, chunk_index, staging)
+    return out
+
+
+def memory_kv_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: ChunkListKVCache,
+                        layer: int, chunk_index: int, *, text_rows: int, n_bank: int,
+                        audio_rows: int, commit: bool = False,
+                        softmax_scale: float | None = None) -> torch.Tensor:
+    """H3 memory-KV attention (MemoryKVAttention.attend, memory_kv_attention.py:39-140) on
+    post-transform inputs packed ``[text | anchor frame | bank frames | audio | chunk]``: shared
+    rows see the shared rows, bank rows see shared + bank + history, audio rows see shared +
+    audio, the chunk sees everything; the chunk's raw K/V are committed with ``commit``."""
+    T = cache.T
+    chunk_rows = cache.chunk_frames * T
+    shared = text_rows + T
+    bank_end = shared + n_bank * T
+    prefix = bank_end + audio_rows
+    if q.shape[1] != prefix + chunk_rows or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("Memory KV packed layout mismatch")
+    spans = [(k[:, :text_rows], v[:, :text_rows]), (k[:, text_rows:shared], v[:, text_rows:shared])]
+    spans += [(k[:, shared:bank_end], v[:, shared:bank_end]), (k[:, bank_end:prefix], v[:, bank_end:prefix])]
+    (ts, tl), (anc, al), (bk, bl), (au, aul) = cache.write_spans(layer, spans)
+    hist, staging = cache.stage_chunk(layer, chunk_index, k[:, prefix:], v[:, prefix:])
+    kp, vp = cache.pools[layer]
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    full = [T] * len(hist)
+    segs = [((0, shared), ts + anc, tl + al)]
+    if n_bank:
+        segs.append(((shared, bank_end), ts + anc + bk + hist, tl + al + bl + full))
+    if audio_rows:
+        segs.append(((bank_end, prefix), ts + anc + au, tl + al + aul))
+    segs.append(((prefix, prefix + chunk_rows), ts + anc + bk + au + hist + staging,
+                 tl + al + bl + aul + full + [T] * len(staging)))
+    for (a, b), frames, lens in segs:
+        kernels.attention_frames(q[:, a:b], kp, vp, frames, frame_tokens=T,
+                                 softmax_scale=softmax_scale, out=out[:, a:b], frame_lens=lens)
+    if commit:
+        cache.commit_staged(layer, chunk_index, staging)
+    return out
