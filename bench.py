@@ -611,6 +611,95 @@ def commit_path(device, iters=20):
     }
 
 
+def segments_leg(device, iters=5):
+    """Segmented attention at the config-2 head shape (H12, 1560 tok/frame):
+    * teacher forcing over [clean | noisy] x 6 frames (2 chunks of 3, sink 1 chunk, 1 prior clean
+      chunk; causal_model.py:337-471): ours (one launch per query chunk over its frame list)
+      vs SDPA with the dense boolean mask (FlexAttention needs Triton, absent here);
+    * H3 rollout window (sgf_attention.py:236-258): a 5-frame chunk over a 1000-token prefix,
+      5 history chunks and itself: ours (chunk-list cache, ragged prefix) vs torch.cat + flash
+      SDPA.
+    FLOPs count visible keys only."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from solarwm_amd.segments import (ChunkListKVCache, teacher_forcing_attention,
+                                      teacher_forcing_frame_lists, windowed_attention)
+
+    T, H = 1560, 12
+    g = torch.Generator(device=device).manual_seed(9)
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.bfloat16)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    F, nb = 6, 3
+    kw = dict(num_frames=F, frame_seqlen=T, num_frame_per_block=nb, max_prior_clean_chunks=1,
+              sink_size=3)
+    L = 2 * F * T
+    q, k, v = rnd(1, L, H, 128), rnd(1, L, H, 128), rnd(1, L, H, 128)
+    lists = teacher_forcing_frame_lists(**{x: kw[x] for x in ("num_frames", "num_frame_per_block",
+                                                               "max_prior_clean_chunks", "sink_size")})
+    tf_flops = sum(4.0 * nb * T * len(fr) * T * H * 128 for _, fr in lists)
+    ours_tf = timed(lambda: teacher_forcing_attention(q, k, v, **kw))
+    # the dense mask of the same rule, built on the host from the frame lists
+    mask = torch.zeros(L, L, dtype=torch.bool)
+    for f0, frames in lists:
+        for fr in frames:
+            mask[f0 * T : (f0 + nb) * T, fr * T : (fr + 1) * T] = True
+    mask = mask.to(device)
+    qt, kt, vt = (x.transpose(1, 2).contiguous() for x in (q, k, v))
+    ref_tf = timed(lambda: torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask))
+    del mask, qt, kt, vt, q, k, v
+
+    cf, P = 5, 1000
+    cache = ChunkListKVCache(num_layers=1, batch=1, heads=H, frame_tokens=T, chunk_frames=cf,
+                             window=5, span_frames=1, device=device)
+    pk, pv = rnd(1, P, H, 128), rnd(1, P, H, 128)
+    for c in range(5):
+        windowed_attention(rnd(1, cf * T, H, 128), rnd(1, cf * T, H, 128), rnd(1, cf * T, H, 128),
+                           cache, 0, c, prefix=(pk, pv), commit=True)
+    q, k, v = rnd(1, cf * T, H, 128), rnd(1, cf * T, H, 128), rnd(1, cf * T, H, 128)
+    ours_w = timed(lambda: windowed_attention(q, k, v, cache, 0, 5, prefix=(pk, pv)))
+    hist = [(rnd(1, cf * T, H, 128), rnd(1, cf * T, H, 128)) for _ in range(5)]
+
+    def ref_window():
+        keys = torch.cat([pk, *(a for a, _ in hist), k], 1)
+        vals = torch.cat([pv, *(b for _, b in hist), v], 1)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            torch.nn.functional.scaled_dot_product_attention(
+                q.transpose(1, 2).contiguous(), keys.transpose(1, 2).contiguous(),
+                vals.transpose(1, 2).contiguous())
+
+    ref_w = timed(ref_window)
+    w_flops = 4.0 * cf * T * (P + 6 * cf * T) * H * 128
+    del cache, hist, q, k, v, pk, pv
+    torch.cuda.empty_cache()
+    return {
+        "teacher_forcing_ms": round(ours_tf, 3),
+        "teacher_forcing_tflops": round(tf_flops / (ours_tf / 1e3) / 1e12, 1),
+        "teacher_forcing_reference_ms": round(ref_tf, 3),
+        "teacher_forcing_speedup": round(ref_tf / ours_tf, 2),
+        "h3_window_ms": round(ours_w, 3),
+        "h3_window_tflops": round(w_flops / (ours_w / 1e3) / 1e12, 1),
+        "h3_window_reference_ms": round(ref_w, 3),
+        "h3_window_speedup": round(ref_w / ours_w, 2),
+        "workload": (f"teacher forcing [clean|noisy] 2x{F} frames x {T} tok, H{H}, chunks of {nb}, "
+                     f"sink 1 chunk, 1 prior chunk (reference: SDPA + dense bool mask); H3 window "
+                     f"{cf}-frame chunk over {P} prefix + 5 history chunks (reference: cat + flash SDPA)"),
+    }
+
+
 def c5_quality(device):
     """Config 5 cache memory and attention error: one steady-state layer pass with the fp8
     cache against the same pass with a bf16 cache (4 streams, 1% x20 outlier channels)."""
@@ -861,6 +950,8 @@ def main():
         log(f"[bench] aux c2_prope: {aux['c2_prope']}")
         aux["commit_path"] = commit_path(dev)
         log(f"[bench] aux commit_path: {aux['commit_path']}")
+        aux["segments"] = segments_leg(dev)
+        log(f"[bench] aux segments: {aux['segments']}")
         log("[bench] aux c5: fp8 vs bf16 quality")
         aux["c5"]["quality"] = c5_quality(dev)
         log(f"[bench] aux c5 quality: {aux['c5']['quality']}")

@@ -8,8 +8,7 @@ from solarwm_amd.segments import teacher_forcing_frame_lists
 
 
 def test_teacher_forcing_frame_lists_match_mask():
-    """The product's frame lists are the oracle's intervals in frames (CPU check run with the GPU
-    tests so both restatements are exercised on the same geometries)."""
+    """The product's frame lists are the oracle's key intervals, in frames."""
     for F, nb, sink, m in [(6, 2, 0, None), (6, 2, 2, 1), (9, 3, 3, 0), (8, 2, 4, 2)]:
         segs = sr.teacher_forcing_segments(num_frames=F, frame_seqlen=1, num_frame_per_block=nb,
                                            max_prior_clean_chunks=m, sink_size=sink)
