@@ -649,53 +649,89 @@ void attn_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp8-e4m3 pools (one dequantisation scale per (slot, stream, head) for K and for V).
-//
-// Same decomposition and 3-stage loop as attn_kernel, with v_mfma_f32_32x32x16_fp8_fp8 (8 fp8
-// per lane per operand) for both products:
+// fp8-e4m3 pools (one dequantisation scale per (slot, stream, head) for K and for V), on gfx950's
+// v_mfma_f32_32x32x64_f8f6f4: each operand lane (n, hh) holds row / column n and k values
+// 32 hh .. 32 hh + 31 (32 bytes).
 //   * Q is quantised in-kernel per query row (scale = absmax/448); the K frame scale and the Q
 //     row scale fold into the softmax FMA: x = acc * (log2e*scale*sq*sk) - m;
 //   * P is quantised as P * sv * G (sv = the tile's V frame scale, G = 110 / max_window(sv), so
 //     P <= 2^kStale8 = 4 maps below 448) and O is divided by G * sum(P) at the end;
-//   * K rows are read in the order key_perm8(), which puts key kb*32 + hh*16 + i in accumulator
-//     register i of lane half hh, so P^T's B operand for a 16-key step is 8 consecutive keys and
-//     the matching V^T operand is 8 consecutive bytes of a V^T row;
-//   * LDS keeps each tile as 1 KB "double blocks": lane L's 16 B hold its operands for two
-//     consecutive k-steps, written by one direct 16 B global->LDS load and read by one
-//     ds_read_b128 (K: d = hh*64 + step*8 .. +7 for both Q and K, which only has to agree
-//     between the two operands; V^T: keys kb*32 + hh*16 .. +15).
-constexpr int kBlock8 = 1024;          // one double block
-constexpr int kTile8 = 8 * kBlock8;    // one 64-key K (or V^T) tile in fp8
-typedef long fp8x8;                    // 8 e4m3 codes, the operand of the fp8 MFMA
+//   * per 64-key tile and wave: 4 QK MFMAs (2 key blocks kb x 2 channel halves cs; A = K rows,
+//     B = the lane's 32 quantised Q channels cs*64 + 32 hh ..) and 4 PV MFMAs (one per
+//     32-channel block db; A = V^T row 32 db + n, keys 32 hh .. +31; B = P^T, the lane's
+//     probabilities of keys 32 hh .. +31 in key order);
+//   * K rows are staged in the order key_perm64(kb, r), which puts key 32 hh + 16 kb + i of the
+//     tile in accumulator register i of lane half hh, so the scores of a lane are already in
+//     P^T's operand order;
+//   * LDS: one 2 KB operand block per (kb, cs) for K and per db for V^T (lane n*32 .. +32),
+//     written by direct buffer->LDS loads: DMA lane i of part p fills operand lane 32 p + i / 2,
+//     bytes 16 (i & 1) .. +16.
+constexpr int kOp8 = 2048;
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
-__device__ inline int key_perm8(int m) {
-  return ((m >> 2) & 1) * 16 + (m >> 3) * 4 + (m & 3);
+__device__ inline int key_perm64(int kb, int r) {
+  return 32 * ((r >> 2) & 1) + 16 * kb + 4 * (r >> 3) + (r & 3);
 }
 
-__device__ inline void mask_tile8(f32x16 (&s)[2], int hh, int tok0, int T, int key0, int lim) {
+__device__ inline int pack_fp8x4(float x0, float x1, float x2, float x3) {
+  const int v = __builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false);
+  return __builtin_amdgcn_cvt_pk_fp8_f32(x2, x3, v, true);
+}
+
+__device__ inline void mask_tile64(f32x16 (&s)[2], int hh, int tok0, int T, int key0, int lim) {
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int kk = kb * 32 + hh * 16 + i;
+      const int kk = 32 * hh + 16 * kb + i;
       if (tok0 + kk >= T || key0 + kk >= lim) s[kb][i] = -INFINITY;
     }
 }
 
-__device__ inline fp8x8 pack_fp8x8(const float* v) {
-  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
-  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], 0, false);
-  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
-  return (fp8x8)(((unsigned long)(unsigned)hi << 32) | (unsigned)lo);
+__device__ inline i32x8 lds_op32(const char* p) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16);
+  return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+               (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+__device__ inline f32x16 mfma64(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// direct buffer->LDS copy of this lane's N 16-byte pieces of one tile: goff = the piece's byte
+// offset inside the tile, loff = its byte offset inside the LDS buffer
+template <int N>
+struct Stage64 {
+  uint32_t goff[N];
+  int loff[N];
+  __device__ void operator()(const uint8_t* tile, char* buf) const {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the calling kernels' launch stubs
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)tile, (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(buf + loff[j]), 16, goff[j], 0, 0, 0);
+#endif
+  }
+};
+
+// scores of one 64-key tile: s[kb] = K rows (kb, both channel halves) . Q
+__device__ inline void qk64(const char* kl, const i32x8 (&q8)[2], const f32x16& zero16,
+                            f32x16 (&s)[2]) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    s[kb] = mfma64(lds_op32(kl + (kb * 2) * kOp8), q8[0], zero16);
+    s[kb] = mfma64(lds_op32(kl + (kb * 2 + 1) * kOp8), q8[1], s[kb]);
+  }
 }
 
 template <int NW, typename QT>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fp8_kernel(AttnArgs a) {
   constexpr int kBQ = NW * 32;
-  constexpr int kDpw = 8 / NW;  // double blocks per wave per tile
-  // LDS: K tiles [0, 16 KB) (two buffers), V^T tiles [16 KB, 32 KB) (two buffers).
+  constexpr int kDma = 16 / NW;     // 1 KB DMA parts per wave per tile (8 for K, 8 for V^T)
+  constexpr int kBuf = 4 * kOp8;    // one K (or V^T) tile
   extern __shared__ __attribute__((aligned(16))) char lds[];
   int logical;
   {
@@ -712,39 +748,43 @@ void attn_fp8_kernel(AttnArgs a) {
   const int qrow = q0 + w * 32 + n;
   const bool qlive = qrow < a.Lq;
 
-  // Q row quantisation: lane (n, hh) holds channels hh*64 .. hh*64+63 of its query.
-  fp8x8 q8[8];
-  float q_scale;  // dequantisation scale of this query row (absmax / 448)
+  // Q row quantisation: lane (n, hh) holds channels cs*64 + 32 hh .. +31 for cs = 0, 1.
+  i32x8 q8[2];
+  float q_scale;
   {
-    float qv[64];
+    float qv[64];  // qv[cs * 32 + j] = channel cs * 64 + 32 hh + j
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
-                   (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 64;
+                   (int64_t)(qlive ? qrow : 0) * a.q_st + hh * 32;
     const float qn = a.q_rms && qlive ? a.q_rms[(int64_t)b * a.q_rms_sb + qrow] : 0.f;
-    const float* qw = a.q_w + h * kHeadDim + hh * 64;
+    const float* qw = a.q_w + h * kHeadDim + hh * 32;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      Vec8<QT> v = qlive ? Vec8<QT>::load(qp + c * 8) : Vec8<QT>::zero();
-      if (a.q_rms) {  // normalised Q in bf16, as the reference's norm_q output
+    for (int cs = 0; cs < 2; ++cs)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qv[c * 8 + j] = (float)(bf16)((float)v.get(j) * qn * qw[c * 8 + j]);
-      } else {
+      for (int c = 0; c < 4; ++c) {
+        Vec8<QT> v = qlive ? Vec8<QT>::load(qp + cs * 64 + c * 8) : Vec8<QT>::zero();
+        if (a.q_rms) {  // normalised Q in bf16, as the reference's norm_q output
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qv[c * 8 + j] = (float)(bf16)v.get(j);  // bf16 rounding first
+          for (int j = 0; j < 8; ++j)
+            qv[cs * 32 + c * 8 + j] = (float)(bf16)((float)v.get(j) * qn * qw[cs * 64 + c * 8 + j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) qv[cs * 32 + c * 8 + j] = (float)(bf16)v.get(j);  // bf16 first
+        }
       }
-    }
     float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < 64; ++j) amax = fmaxf(amax, __builtin_fabsf(qv[j]));
     amax = pair_max(amax);
     const float inv = amax > 0.f ? 448.0f / amax : 0.f;
     q_scale = amax / 448.0f;
+    auto cl = [&](float x) { return fminf(fmaxf(x * inv, -448.f), 448.f); };
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float t[8];
+    for (int cs = 0; cs < 2; ++cs)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) t[j] = fminf(fmaxf(qv[c * 8 + j] * inv, -448.f), 448.f);
-      q8[c] = pack_fp8x8(t);
-    }
+      for (int d = 0; d < 8; ++d) {
+        const float* t = qv + cs * 32 + 4 * d;
+        q8[cs][d] = pack_fp8x4(cl(t[0]), cl(t[1]), cl(t[2]), cl(t[3]));
+      }
   }
 
   const int n_keys = (int)a.n_keys;
@@ -782,35 +822,35 @@ void attn_fp8_kernel(AttnArgs a) {
     tj = a.flen[j];
     return (tok0 + kTile > tj) || (key0 + kTile > lim_lo);
   };
-  // wave w stages K double blocks b = w*kDpw + j (kb = b>>2, steps 2(b&3), 2(b&3)+1) and V^T
-  // double blocks b (db = b>>1, kb = b&1)
-  const int b0 = w * kDpw;
-  const int64_t koff = (int64_t)((b0 >> 2) * 32 + key_perm8(n)) * kHeadDim + hh * 64 + (b0 & 3) * 16;
-  const int64_t voff = (int64_t)((b0 >> 1) * 32 + n) * a.Tp + (b0 & 1) * 32 + hh * 16;
-  auto kb_lds = [&](int i) { return lds + i * kTile8; };
-  auto vb_lds = [&](int i) { return lds + (2 + i) * kTile8; };
-  auto issue_k = [&](int tau, char* dst) {
+  // staging: wave wu moves parts c = wu * kDma + j; parts 0..7 are K (block c >> 1 = (kb, cs),
+  // half c & 1), parts 8..15 V^T (block db = (c - 8) >> 1, half c & 1); a wave is all K or all V
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const bool kload = wu * kDma < 8;
+  Stage64<kDma> stage;
 #pragma unroll
-    for (int j = 0; j < kDpw; ++j)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(ktile(tau) + koff + j * 16),
-                                       (lds_void_t*)(dst + (b0 + j) * kBlock8), 16, 0, 0);
-  };
-  auto issue_v = [&](int tau, char* dst) {
-#pragma unroll
-    for (int j = 0; j < kDpw; ++j)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(vtile(tau) + voff + j * 32),
-                                       (lds_void_t*)(dst + (b0 + j) * kBlock8), 16, 0, 0);
-  };
+  for (int j = 0; j < kDma; ++j) {
+    const int c = wu * kDma + j, p = c & 1;
+    if (c < 8) {
+      const int blk = c >> 1;
+      stage.goff[j] = (uint32_t)(key_perm64(blk >> 1, lane >> 1) * kHeadDim + (blk & 1) * 64 + 32 * p +
+                           16 * (lane & 1));
+      stage.loff[j] = blk * kOp8 + p * 1024;
+    } else {
+      const int db = (c - 8) >> 1;
+      stage.goff[j] = (uint32_t)((32 * db + (lane >> 1)) * a.Tp + 32 * p + 16 * (lane & 1));
+      stage.loff[j] = db * kOp8 + p * 1024;
+    }
+  }
+  auto kb_lds = [&](int i) { return lds + i * kBuf; };
+  auto vb_lds = [&](int i) { return lds + (2 + i) * kBuf; };
 
-  // G maps the largest probability (<= 2^kStale8) times the largest V scale of the window
-  // just below 448.
   constexpr float kStale8 = 2.0f;
   float sv_max = 0.f;
   for (int j = 0; j < a.n_frames; ++j)
     sv_max = fmaxf(sv_max, a.vscale[(int64_t)a.slots[j] * a.B * a.H + sc_bh]);
   const float G = sv_max > 0.f ? 110.0f / sv_max : 1.0f;
   const float c2q = a.scale_log2 * q_scale;
-  const int lane16 = lane * 16;
+  const int lane32 = lane * 32;
 
   f32x16 oacc[4];
 #pragma unroll
@@ -818,48 +858,31 @@ void attn_fp8_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
-
-  auto qk = [&](const char* kl, f32x16 (&s)[2]) {
+  f32x16 zero16;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const u32x4 d = *reinterpret_cast<const u32x4*>(kl + (kb * 4 + t) * kBlock8);
-        const fp8x8 lo = (fp8x8)(((unsigned long)d[1] << 32) | d[0]);
-        const fp8x8 hi = (fp8x8)(((unsigned long)d[3] << 32) | d[2]);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(lo, q8[2 * t], s[kb], 0, 0, 0);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(hi, q8[2 * t + 1], s[kb], 0, 0, 0);
-      }
-    }
-  };
+  for (int i = 0; i < 16; ++i) zero16[i] = 0.f;
 
   f32x16 s_cur[2];
-  fp8x8 pprev[2][2];
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) pprev[x][y] = 0;
+  i32x8 pprev = {0, 0, 0, 0, 0, 0, 0, 0};
   if (ntau > 0) {
-    issue_k(0, kb_lds(0));
-    if (ntau > 1) issue_k(1, kb_lds(1));
+    if (kload) stage(ktile(0), kb_lds(0));
+    if (ntau > 1) if (kload) stage(ktile(1), kb_lds(1));
 #pragma unroll
     for (int r = 0; r < 8 / NW; ++r)
       *reinterpret_cast<u32x4*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    qk(kb_lds(0) + lane16, s_cur);
+    qk64(kb_lds(0) + lane32, q8, zero16, s_cur);
     int tok0, key0, tj;
-    if (tile_needs_mask(0, tok0, key0, tj)) mask_tile8(s_cur, hh, tok0, tj, key0, lim_lane);
+    if (tile_needs_mask(0, tok0, key0, tj)) mask_tile64(s_cur, hh, tok0, tj, key0, lim_lane);
     __syncthreads();
   }
   for (int tau = 0; tau < ntau; ++tau) {
     const int cb = tau & 1;
-    if (tau + 2 < ntau) issue_k(tau + 2, kb_lds(cb));
-    issue_v(tau, vb_lds(cb));
-    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1)
-    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
+    if (tau + 2 < ntau) if (kload) stage(ktile(tau + 2), kb_lds(cb));
+    if (!kload) stage(vtile(tau), vb_lds(cb));
+    const char* kl = kb_lds(cb ^ 1) + lane32;  // K(tau+1)
+    const char* vl = vb_lds(cb ^ 1) + lane32;  // V(tau-1) (zeros on the first iteration)
     const int64_t slot = slot_of(tau);
     // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
     // masked (-inf) logits stay -inf instead of becoming NaN
@@ -867,7 +890,7 @@ void attn_fp8_kernel(AttnArgs a) {
     const float pv_scale = a.vscale[slot * a.B * a.H + sc_bh] * G;
 
     f32x16 s_nxt[2];
-    qk(kl, s_nxt);
+    qk64(kl, q8, zero16, s_nxt);
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -879,33 +902,24 @@ void attn_fp8_kernel(AttnArgs a) {
     m_run = raise ? mx : m_run;
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ls[4] = {0.f, 0.f, 0.f, 0.f};
-    fp8x8 pb[2][2];
+    i32x8 pb;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int d = 0; d < 8; ++d) {
+      const int kb = d >> 2, i0 = 4 * (d & 3);
+      float t[4];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        float t[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[kb][s2 * 8 + j], mult, -m_use));
-          ls[j & 3] += p;
-          t[j] = p * pv_scale;
-        }
-        pb[kb][s2] = pack_fp8x8(t);
+      for (int j = 0; j < 4; ++j) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[kb][i0 + j], mult, -m_use));
+        ls[j] += p;
+        t[j] = p * pv_scale;
       }
+      pb[d] = pack_fp8x4(t[0], t[1], t[2], t[3]);
+    }
     l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
-    asm volatile("" ::"v"(pb[0][0]), "v"(pb[0][1]), "v"(pb[1][0]), "v"(pb[1][1]), "v"(l_run));
+    asm volatile("" ::"v"(pb), "v"(l_run));
     // PV(tau-1)
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 d = *reinterpret_cast<const u32x4*>(vl + (db * 2 + kb) * kBlock8);
-        const fp8x8 lo = (fp8x8)(((unsigned long)d[1] << 32) | d[0]);
-        const fp8x8 hi = (fp8x8)(((unsigned long)d[3] << 32) | d[2]);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(lo, pprev[kb][0], oacc[db], 0, 0, 0);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(hi, pprev[kb][1], oacc[db], 0, 0, 0);
-      }
+    for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
     if (__any(alpha != 1.0f)) {
 #pragma unroll
       for (int db = 0; db < 4; ++db)
@@ -914,29 +928,18 @@ void attn_fp8_kernel(AttnArgs a) {
     }
     if (tau + 1 < ntau) {
       int tok0, key0, tj;
-      if (tile_needs_mask(tau + 1, tok0, key0, tj)) mask_tile8(s_nxt, hh, tok0, tj, key0, lim_lane);
+      if (tile_needs_mask(tau + 1, tok0, key0, tj)) mask_tile64(s_nxt, hh, tok0, tj, key0, lim_lane);
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int y = 0; y < 2; ++y) pprev[x][y] = pb[x][y];
+    pprev = pb;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
   if (ntau > 0) {
-    const char* vl = vb_lds((ntau - 1) & 1) + lane16;
+    const char* vl = vb_lds((ntau - 1) & 1) + lane32;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 d = *reinterpret_cast<const u32x4*>(vl + (db * 2 + kb) * kBlock8);
-        const fp8x8 lo = (fp8x8)(((unsigned long)d[1] << 32) | d[0]);
-        const fp8x8 hi = (fp8x8)(((unsigned long)d[3] << 32) | d[2]);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(lo, pprev[kb][0], oacc[db], 0, 0, 0);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(hi, pprev[kb][1], oacc[db], 0, 0, 0);
-      }
+    for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
   }
   const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / (l_tot * G) : 0.f;
@@ -976,9 +979,9 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
   dim3 grid(a.n_wg), block(NW * 64);
   if (pool_dtype == SKV_FP8_E4M3) {
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 4 * kTile8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 16 * kOp8, s, a);
     else
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 4 * kTile8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 16 * kOp8, s, a);
     return;
   }
   const size_t lds_bytes = 2 * kTileBytes;
