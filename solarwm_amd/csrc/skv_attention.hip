@@ -32,6 +32,7 @@
 //   * tiles never straddle frames (frames are padded to 64 tokens); padding keys and keys
 //     beyond a query's chunk-causal limit get -inf, decided per tile: full tiles skip the
 //     mask, tiles past every query's limit are not visited.
+#include <mutex>
 #include <math.h>
 
 #include "skv_common.h"
@@ -76,6 +77,16 @@ struct AttnArgs {
   // valid keys of each listed frame (T unless the caller gives ragged frames, e.g. a prefix span
   // stored in partly filled slots); keys t >= flen[j] of frame j are masked
   uint16_t flen[SKV_MAX_FRAMES];
+  // Balanced key split (no mask, 8-wave groups): the n_wg workgroups share the
+  // units = B*H*n_qtiles*nt (q-tile, key tile) pairs equally, nt = n_frames*ntiles_f; workgroup i
+  // takes units [i*units/n_wg, (i+1)*units/n_wg) in q-tile order.  A q-tile that one workgroup
+  // covers whole is written directly; a part of a split q-tile goes to record 2i (the
+  // workgroup's first segment) or 2i+1 (its last) of part_o / part_ml, and attn_combine_kernel
+  // merges the records of each split q-tile.
+  int split;
+  int64_t units;
+  float* part_o;   // [2*n_wg][256][128] unnormalised O
+  float* part_ml;  // [2*n_wg][256][2] (running max in log2 units, row sum)
 };
 
 // Wan's split of a head's 64 complex channel pairs (2i, 2i+1): 22 temporal, 21 height, 21 width
@@ -234,7 +245,7 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
     }
 }
 
-template <int NW, typename QT, typename KT, int RM>
+template <int NW, typename QT, typename KT, int RM, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   constexpr int kBQ = NW * 32;
@@ -251,11 +262,38 @@ void attn_kernel(AttnArgs a) {
     const int per = a.n_wg >> 3, rem = a.n_wg & 7;
     logical = xcd * per + min(xcd, rem) + idx;
   }
-  const int qt = logical % a.n_qtiles;
-  const int bh = logical / a.n_qtiles;
+  // Segments: key tiles [tb, te) of q-tile qg; one whole q-tile unless split.  A split share
+  // [u0, u1) covers q-tiles q_first .. q_first + nseg - 1 (segment j = q-tile q_first + j); the
+  // whole ones run first, then the last segment (key tiles from 0, in step with the other
+  // workgroups, which all start at key tile 0), then the first (the tail of a q-tile, a fixed
+  // number of tiles ahead of them): K/V tiles stay shared through L2 as in the unsplit grid.
+  const int nt = a.n_frames * a.ntiles_f;
+  int q_first = logical, nseg = 1;
+  int64_t u0 = 0, u1 = 0;
+  if constexpr (SPLIT) {
+    u0 = (int64_t)logical * a.units / a.n_wg;
+    u1 = (int64_t)(logical + 1) * a.units / a.n_wg;
+    q_first = (int)(u0 / nt);
+    nseg = u1 > u0 ? (int)((u1 - 1) / nt) - q_first + 1 : 0;
+  }
+  for (int k = 0; k < nseg; ++k) {
+  const int seg = nseg == 1 ? 0 : k < nseg - 2 ? k + 1 : k == nseg - 2 ? nseg - 1 : 0;
+  const int qg = q_first + seg;
+  int tb = 0, te = nt;
+  if constexpr (SPLIT) {
+    if (seg == 0) tb = (int)(u0 - (int64_t)q_first * nt);
+    if (seg == nseg - 1) te = (int)(u1 - (int64_t)qg * nt);
+  }
+  if (k > 0) __syncthreads();  // the previous segment's last LDS reads are done
+  const int qt = qg % a.n_qtiles;
+  const int bh = qg / a.n_qtiles;
   const int h = bh % a.H, b = bh / a.H;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // SPLIT: an opaque copy per segment, so lane-derived values are recomputed here instead of
+  // hoisted out of the segment loop, where they would stay live through the tile loop
+  int tid = threadIdx.x;
+  if constexpr (SPLIT) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, w = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
   const int q0 = qt * kBQ;
   const int qrow = q0 + w * 32 + n;
@@ -408,6 +446,7 @@ void attn_kernel(AttnArgs a) {
     const int jf = lim_hi / a.T;
     ntau = jf >= a.n_frames ? a.n_frames * a.ntiles_f
                             : jf * a.ntiles_f + (lim_hi - jf * a.T + kTile - 1) / kTile;
+    if constexpr (SPLIT) ntau = te - tb;  // no mask: the segment's tiles
   }
 
   const KT* kpool = static_cast<const KT*>(a.kpool);
@@ -416,16 +455,16 @@ void attn_kernel(AttnArgs a) {
   TileLoader<NW, KT> loader;
   loader.init(w, lane, a.Tp);
   auto tile_base = [&](int tau) -> int64_t {
-    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
     return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
   };
   auto vtile_base = [&](int tau) -> int64_t {
-    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
     return (int64_t)a.slots[j] * a.slot_stride + kbh + t * kTile;
   };
   // mask decision for tile tau (uniform): returns true if any key of the tile may be hidden
   auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
-    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
     tok0 = t * kTile;
     key0 = j * a.T + tok0;
     tj = a.flen[j];
@@ -463,15 +502,15 @@ void attn_kernel(AttnArgs a) {
     loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
     if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
     if constexpr (RM == 2) {
-      issue_w(0);
-      if (ntau > 1 && a.ntiles_f == 1) issue_w(1);
+      issue_w(tb / a.ntiles_f);
+      if (ntau > 1 && (tb + 1) % a.ntiles_f == 0) issue_w((tb + 1) / a.ntiles_f);
     }
 #pragma unroll
     for (int r = 0; r < 16 / NW; ++r)
       *reinterpret_cast<bf16x8*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = Vec8<bf16>::zero().to_bf16();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if constexpr (RM > 0) rot_q(0);
+    if constexpr (RM > 0) rot_q(tb / a.ntiles_f);
     qk_tile(kb_lds(0) + lane16, qf, s_cur);
     int tok0, key0, tj;
     if (tile_needs_mask(0, tok0, key0, tj)) mask_tile(s_cur, hh, tok0, tj, key0, lim_lane);
@@ -492,18 +531,18 @@ void attn_kernel(AttnArgs a) {
     loader.issue_v(vpool + vtile_base(tau), vb_lds(cb), w);
     if constexpr (RM == 2) {
       // W for the frame tile tau+2 opens (rot_q reads it at the start of step tau+1)
-      if (tau + 2 < ntau && (tau + 2) % a.ntiles_f == 0) issue_w((tau + 2) / a.ntiles_f);
+      if (tau + 2 < ntau && (tb + tau + 2) % a.ntiles_f == 0) issue_w((tb + tau + 2) / a.ntiles_f);
     }
     const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
     const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
     if constexpr (RM > 0) {
       // QK(tau+1) below opens a new key frame: turn Q's temporal pairs for it
       const int t1 = tau + 1;
-      if (t1 < ntau && t1 % a.ntiles_f == 0) rot_q(t1 / a.ntiles_f);
+      if (t1 < ntau && (tb + t1) % a.ntiles_f == 0) rot_q((tb + t1) / a.ntiles_f);
     }
 
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    float ls[4] = {0.f, 0.f, 0.f, 0.f};
+    float ls[4];
     float pf[32];
     // operand of MFMA step i: even i -> QK step i/2 (k = i/4, kb = (i/2)&1), odd i -> PV step
     // i/2 (db = (i/2)/4, kb = ((i/2)>>1)&1, s2 = (i/2)&1)
@@ -550,16 +589,24 @@ void attn_kernel(AttnArgs a) {
         const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
         asm volatile("" ::"v"(p));  // keep this slice's exp next to its MFMA
         pf[e] = p;
-        ls[e & 3] += p;
-        asm volatile("" ::"v"(ls[e & 3]));
-        if (e & 1) {
-          pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
-          pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
+        // the sum and the bf16 pack take the previous slice's probability, whose exp has
+        // finished, so no VALU op waits on the transcendental unit
+        if (e > 0) {
+          const int d = e - 1;
+          ls[d & 3] = d < 4 ? pf[d] : ls[d & 3] + pf[d];
+          asm volatile("" ::"v"(ls[d & 3]));
+          if (d & 1) {
+            pb[d >> 4][(d >> 3) & 1][(d & 7) - 1] = (bf16)pf[d - 1];
+            pb[d >> 4][(d >> 3) & 1][d & 7] = (bf16)pf[d];
+          }
+          if ((d & 7) == 7) asm volatile("" ::"v"(pb[d >> 4][(d >> 3) & 1]));
         }
-        if ((e & 7) == 7) asm volatile("" ::"v"(pb[e >> 4][(e >> 3) & 1]));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    ls[3] += pf[31];
+    pb[1][1][6] = (bf16)pf[30];
+    pb[1][1][7] = (bf16)pf[31];
     float lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
     const bool need = !(lp <= kMaxPart) || m_run == -INFINITY;
     if (__any(need)) {
@@ -622,6 +669,21 @@ void attn_kernel(AttnArgs a) {
   }
 
   const float l_tot = pair_sum(l_run);
+  if (SPLIT && (tb > 0 || te < nt)) {
+    // part of a split q-tile: unnormalised O, the running max and the row sum
+    if (qlive) {
+      const int64_t row = (2 * (int64_t)logical + (seg > 0 ? 1 : 0)) * kBQ + w * 32 + n;
+      float* po = a.part_o + row * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(po + db * 32 + g * 8 + hh * 4) =
+              f32x4{oacc[db][g * 4], oacc[db][g * 4 + 1], oacc[db][g * 4 + 2], oacc[db][g * 4 + 3]};
+      if (hh == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run, l_tot);
+    }
+    continue;
+  }
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if (qlive) {
     QT* op = static_cast<QT*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
@@ -646,6 +708,7 @@ void attn_kernel(AttnArgs a) {
         store4<QT>(op + d0, x0, x1, x2, x3);
       }
   }
+  }  // segments
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -957,6 +1020,77 @@ void attn_fp8_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Merge of the split q-tiles (AttnArgs.split): workgroup qg of the grid owns q-tile qg.  It finds
+// the split workgroups whose unit ranges cover the q-tile's units [qg*nt, (qg+1)*nt) and
+// combines their records per query row: M = max m_p, O = sum 2^(m_p - M) O_p / sum 2^(m_p - M)
+// l_p (a record with m_p = -inf has O_p = 0, l_p = 0).  A q-tile inside one workgroup's range was
+// written by attn_kernel itself.  Workgroup (qg, g) merges rows 8g .. 8g+7 of q-tile qg, half a
+// wave per row and 4 channels (one PRoPE group) per lane, so the grid has enough waves in flight
+// to cover the load latency.
+constexpr int kSplitBQ = 256;     // queries per q-tile of the split (8-wave) kernel
+constexpr int kMaxSplitWg = 1024;  // split grids have at most this many workgroups
+
+template <typename QT>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  __shared__ int64_t recs[kMaxSplitWg];
+  __shared__ int n_rec;
+  const int nt = a.n_frames * a.ntiles_f;
+  const int qg = blockIdx.x / (kSplitBQ / 8), rg = blockIdx.x % (kSplitBQ / 8);
+  const int64_t x0 = (int64_t)qg * nt, x1 = x0 + nt - 1;
+  auto lo = [&](int i) { return (int64_t)i * a.units / a.n_wg; };
+  auto owner = [&](int64_t x) {  // the workgroup whose range holds unit x
+    int i = (int)(x * a.n_wg / a.units);
+    while (i + 1 < a.n_wg && lo(i + 1) <= x) ++i;
+    while (i > 0 && lo(i) > x) --i;
+    return i;
+  };
+  const int i0 = owner(x0), i1 = owner(x1);
+  if (i0 == i1) return;  // uniform: one workgroup covered the q-tile and wrote it
+  if (threadIdx.x == 0) {  // the records of this q-tile, once
+    int m = 0;
+    for (int i = i0; i <= i1; ++i)
+      if (lo(i) < lo(i + 1)) recs[m++] = 2 * (int64_t)i + (i == i0 && lo(i) < x0 ? 1 : 0);
+    n_rec = m;
+  }
+  __syncthreads();
+  const int nr = n_rec;
+  const int qt = qg % a.n_qtiles, bh = qg / a.n_qtiles;
+  const int h = bh % a.H, b = bh / a.H;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = (lane & 31) * 4;
+  {
+    const int r = rg * 8 + 2 * w + (lane >> 5);
+    const int qrow = qt * kSplitBQ + r;
+    if (qrow >= a.Lq) return;
+    float M = -INFINITY;
+    for (int p = 0; p < nr; ++p) M = fmaxf(M, a.part_ml[(recs[p] * kSplitBQ + r) * 2]);
+    float L = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    for (int p = 0; p < nr; ++p) {
+      const int64_t row = recs[p] * kSplitBQ + r;
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+      if (ml.x == -INFINITY) continue;
+      const float wgt = __builtin_amdgcn_exp2f(ml.x - M);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + row * kHeadDim + c);
+      L = fmaf(wgt, ml.y, L);
+      o0 = fmaf(wgt, v[0], o0), o1 = fmaf(wgt, v[1], o1);
+      o2 = fmaf(wgt, v[2], o2), o3 = fmaf(wgt, v[3], o3);
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    float x0v = o0 * inv, x1v = o1 * inv, x2v = o2 * inv, x3v = o3 * inv;
+    if (a.pq_o) {  // PRoPE: P_q of the query's frame on every group of the output
+      const float* po = a.pq_o + ((int64_t)b * a.n_qframes + qrow / a.T) * 16;
+      const float y0 = fmaf(po[0], x0v, fmaf(po[1], x1v, fmaf(po[2], x2v, po[3] * x3v)));
+      const float y1 = fmaf(po[4], x0v, fmaf(po[5], x1v, fmaf(po[6], x2v, po[7] * x3v)));
+      const float y2 = fmaf(po[8], x0v, fmaf(po[9], x1v, fmaf(po[10], x2v, po[11] * x3v)));
+      const float y3 = fmaf(po[12], x0v, fmaf(po[13], x1v, fmaf(po[14], x2v, po[15] * x3v)));
+      x0v = y0, x1v = y1, x2v = y2, x3v = y3;
+    }
+    QT* op = static_cast<QT*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qrow * a.o_st;
+    store4<QT>(op + c, x0v, x1v, x2v, x3v);
+  }
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -974,6 +1108,28 @@ static int cu_count() {
   return n;
 }
 
+// Workspace of the split path, stream-ordered from the device's default memory pool.  The pool
+// keeps freed memory for reuse (release threshold raised once per device), so repeated calls
+// do not map and unmap pages.
+static bool split_workspace(void** p, size_t bytes, hipStream_t s) {
+  static std::mutex mu;
+  static bool tuned[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    if (dev >= 0 && dev < 64 && !tuned[dev]) {
+      hipMemPool_t pool;
+      if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+        uint64_t keep = UINT64_MAX;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+      }
+      tuned[dev] = true;
+    }
+  }
+  return hipMallocAsync(p, bytes, s) == hipSuccess;
+}
+
 template <int NW>
 static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipStream_t s) {
   dim3 grid(a.n_wg), block(NW * 64);
@@ -985,6 +1141,26 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     return;
   }
   const size_t lds_bytes = 2 * kTileBytes;
+  if constexpr (NW == 8) {
+    if (a.split) {  // bf16 or fp32 pools, no mask (checked by the caller)
+      const size_t lds = lds_bytes + (rm == 2 ? 2 * kWBuf : 0);
+      const bool qb = q_dtype == SKV_BF16;
+      if (rm == 2) {
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 2, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 2, true>), grid, block, lds, s, a);
+      } else if (rm == 1) {
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 1, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1, true>), grid, block, lds, s, a);
+      } else if (pool_dtype == SKV_BF16) {
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, true>), grid, block, lds, s, a);
+      } else {
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, float, 0, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, float, 0, true>), grid, block, lds, s, a);
+      }
+      return;
+    }
+  }
   if (rm == 2) {  // bf16 pools, frame_tokens >= 64 (checked by the caller)
     const size_t lds_w = lds_bytes + 2 * kWBuf;
     if (q_dtype == SKV_BF16)
@@ -1151,9 +1327,39 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     const int64_t slots = (int64_t)n_cu * per_cu;
     return (double)wg / (double)(((wg + slots - 1) / slots) * slots);
   };
-  const int nw = fill(256, 1) * 1.04 >= fill(128, 2) ? 8 : 4;
+  int nw = fill(256, 1) * 1.04 >= fill(128, 2) ? 8 : 4;
   a.n_qtiles = (q_len + nw * 32 - 1) / (nw * 32);
   a.n_wg = a.n_qtiles * heads * batch;
+  // Balanced key split: when the grid leaves many CUs idle (few q-tiles, e.g. one frame of
+  // queries), one 8-wave workgroup per CU takes an equal share of all (q-tile, key tile) units;
+  // split q-tiles are merged by attn_combine_kernel.  A tile costs more the more CUs are busy
+  // (measured on MI355X with 525 tiles per workgroup: 128, 224 and 256 busy CUs take 0.81, 0.92
+  // and 1.0 of the full-chip time), modelled as t(busy) ~ 1 + 0.62 * busy / n_cu; the split
+  // runs all CUs, plus about three tiles of segment set-up and merge.  Near-full grids (e.g.
+  // 228 q-tiles on 256 CUs) gain too little to pay for the merge and stay unsplit.
+  a.split = 0;
+  a.units = 0;
+  a.part_o = a.part_ml = nullptr;
+  const int nt = n_frames * a.ntiles_f;
+  const int64_t qt8 = (int64_t)((q_len + kSplitBQ - 1) / kSplitBQ) * heads * batch;
+  const int64_t units8 = qt8 * nt;
+  if (mask_mode == SKV_MASK_NONE && pool_dtype != SKV_FP8_E4M3 && nt >= 8 && units8 >= 4 * n_cu &&
+      n_cu <= kMaxSplitWg) {
+    auto t_tile = [&](int64_t busy) { return 1.0 + 0.62 * (double)busy / n_cu; };
+    auto t_grid = [&](int64_t wg, int per_cu, double per_tile) {  // rounds of nt tiles
+      const int64_t slots = (int64_t)n_cu * per_cu, full = wg / slots, last = wg - full * slots;
+      return per_tile * nt * (full * t_tile(n_cu) + (last ? t_tile((last + per_cu - 1) / per_cu) : 0.0));
+    };
+    const double t_plain = nw == 8 ? t_grid(a.n_wg, 1, 1.0) : t_grid(a.n_wg, 2, 1.04);
+    const double t_split = ((double)units8 / n_cu + 3.0) * t_tile(n_cu);
+    if (t_split < 0.85 * t_plain) {
+      nw = 8;
+      a.split = 1;
+      a.n_qtiles = (int)(qt8 / ((int64_t)heads * batch));
+      a.n_wg = n_cu;
+      a.units = units8;
+    }
+  }
   a.slot_stride = (int64_t)batch * heads * a.Tp * kHeadDim;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.mask_mode = mask_mode;
@@ -1185,10 +1391,29 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rm = prope ? 2 : rope ? 1 : 0;
+  void* ws = nullptr;
+  if (a.split) {
+    // stream-ordered workspace: 2 records per workgroup (O, then max and sum)
+    const size_t rec_rows = (size_t)2 * a.n_wg * kSplitBQ;
+    if (!split_workspace(&ws, rec_rows * (kHeadDim + 2) * sizeof(float), s)) {
+      set_error("skv_attention: workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
+      return SKV_E_LAUNCH;
+    }
+    a.part_o = static_cast<float*>(ws);
+    a.part_ml = a.part_o + rec_rows * kHeadDim;
+  }
   if (nw == 8)
     launch<8>(a, q_dtype, pool_dtype, rm, s);
   else
     launch<4>(a, q_dtype, pool_dtype, rm, s);
+  if (a.split) {
+    const int n_q = a.n_qtiles * heads * batch;
+    if (q_dtype == SKV_BF16)
+      hipLaunchKernelGGL((attn_combine_kernel<bf16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((attn_combine_kernel<float>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, a);
+    (void)hipFreeAsync(ws, s);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("skv_attention: launch failed: %s", hipGetErrorString(e));

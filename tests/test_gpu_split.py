@@ -1,0 +1,89 @@
+"""GPU parity of the balanced key split of the bf16 attention kernel (one workgroup per CU over
+equal shares of the (q-tile, key tile) units, split q-tiles merged by a second kernel) against
+the float64 oracle (oracle/wan_cache_ref.py attention, attention.py:141-188 of the reference).
+
+The launcher takes the split when the unsplit grid would leave most CUs idle: every case below
+has few q-tiles over a long key window, so it does.  Cases: a q-tile shared by many
+workgroups (each gets about four key tiles), float queries with a ragged last q-tile, frames
+with short valid spans so some workgroups see only masked keys, and the C2 window with a query
+count that leaves most of the last q-tile empty.  Bars: tests/helpers.py."""
+
+import pytest
+import torch
+
+from oracle import segments_ref as sr
+from oracle import wan_cache_ref as ref
+from solarwm_amd import kernels
+
+from .helpers import assert_attn_close
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _rand(shape, seed, dtype=BF):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(dtype)
+
+
+def _pools(k, v, T, gpu, seed=0):
+    B, L, H, _ = k.shape
+    n = L // T
+    g = torch.Generator().manual_seed(seed)
+    slots = torch.randperm(n + 2, generator=g)[:n].tolist()
+    kp, vp, _, _ = kernels.new_pools(n + 2, B, H, T, BF, gpu)
+    for f in range(n):
+        kernels.append_frames(k.to(gpu), v.to(gpu), kp, vp, [slots[f]], frame_tokens=T, src_frame0=f)
+    return kp, vp, slots
+
+
+@pytest.mark.parametrize("B,H,Lq,T,n,dtype", [
+    (1, 2, 256, 1560, 21, BF),              # 2 q-tiles x 525 key tiles over 256 workgroups
+    (2, 3, 300, 390, 14, torch.float32),    # float Q/O, last q-tile 44 of 256 rows
+    (1, 4, 1000, 1560, 8, BF),              # C2 frame size, 4 q-tiles per head
+])
+def test_split_vs_oracle(gpu, B, H, Lq, T, n, dtype):
+    _say("split attention", B, H, Lq, T, n, dtype)
+    q = _rand((B, Lq, H, 128), 1, dtype)
+    k, v = _rand((B, n * T, H, 128), 2), _rand((B, n * T, H, 128), 3)
+    kp, vp, slots = _pools(k, v, T, gpu)
+    out = kernels.attention_frames(q.to(gpu), kp, vp, slots, frame_tokens=T)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype
+    assert_attn_close(out, ref.attention(q, k.to(dtype), v.to(dtype)))
+
+
+def test_split_ragged_frames_with_fully_masked_shares(gpu):
+    """Frames keep 5..70 of 1560 keys: most key tiles are wholly masked, so many workgroups'
+    shares hold no visible key (max -inf, sum 0) and the merge must skip them."""
+    T, n, H = 1560, 21, 2
+    lens = [5, 70, 1560, 64, 65, 1] + [7] * (n - 6)
+    k, v = _rand((1, n * T, H, 128), 4), _rand((1, n * T, H, 128), 5)
+    q = _rand((1, 256, H, 128), 6)
+    kp, vp, slots = _pools(k, v, T, gpu, seed=1)
+    out = kernels.attention_frames(q.to(gpu), kp, vp, slots, frame_tokens=T, frame_lens=lens)
+    keys = torch.cat([k[:, j * T : j * T + lens[j]] for j in range(n)], 1)
+    vals = torch.cat([v[:, j * T : j * T + lens[j]] for j in range(n)], 1)
+    torch.cuda.synchronize()
+    assert_attn_close(out, sr.attention(q, keys, vals))
+
+
+def test_split_is_deterministic_and_strided_output(gpu):
+    """Same inputs twice give identical bits; an output view with padded strides is written
+    only inside the view."""
+    T, n, H, Lq = 1560, 6, 4, 700
+    q = _rand((1, Lq, H, 128), 7).to(gpu)
+    k = _rand((1, n * T, H, 128), 8)
+    kp, vp, slots = _pools(k, k * 0.5, T, gpu)
+    a = kernels.attention_frames(q, kp, vp, slots, frame_tokens=T)
+    b = kernels.attention_frames(q, kp, vp, slots, frame_tokens=T)
+    big = torch.full((1, Lq, H, 160), 7.0, device=gpu, dtype=BF)
+    c = kernels.attention_frames(q, kp, vp, slots, frame_tokens=T, out=big[..., :128])
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(a, c)
+    assert bool((big[..., 128:] == 7.0).all())
