@@ -736,6 +736,9 @@ __device__ inline int key_perm64(int kb, int r) {
   return 32 * ((r >> 2) & 1) + 16 * kb + 4 * (r >> 3) + (r & 3);
 }
 
+// QK step t of a tile -> K operand block c = 2 kb + cs: (0,0), (1,0), (0,1), (1,1)
+__device__ inline int korder64(int t) { return ((t & 1) << 1) | (t >> 1); }
+
 __device__ inline int pack_fp8x4(float x0, float x1, float x2, float x3) {
   const int v = __builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false);
   return __builtin_amdgcn_cvt_pk_fp8_f32(x2, x3, v, true);
@@ -950,39 +953,68 @@ void attn_fp8_kernel(AttnArgs a) {
     // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
     // masked (-inf) logits stay -inf instead of becoming NaN
     const float mult = fmaxf(c2q * a.kscale[slot * a.B * a.H + sc_bh], 1e-30f);
-    const float pv_scale = a.vscale[slot * a.B * a.H + sc_bh] * G;
+    // P is stored as p * sv * G: the factor rides in the exponent's bias (one log per tile
+    // instead of 32 multiplies) and the row sum divides it out once.  An all-zero V frame
+    // (sv = 0) keeps P unscaled: its V codes are all 0, so only the sum sees P.
+    const float pv_raw = a.vscale[slot * a.B * a.H + sc_bh] * G;
+    const float pv = pv_raw > 0.f ? pv_raw : 1.0f;
 
+    // Eight MFMA slots, QK(tau+1) and PV(tau-1) alternating (QK steps in the order (kb, cs) =
+    // (0,0), (1,0), (0,1), (1,1), so the two halves of one key block are four slots apart), each
+    // followed by a quarter of softmax(tau): the 4 probabilities of P^T dword i.  The operands
+    // come from LDS three slots ahead; the sum and the fp8 pack of a quarter run one slot later,
+    // when its exps have finished.
     f32x16 s_nxt[2];
-    qk64(kl, q8, zero16, s_nxt);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[kb][i]);
-    mx = pair_max(mx) * mult;
-    const bool raise = mx > m_run + kStale8;
-    const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
-    m_run = raise ? mx : m_run;
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    float ls[4] = {0.f, 0.f, 0.f, 0.f};
+    i32x8 op[4];
+    float pf[32], ls[4];
+    float alpha = 1.0f, bias = 0.f;
     i32x8 pb;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const int kb = d >> 2, i0 = 4 * (d & 3);
-      float t[4];
+    for (int i = 0; i < 3; ++i)
+      op[i] = (i & 1) ? lds_op32(vl + (i >> 1) * kOp8) : lds_op32(kl + korder64(i >> 1) * kOp8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i + 3 < 8) {
+        const int j = i + 3;
+        op[j & 3] = (j & 1) ? lds_op32(vl + (j >> 1) * kOp8) : lds_op32(kl + korder64(j >> 1) * kOp8);
+      }
+      if ((i & 1) == 0) {
+        const int c = korder64(i >> 1), kb = c >> 1, cs = c & 1;
+        s_nxt[kb] = mfma64(op[i & 3], q8[cs], cs == 0 ? zero16 : s_nxt[kb]);
+      } else {
+        oacc[i >> 1] = mfma64(op[i & 3], pprev, oacc[i >> 1]);
+      }
+      if (i == 0) {  // the tile's max, the running max and the exponent bias
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[kb][r]);
+        mx = pair_max(mx) * mult;
+        const bool raise = mx > m_run + kStale8;
+        alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
+        m_run = raise ? mx : m_run;
+        bias = __builtin_amdgcn_logf(pv) - (m_run == -INFINITY ? 0.f : m_run);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[kb][i0 + j], mult, -m_use));
-        ls[j] += p;
-        t[j] = p * pv_scale;
+        const int e = 4 * i + j;
+        pf[e] = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], mult, bias));
+        asm volatile("" ::"v"(pf[e]));  // keep this quarter's exps next to its MFMA
       }
-      pb[d] = pack_fp8x4(t[0], t[1], t[2], t[3]);
-    }
-    l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
-    asm volatile("" ::"v"(pb), "v"(l_run));
-    // PV(tau-1)
+      if (i > 0) {
+        const int d = i - 1;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
+        for (int j = 0; j < 4; ++j) ls[j] = d == 0 ? pf[4 * d + j] : ls[j] + pf[4 * d + j];
+        pb[d] = pack_fp8x4(pf[4 * d], pf[4 * d + 1], pf[4 * d + 2], pf[4 * d + 3]);
+        asm volatile("" ::"v"(pb[d]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ls[j] += pf[28 + j];
+    pb[7] = pack_fp8x4(pf[28], pf[29], pf[30], pf[31]);
+    l_run = fmaf(l_run, alpha, ((ls[0] + ls[1]) + (ls[2] + ls[3])) * __builtin_amdgcn_rcpf(pv));
     if (__any(alpha != 1.0f)) {
 #pragma unroll
       for (int db = 0; db < 4; ++db)
