@@ -611,6 +611,59 @@ def commit_path(device, iters=20):
     }
 
 
+def single_frame_leg(device, iters=20):
+    """One frame of queries per block (num_frame_per_block = 1: Lq = 1560) over the config-2
+    window (21 frames x 1560 keys, H12).  The unsplit grid would be 7 q-tiles x 12 heads = 84
+    workgroups on 256 CUs, so the launcher splits the key range over every CU (one workgroup per
+    CU, partials merged by a second kernel).  Reference: flash SDPA on the already-materialised
+    window (its cat/clone copies are not counted)."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from solarwm_amd import kernels
+
+    T, H, n, Lq = 1560, 12, 21, 1560
+    g = torch.Generator(device=device).manual_seed(11)
+    q = torch.randn(1, Lq, H, 128, generator=g, device=device, dtype=torch.bfloat16)
+    k = torch.randn(1, n * T, H, 128, generator=g, device=device, dtype=torch.bfloat16)
+    v = torch.randn(1, n * T, H, 128, generator=g, device=device, dtype=torch.bfloat16)
+    kp, vp, _, _ = kernels.new_pools(n, 1, H, T, torch.bfloat16, device)
+    kernels.append_frames(k, v, kp, vp, list(range(n)), frame_tokens=T)
+    slots = list(range(n))
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    ours = timed(lambda: kernels.attention_frames(q, kp, vp, slots, frame_tokens=T))
+    qt, kt, vt = (x.transpose(1, 2).contiguous() for x in (q, k, v))
+
+    def ref():
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            torch.nn.functional.scaled_dot_product_attention(qt, kt, vt)
+
+    ref_ms = timed(ref)
+    flops = 4.0 * Lq * n * T * H * 128
+    del q, k, v, kp, vp, qt, kt, vt
+    torch.cuda.empty_cache()
+    return {
+        "attn_ms": round(ours, 4),
+        "attn_tflops": round(flops / (ours / 1e3) / 1e12, 1),
+        "reference_ms": round(ref_ms, 4),
+        "reference_tflops": round(flops / (ref_ms / 1e3) / 1e12, 1),
+        "speedup": round(ref_ms / ours, 2),
+        "workload": f"one frame of queries (Lq {Lq}) over {n} x {T} cached keys, H{H}, bf16; "
+                    "key range split over all CUs (84 q-tile workgroups unsplit)",
+    }
+
+
 def segments_leg(device, iters=5):
     """Segmented attention at the config-2 head shape (H12, 1560 tok/frame):
     * teacher forcing over [clean | noisy] x 6 frames (2 chunks of 3, sink 1 chunk, 1 prior clean
@@ -952,6 +1005,8 @@ def main():
         log(f"[bench] aux commit_path: {aux['commit_path']}")
         aux["segments"] = segments_leg(dev)
         log(f"[bench] aux segments: {aux['segments']}")
+        aux["single_frame"] = single_frame_leg(dev)
+        log(f"[bench] aux single_frame: {aux['single_frame']}")
         log("[bench] aux c5: fp8 vs bf16 quality")
         aux["c5"]["quality"] = c5_quality(dev)
         log(f"[bench] aux c5 quality: {aux['c5']['quality']}")

@@ -87,3 +87,37 @@ def test_split_is_deterministic_and_strided_output(gpu):
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(a, c)
     assert bool((big[..., 128:] == 7.0).all())
+
+
+def test_split_float32_pools(gpu):
+    """The split path on fp32 pools (the config-1 cache dtype): 2 q-tiles x 4 heads over 21
+    frames of 390 tokens."""
+    B, H, Lq, T, n = 1, 4, 512, 390, 21
+    q = _rand((B, Lq, H, 128), 30, torch.float32)
+    k, v = _rand((B, n * T, H, 128), 31, torch.float32), _rand((B, n * T, H, 128), 32, torch.float32)
+    g = torch.Generator().manual_seed(3)
+    slots = torch.randperm(n + 2, generator=g)[:n].tolist()
+    kp, vp, _, _ = kernels.new_pools(n + 2, B, H, T, torch.float32, gpu)
+    for f in range(n):
+        kernels.append_frames(k.to(gpu), v.to(gpu), kp, vp, [slots[f]], frame_tokens=T, src_frame0=f)
+    out = kernels.attention_frames(q.to(gpu), kp, vp, slots, frame_tokens=T)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    assert_attn_close(out, ref.attention(q, k, v))
+
+
+def test_split_with_q_norm(gpu):
+    """Q RMSNorm at load on the split path: equal to the oracle's attention of the normalised
+    queries (WanRMSNorm's statistic, model.py:69-84)."""
+    B, H, Lq, T, n, eps = 1, 2, 300, 1560, 21, 1e-6
+    g = torch.Generator().manual_seed(40)
+    q = (torch.randn(B, Lq, H, 128, generator=g) *
+         torch.exp(torch.randn(B, Lq, 1, 1, generator=g) * 1.2)).to(BF)
+    w = torch.rand(H * 128, generator=g) + 0.5
+    k, v = _rand((B, n * T, H, 128), 41), _rand((B, n * T, H, 128), 42)
+    kp, vp, slots = _pools(k, v, T, gpu, seed=2)
+    qd = q.to(gpu)
+    got = kernels.attention_frames(qd, kp, vp, slots, frame_tokens=T,
+                                   q_norm=(kernels.rms_rows(qd, eps), w.to(gpu)))
+    torch.cuda.synchronize()
+    assert_attn_close(got, ref.attention(ref.norm_heads(q, w, eps), k, v))
