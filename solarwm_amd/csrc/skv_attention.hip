@@ -75,8 +75,9 @@ struct AttnArgs {
   const float* q_w;
   int32_t slots[SKV_MAX_FRAMES];
   // valid keys of each listed frame (T unless the caller gives ragged frames, e.g. a prefix span
-  // stored in partly filled slots); keys t >= flen[j] of frame j are masked
-  uint16_t flen[SKV_MAX_FRAMES];
+  // stored in partly filled slots); keys t >= flen[j] of frame j are masked.  32-bit so a
+  // wave-uniform index reads it with a scalar load.
+  int32_t flen[SKV_MAX_FRAMES];
   // Balanced key split (no mask, 8-wave groups): the n_wg workgroups share the
   // units = B*H*n_qtiles*nt (q-tile, key tile) pairs equally, nt = n_frames*ntiles_f; workgroup i
   // takes units [i*units/n_wg, (i+1)*units/n_wg) in q-tile order.  A q-tile that one workgroup
@@ -140,6 +141,35 @@ __device__ inline float pair_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+
+// Walks key tiles in frame-list order.  The frame's pool offset and valid length are read when
+// the walk enters the frame, so advancing by one tile costs a few scalar adds: no division by
+// the tiles per frame and no table load on the tiles in between.  Every member is wave-uniform.
+struct TileWalk {
+  int j = 0, t = 0;   // frame index in the list, tile inside the frame
+  int32_t slot = 0;   // slots[j]
+  int64_t base = 0;   // element offset of frame j's (b, h) block: slot * slot_stride + kbh
+  int flen = 0;       // valid keys of frame j
+  __device__ void open(const AttnArgs& a, int64_t kbh) {
+    if (j < a.n_frames) {
+      slot = a.slots[j];
+      base = (int64_t)slot * a.slot_stride + kbh;
+      flen = a.flen[j];
+    }
+  }
+  __device__ void start(const AttnArgs& a, int64_t kbh, int tg) {
+    j = tg / a.ntiles_f;
+    t = tg - j * a.ntiles_f;
+    open(a, kbh);
+  }
+  __device__ void next(const AttnArgs& a, int64_t kbh) {
+    if (++t == a.ntiles_f) {
+      t = 0;
+      ++j;
+      open(a, kbh);
+    }
+  }
+};
 
 __device__ inline int64_t chunk_limit(int64_t pos, int64_t chunk, int64_t n_keys) {
   const int64_t lim = (pos / chunk + 1) * chunk;
@@ -458,10 +488,6 @@ void attn_kernel(AttnArgs a) {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
     return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
   };
-  auto vtile_base = [&](int tau) -> int64_t {
-    const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
-    return (int64_t)a.slots[j] * a.slot_stride + kbh + t * kTile;
-  };
   // mask decision for tile tau (uniform): returns true if any key of the tile may be hidden
   auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
@@ -469,6 +495,12 @@ void attn_kernel(AttnArgs a) {
     key0 = j * a.T + tok0;
     tj = a.flen[j];
     return (tok0 + kTile > tj) || (key0 + kTile > lim_lo);
+  };
+  // the same decision for the tile a walk stands on
+  auto walk_needs_mask = [&](const TileWalk& wk, int& tok0, int& key0) -> bool {
+    tok0 = wk.t * kTile;
+    key0 = wk.j * a.T + tok0;
+    return (tok0 + kTile > wk.flen) || (key0 + kTile > lim_lo);
   };
 
   f32x16 oacc[4];
@@ -525,20 +557,25 @@ void attn_kernel(AttnArgs a) {
   f32x16 zero16;
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero16[i] = 0.f;
+  // Tiles addressed in step tau: K(tau+2) (kw), V(tau) (vw) and the mask / RoPE frame of
+  // QK(tau+1) (mw); the walks advance one tile per step.
+  TileWalk kw, vw, mw;
+  kw.start(a, kbh, tb + 2);
+  vw.start(a, kbh, tb);
+  mw.start(a, kbh, tb + 1);
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
                   bf16x8 (&pprev)[2][2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
-    if (tau + 2 < ntau) loader.issue_k(kpool + tile_base(tau + 2), kb_lds(cb), w);
-    loader.issue_v(vpool + vtile_base(tau), vb_lds(cb), w);
+    if (tau + 2 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb), w);
+    loader.issue_v(vpool + vw.base + vw.t * kTile, vb_lds(cb), w);
     if constexpr (RM == 2) {
       // W for the frame tile tau+2 opens (rot_q reads it at the start of step tau+1)
-      if (tau + 2 < ntau && (tb + tau + 2) % a.ntiles_f == 0) issue_w((tb + tau + 2) / a.ntiles_f);
+      if (tau + 2 < ntau && kw.t == 0) issue_w(kw.j);
     }
     const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
     const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
     if constexpr (RM > 0) {
       // QK(tau+1) below opens a new key frame: turn Q's temporal pairs for it
-      const int t1 = tau + 1;
-      if (t1 < ntau && (tb + t1) % a.ntiles_f == 0) rot_q((tb + t1) / a.ntiles_f);
+      if (tau + 1 < ntau && mw.t == 0) rot_q(mw.j);
     }
 
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
@@ -634,9 +671,12 @@ void attn_kernel(AttnArgs a) {
     }
     l_run += lp;
     if (tau + 1 < ntau) {
-      int tok0, key0, tj;
-      if (tile_needs_mask(tau + 1, tok0, key0, tj)) mask_tile(s_nxt, hh, tok0, tj, key0, lim_lane);
+      int tok0, key0;
+      if (walk_needs_mask(mw, tok0, key0)) mask_tile(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
     }
+    kw.next(a, kbh);
+    vw.next(a, kbh);
+    mw.next(a, kbh);
     // K(tau+2) and V(tau) have landed; every wave is done with K(tau+1)'s and V(tau-1)'s
     // buffers (they take K(tau+3) and V(tau+1) next)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -872,14 +912,9 @@ void attn_fp8_kernel(AttnArgs a) {
   const uint8_t* vpool = static_cast<const uint8_t*>(a.vpool);
   const int64_t kbh = (int64_t)(b * a.H + h) * a.Tp * kHeadDim;
   const int64_t sc_bh = (int64_t)b * a.H + h;
-  auto slot_of = [&](int tau) { return (int64_t)a.slots[tau / a.ntiles_f]; };
   auto ktile = [&](int tau) {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
     return kpool + (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
-  };
-  auto vtile = [&](int tau) {
-    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
-    return vpool + (int64_t)a.slots[j] * a.slot_stride + kbh + t * kTile;
   };
   auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
     const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
@@ -943,21 +978,30 @@ void attn_fp8_kernel(AttnArgs a) {
     if (tile_needs_mask(0, tok0, key0, tj)) mask_tile64(s_cur, hh, tok0, tj, key0, lim_lane);
     __syncthreads();
   }
+  // Tiles addressed in step tau: K(tau+2) (kw), V(tau) and its frame's scales (vw), the mask of
+  // QK(tau+1) (mw); the walks advance one tile per step.
+  TileWalk kw, vw, mw;
+  kw.start(a, kbh, 2);
+  vw.start(a, kbh, 0);
+  mw.start(a, kbh, 1);
+  float mult = 0.f, pv = 1.0f;
   for (int tau = 0; tau < ntau; ++tau) {
     const int cb = tau & 1;
-    if (tau + 2 < ntau) if (kload) stage(ktile(tau + 2), kb_lds(cb));
-    if (!kload) stage(vtile(tau), vb_lds(cb));
+    if (tau + 2 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb));
+    if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(cb));
     const char* kl = kb_lds(cb ^ 1) + lane32;  // K(tau+1)
     const char* vl = vb_lds(cb ^ 1) + lane32;  // V(tau-1) (zeros on the first iteration)
-    const int64_t slot = slot_of(tau);
-    // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
-    // masked (-inf) logits stay -inf instead of becoming NaN
-    const float mult = fmaxf(c2q * a.kscale[slot * a.B * a.H + sc_bh], 1e-30f);
-    // P is stored as p * sv * G: the factor rides in the exponent's bias (one log per tile
-    // instead of 32 multiplies) and the row sum divides it out once.  An all-zero V frame
-    // (sv = 0) keeps P unscaled: its V codes are all 0, so only the sum sees P.
-    const float pv_raw = a.vscale[slot * a.B * a.H + sc_bh] * G;
-    const float pv = pv_raw > 0.f ? pv_raw : 1.0f;
+    if (tau == 0 || vw.t == 0) {  // a new key frame: its K and V scales
+      const int64_t sc = (int64_t)vw.slot * a.B * a.H + sc_bh;
+      // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
+      // masked (-inf) logits stay -inf instead of becoming NaN
+      mult = fmaxf(c2q * a.kscale[sc], 1e-30f);
+      // P is stored as p * sv * G: the factor rides in the exponent's bias (one log per tile
+      // instead of 32 multiplies) and the row sum divides it out once.  An all-zero V frame
+      // (sv = 0) keeps P unscaled: its V codes are all 0, so only the sum sees P.
+      const float pv_raw = a.vscale[sc] * G;
+      pv = pv_raw > 0.f ? pv_raw : 1.0f;
+    }
 
     // Eight MFMA slots, QK(tau+1) and PV(tau-1) alternating (QK steps in the order (kb, cs) =
     // (0,0), (1,0), (0,1), (1,1), so the two halves of one key block are four slots apart), each
@@ -1022,9 +1066,13 @@ void attn_fp8_kernel(AttnArgs a) {
         for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
     }
     if (tau + 1 < ntau) {
-      int tok0, key0, tj;
-      if (tile_needs_mask(tau + 1, tok0, key0, tj)) mask_tile64(s_nxt, hh, tok0, tj, key0, lim_lane);
+      const int tok0 = mw.t * kTile, key0 = mw.j * a.T + tok0;
+      if ((tok0 + kTile > mw.flen) || (key0 + kTile > lim_lo))
+        mask_tile64(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
     }
+    kw.next(a, kbh);
+    vw.next(a, kbh);
+    mw.next(a, kbh);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
     pprev = pb;
@@ -1414,7 +1462,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
       set_error("skv_attention_ex: frame_lens[%d]=%d outside [1, %d]", j, len, frame_tokens);
       return SKV_E_ARG;
     }
-    a.flen[j] = (uint16_t)len;
+    a.flen[j] = (int32_t)len;
     ragged |= len != frame_tokens;
   }
   if (ragged && mask_mode == SKV_MASK_CHUNK_CAUSAL) {
