@@ -26,8 +26,9 @@
 //     the bf16x8 B operand (P^T) of the PV product; V is stored transposed in the pool so
 //     its A operand (V^T rows) is one 16 B LDS read;
 //   * iteration tau runs three independent streams — QK(tau+1), softmax(tau), PV(tau-1) —
-//     interleaved by hand (one MFMA, then one probability) so the matrix core and the VALU
-//     work at the same time; the loop is unrolled twice so score and probability registers
+//     interleaved by hand (one MFMA, then a slice of the softmax) so the matrix core and the
+//     VALU work at the same time; the softmax is front-loaded so its row sum is ready when the
+//     last MFMA issues; the loop is unrolled twice so score and probability registers
 //     alternate between two sets instead of being copied;
 //   * tiles never straddle frames (frames are padded to 64 tokens); padding keys and keys
 //     beyond a query's chunk-causal limit get -inf, decided per tile: full tiles skip the
@@ -129,6 +130,13 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 __device__ inline int key_perm(int m) {
   const int a = m >> 3, h = (m >> 2) & 1, c = m & 3;
   return (a >> 1) * 16 + h * 8 + (a & 1) * 4 + c;
+}
+
+// PV step st (0..15) of a tile: O block db += V^T(db, kb, s2) P^T(kb, s2), the four O blocks in
+// turn so consecutive PV MFMAs never accumulate into the same block (each block still sums its
+// four products in the order (kb, s2) = (0,0), (0,1), (1,0), (1,1))
+__device__ inline void pv_order(int st, int& db, int& kbb, int& s2) {
+  db = st & 3, kbb = (st >> 3) & 1, s2 = (st >> 2) & 1;
 }
 
 // Combine a lane's value with lane l^32's (the other key half of the same query) using the
@@ -565,14 +573,30 @@ void attn_kernel(AttnArgs a) {
   mw.start(a, kbh, tb + 1);
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
                   bf16x8 (&pprev)[2][2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
+    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
+    // operand of MFMA slot i: even i -> QK step i/2 (k = i/4, kb = (i/2)&1), odd i -> PV step i/2
+    auto operand = [&](int i) -> bf16x8 {
+      const int st = i >> 1;
+      if ((i & 1) == 0) {
+        const int k = st >> 1, kbb = st & 1;
+        return *reinterpret_cast<const bf16x8*>(kl + (kbb * 8 + k) * kBlockBytes);
+      }
+      int db, kbb, s2;
+      pv_order(st, db, kbb, s2);
+      return *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
+    };
+    // the first three operands are requested before this step's loads are issued, so their LDS
+    // latency overlaps the load set-up
+    bf16x8 opq[4];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) opq[i] = operand(i);
     if (tau + 2 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb), w);
     loader.issue_v(vpool + vw.base + vw.t * kTile, vb_lds(cb), w);
     if constexpr (RM == 2) {
       // W for the frame tile tau+2 opens (rot_q reads it at the start of step tau+1)
       if (tau + 2 < ntau && kw.t == 0) issue_w(kw.j);
     }
-    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
-    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
     if constexpr (RM > 0) {
       // QK(tau+1) below opens a new key frame: turn Q's temporal pairs for it
       if (tau + 1 < ntau && mw.t == 0) rot_q(mw.j);
@@ -581,17 +605,6 @@ void attn_kernel(AttnArgs a) {
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ls[4];
     float pf[32];
-    // operand of MFMA step i: even i -> QK step i/2 (k = i/4, kb = (i/2)&1), odd i -> PV step
-    // i/2 (db = (i/2)/4, kb = ((i/2)>>1)&1, s2 = (i/2)&1)
-    auto operand = [&](int i) -> bf16x8 {
-      const int st = i >> 1;
-      if ((i & 1) == 0) {
-        const int k = st >> 1, kbb = st & 1;
-        return *reinterpret_cast<const bf16x8*>(kl + (kbb * 8 + k) * kBlockBytes);
-      }
-      const int db = st >> 2, kbb = (st >> 1) & 1, s2 = st & 1;
-      return *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
-    };
     auto prob = [&](int e, float mu) {
       const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -mu));
       pf[e] = p;
@@ -601,9 +614,8 @@ void attn_kernel(AttnArgs a) {
         pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
       }
     };
-    bf16x8 opq[4];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) opq[i] = operand(i);
+    float lp, lp01, lp23;
+    bool need;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       if (i + 3 < 32) opq[(i + 3) & 3] = operand(i + 3);
@@ -617,19 +629,16 @@ void attn_kernel(AttnArgs a) {
         const int k = st >> 1, kbb = st & 1;
         s_nxt[kbb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], qf[k], k == 0 ? zero16 : s_nxt[kbb], 0, 0, 0);
       } else {
-        const int db = st >> 2, kbb = (st >> 1) & 1, s2 = st & 1;
+        int db, kbb, s2;
+        pv_order(st, db, kbb, s2);
         oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], pprev[kbb][s2], oacc[db], 0, 0, 0);
       }
-      // softmax slice i of tile tau: probability i, assuming the tile needs no new max
+      // softmax of tile tau, front-loaded: slot i < 4 takes probabilities 2i and 2i+1, slot
+      // 4 <= i < 28 probability i + 4; each is summed and packed one slot after its exp (so no
+      // VALU op waits on the transcendental unit), and slots 29 and 30 form the row sum, so the
+      // rare-path test after the last MFMA has its operands ready
       {
-        const int e = i;
-        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
-        asm volatile("" ::"v"(p));  // keep this slice's exp next to its MFMA
-        pf[e] = p;
-        // the sum and the bf16 pack take the previous slice's probability, whose exp has
-        // finished, so no VALU op waits on the transcendental unit
-        if (e > 0) {
-          const int d = e - 1;
+        auto retire = [&](int d) {
           ls[d & 3] = d < 4 ? pf[d] : ls[d & 3] + pf[d];
           asm volatile("" ::"v"(ls[d & 3]));
           if (d & 1) {
@@ -637,15 +646,35 @@ void attn_kernel(AttnArgs a) {
             pb[d >> 4][(d >> 3) & 1][d & 7] = (bf16)pf[d];
           }
           if ((d & 7) == 7) asm volatile("" ::"v"(pb[d >> 4][(d >> 3) & 1]));
+        };
+        auto expo = [&](int e) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
+          asm volatile("" ::"v"(p));  // keep this exp next to its MFMA
+          pf[e] = p;
+        };
+        if (i >= 1 && i <= 4) {
+          retire(2 * (i - 1));
+          retire(2 * (i - 1) + 1);
+        } else if (i >= 5 && i <= 28) {
+          retire(i + 3);
+        }
+        if (i < 4) {
+          expo(2 * i);
+          expo(2 * i + 1);
+        } else if (i < 28) {
+          expo(i + 4);
+        }
+        if (i == 29) {
+          lp01 = ls[0] + ls[1];
+          lp23 = ls[2] + ls[3];
+        }
+        if (i == 30) {
+          lp = lp01 + lp23;
+          need = !(lp <= kMaxPart) || m_run == -INFINITY;
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    ls[3] += pf[31];
-    pb[1][1][6] = (bf16)pf[30];
-    pb[1][1][7] = (bf16)pf[31];
-    float lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
-    const bool need = !(lp <= kMaxPart) || m_run == -INFINITY;
     if (__any(need)) {
       // rare path: both key halves of a query take the same decision; raise the max of each
       // such query to the tile's true max, recompute its probabilities, rescale O and l
