@@ -587,10 +587,13 @@ void attn_kernel(AttnArgs a) {
       return *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
     };
     // the first three operands are requested before this step's loads are issued, so their LDS
-    // latency overlaps the load set-up
+    // latency overlaps the load set-up (PRoPE: after the query transform below, which needs the
+    // registers)
     bf16x8 opq[4];
+    if constexpr (RM != 2) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) opq[i] = operand(i);
+      for (int i = 0; i < 3; ++i) opq[i] = operand(i);
+    }
     if (tau + 2 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb), w);
     loader.issue_v(vpool + vw.base + vw.t * kTile, vb_lds(cb), w);
     if constexpr (RM == 2) {
@@ -600,6 +603,10 @@ void attn_kernel(AttnArgs a) {
     if constexpr (RM > 0) {
       // QK(tau+1) below opens a new key frame: turn Q's temporal pairs for it
       if (tau + 1 < ntau && mw.t == 0) rot_q(mw.j);
+    }
+    if constexpr (RM == 2) {
+#pragma unroll
+      for (int i = 0; i < 3; ++i) opq[i] = operand(i);
     }
 
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
@@ -614,6 +621,7 @@ void attn_kernel(AttnArgs a) {
         pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
       }
     };
+    constexpr bool kFront = RM != 2;  // softmax schedule, below
     float lp, lp01, lp23;
     bool need;
 #pragma unroll
@@ -636,7 +644,8 @@ void attn_kernel(AttnArgs a) {
       // softmax of tile tau, front-loaded: slot i < 4 takes probabilities 2i and 2i+1, slot
       // 4 <= i < 28 probability i + 4; each is summed and packed one slot after its exp (so no
       // VALU op waits on the transcendental unit), and slots 29 and 30 form the row sum, so the
-      // rare-path test after the last MFMA has its operands ready
+      // rare-path test after the last MFMA has its operands ready.  PRoPE keeps one probability
+      // per slot (its frame-boundary query transform leaves no registers for the extra exps).
       {
         auto retire = [&](int d) {
           ls[d & 3] = d < 4 ? pf[d] : ls[d & 3] + pf[d];
@@ -652,28 +661,40 @@ void attn_kernel(AttnArgs a) {
           asm volatile("" ::"v"(p));  // keep this exp next to its MFMA
           pf[e] = p;
         };
-        if (i >= 1 && i <= 4) {
-          retire(2 * (i - 1));
-          retire(2 * (i - 1) + 1);
-        } else if (i >= 5 && i <= 28) {
-          retire(i + 3);
-        }
-        if (i < 4) {
-          expo(2 * i);
-          expo(2 * i + 1);
-        } else if (i < 28) {
-          expo(i + 4);
-        }
-        if (i == 29) {
-          lp01 = ls[0] + ls[1];
-          lp23 = ls[2] + ls[3];
-        }
-        if (i == 30) {
-          lp = lp01 + lp23;
-          need = !(lp <= kMaxPart) || m_run == -INFINITY;
+        if constexpr (kFront) {
+          if (i >= 1 && i <= 4) {
+            retire(2 * (i - 1));
+            retire(2 * (i - 1) + 1);
+          } else if (i >= 5 && i <= 28) {
+            retire(i + 3);
+          }
+          if (i < 4) {
+            expo(2 * i);
+            expo(2 * i + 1);
+          } else if (i < 28) {
+            expo(i + 4);
+          }
+          if (i == 29) {
+            lp01 = ls[0] + ls[1];
+            lp23 = ls[2] + ls[3];
+          }
+          if (i == 30) {
+            lp = lp01 + lp23;
+            need = !(lp <= kMaxPart) || m_run == -INFINITY;
+          }
+        } else {
+          if (i > 0) retire(i - 1);
+          expo(i);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (!kFront) {
+      ls[3] += pf[31];
+      pb[1][1][6] = (bf16)pf[30];
+      pb[1][1][7] = (bf16)pf[31];
+      lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+      need = !(lp <= kMaxPart) || m_run == -INFINITY;
     }
     if (__any(need)) {
       // rare path: both key halves of a query take the same decision; raise the max of each
