@@ -1039,7 +1039,7 @@ void attn_fp8_kernel(AttnArgs a) {
   kw.start(a, kbh, 2);
   vw.start(a, kbh, 0);
   mw.start(a, kbh, 1);
-  float mult = 0.f, pv = 1.0f;
+  float mult = 0.f, log_pv = 0.f, inv_pv = 1.0f;  // per key frame (see below)
   for (int tau = 0; tau < ntau; ++tau) {
     const int cb = tau & 1;
     if (tau + 2 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb));
@@ -1051,11 +1051,13 @@ void attn_fp8_kernel(AttnArgs a) {
       // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
       // masked (-inf) logits stay -inf instead of becoming NaN
       mult = fmaxf(c2q * a.kscale[sc], 1e-30f);
-      // P is stored as p * sv * G: the factor rides in the exponent's bias (one log per tile
-      // instead of 32 multiplies) and the row sum divides it out once.  An all-zero V frame
+      // P is stored as p * sv * G: the factor rides in the exponent's bias (one log per key
+      // frame instead of 32 multiplies per tile) and the row sum divides it out once.  An all-zero V frame
       // (sv = 0) keeps P unscaled: its V codes are all 0, so only the sum sees P.
       const float pv_raw = a.vscale[sc] * G;
-      pv = pv_raw > 0.f ? pv_raw : 1.0f;
+      const float pv = pv_raw > 0.f ? pv_raw : 1.0f;
+      log_pv = __builtin_amdgcn_logf(pv);
+      inv_pv = __builtin_amdgcn_rcpf(pv);
     }
 
     // Eight MFMA slots, QK(tau+1) and PV(tau-1) alternating (QK steps in the order (kb, cs) =
@@ -1093,7 +1095,7 @@ void attn_fp8_kernel(AttnArgs a) {
         const bool raise = mx > m_run + kStale8;
         alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
         m_run = raise ? mx : m_run;
-        bias = __builtin_amdgcn_logf(pv) - (m_run == -INFINITY ? 0.f : m_run);
+        bias = log_pv - (m_run == -INFINITY ? 0.f : m_run);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -1113,7 +1115,7 @@ void attn_fp8_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) ls[j] += pf[28 + j];
     pb[7] = pack_fp8x4(pf[28], pf[29], pf[30], pf[31]);
-    l_run = fmaf(l_run, alpha, ((ls[0] + ls[1]) + (ls[2] + ls[3])) * __builtin_amdgcn_rcpf(pv));
+    l_run = fmaf(l_run, alpha, ((ls[0] + ls[1]) + (ls[2] + ls[3])) * inv_pv);
     if (__any(alpha != 1.0f)) {
 #pragma unroll
       for (int db = 0; db < 4; ++db)
