@@ -1026,8 +1026,10 @@ void attn_fp8_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero16[i] = 0.f;
 
-  f32x16 s_cur[2];
-  i32x8 pprev = {0, 0, 0, 0, 0, 0, 0, 0};
+  // score and probability registers ping-pong between two sets (A, B) across iterations (the
+  // loop is unrolled twice), so no loop-carried copy is needed
+  f32x16 sA[2], sB[2];
+  i32x8 pA = {0, 0, 0, 0, 0, 0, 0, 0}, pB;
   if (ntau > 0) {
     if (kload) stage(ktile(0), kb_lds(0));
     if (ntau > 1) if (kload) stage(ktile(1), kb_lds(1));
@@ -1036,9 +1038,9 @@ void attn_fp8_kernel(AttnArgs a) {
       *reinterpret_cast<u32x4*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    qk64(kb_lds(0) + lane32, q8, zero16, s_cur);
+    qk64(kb_lds(0) + lane32, q8, zero16, sA);
     int tok0, key0, tj;
-    if (tile_needs_mask(0, tok0, key0, tj)) mask_tile64(s_cur, hh, tok0, tj, key0, lim_lane);
+    if (tile_needs_mask(0, tok0, key0, tj)) mask_tile64(sA, hh, tok0, tj, key0, lim_lane);
     __syncthreads();
   }
   // Tiles addressed in step tau: K(tau+2) (kw), V(tau) and its frame's scales (vw), the mask of
@@ -1048,8 +1050,9 @@ void attn_fp8_kernel(AttnArgs a) {
   vw.start(a, kbh, 0);
   mw.start(a, kbh, 1);
   float mult = 0.f, log_pv = 0.f, inv_pv = 1.0f;  // per key frame (see below)
-  for (int tau = 0; tau < ntau; ++tau) {
-    const int cb = tau & 1;
+  // cb = tau & 1, passed as a literal so buffer addresses fold into immediate offsets
+  auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], const i32x8& pprev,
+                  i32x8& pb) __attribute__((always_inline)) {
     if (tau + 2 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb));
     if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(cb));
     const char* kl = kb_lds(cb ^ 1) + lane32;  // K(tau+1)
@@ -1073,11 +1076,9 @@ void attn_fp8_kernel(AttnArgs a) {
     // followed by a quarter of softmax(tau): the 4 probabilities of P^T dword i.  The operands
     // come from LDS three slots ahead; the sum and the fp8 pack of a quarter run one slot later,
     // when its exps have finished.
-    f32x16 s_nxt[2];
     i32x8 op[4];
     float pf[32], ls[4];
     float alpha = 1.0f, bias = 0.f;
-    i32x8 pb;
 #pragma unroll
     for (int i = 0; i < 3; ++i)
       op[i] = (i & 1) ? lds_op32(vl + (i >> 1) * kOp8) : lds_op32(kl + korder64(i >> 1) * kOp8);
@@ -1138,16 +1139,25 @@ void attn_fp8_kernel(AttnArgs a) {
     kw.next(a, kbh);
     vw.next(a, kbh);
     mw.next(a, kbh);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
-    pprev = pb;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+  int tau = 0;
+  for (; tau + 1 < ntau; tau += 2) {
+    step(tau, 0, sA, sB, pA, pB);
+    step(tau + 1, 1, sB, sA, pB, pA);
   }
-  if (ntau > 0) {
+  // PV(ntau-1)
+  auto epilogue = [&](const i32x8& pprev) __attribute__((always_inline)) {
     const char* vl = vb_lds((ntau - 1) & 1) + lane32;
 #pragma unroll
     for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
+  };
+  if (tau < ntau) {
+    step(tau, 0, sA, sB, pA, pB);
+    epilogue(pB);
+  } else if (ntau > 0) {
+    epilogue(pA);
   }
   const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / (l_tot * G) : 0.f;
