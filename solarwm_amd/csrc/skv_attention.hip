@@ -336,9 +336,6 @@ void attn_kernel(AttnArgs a) {
   const int q0 = qt * kBQ;
   const int qrow = q0 + w * 32 + n;
   const bool qlive = qrow < a.Lq;
-  // a wave whose 32 queries all lie past Lq (in the last q-tile) only stages its share of each
-  // tile and meets the barriers
-  const bool wave_dead = q0 + __builtin_amdgcn_readfirstlane(w) * 32 >= a.Lq;
 
   // Q^T operand: lane (n, hh) holds q[qrow][k*16 + hh*8 .. +7] for k = 0..7.
   bf16x8 qf[8];
@@ -605,7 +602,7 @@ void attn_kernel(AttnArgs a) {
       if (tau + 2 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb), w);
       loader.issue_v(vpool + vw.base + vw.t * kTile, vb_lds(cb), w);
     };
-    if (kLoadSlot < 0 || wave_dead) issue_loads();
+    if (kLoadSlot < 0) issue_loads();
     if constexpr (RM == 2) {
       // W for the frame tile tau+2 opens (rot_q reads it at the start of step tau+1)
       if (tau + 2 < ntau && kw.t == 0) issue_w(kw.j);
@@ -619,124 +616,122 @@ void attn_kernel(AttnArgs a) {
       for (int i = 0; i < 3; ++i) opq[i] = operand(i);
     }
 
-    if (!wave_dead) {
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      float ls[4];
-      float pf[32];
-      auto prob = [&](int e, float mu) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -mu));
-        pf[e] = p;
-        ls[e & 3] += p;
-        if (e & 1) {
-          pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
-          pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
-        }
-      };
-      constexpr bool kFront = RM != 2;  // softmax schedule, below
-      float lp, lp01, lp23;
-      bool need;
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float ls[4];
+    float pf[32];
+    auto prob = [&](int e, float mu) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -mu));
+      pf[e] = p;
+      ls[e & 3] += p;
+      if (e & 1) {
+        pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
+        pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
+      }
+    };
+    constexpr bool kFront = RM != 2;  // softmax schedule, below
+    float lp, lp01, lp23;
+    bool need;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        if (i + 3 < 32) opq[(i + 3) & 3] = operand(i + 3);
-        if (i == kLoadSlot) issue_loads();
-        // wave priority falls over the tile (2, 1, 0 by thirds): the wave that is ahead yields
-        // issue slots to the one behind, so both reach the tile's barrier closer together
-        if (i == 0) __builtin_amdgcn_s_setprio(2);
-        if (i == 11) __builtin_amdgcn_s_setprio(1);
-        if (i == 22) __builtin_amdgcn_s_setprio(0);
-        const int st = i >> 1;
-        if ((i & 1) == 0) {
-          const int k = st >> 1, kbb = st & 1;
-          s_nxt[kbb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], qf[k], k == 0 ? zero16 : s_nxt[kbb], 0, 0, 0);
-        } else {
-          int db, kbb, s2;
-          pv_order(st, db, kbb, s2);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], pprev[kbb][s2], oacc[db], 0, 0, 0);
-        }
-        // softmax of tile tau, front-loaded: slot i < 4 takes probabilities 2i and 2i+1, slot
-        // 4 <= i < 28 probability i + 4; each is summed and packed one slot after its exp (so no
-        // VALU op waits on the transcendental unit), and slots 29 and 30 form the row sum, so the
-        // rare-path test after the last MFMA has its operands ready.  PRoPE keeps one probability
-        // per slot (its frame-boundary query transform leaves no registers for the extra exps).
-        {
-          auto retire = [&](int d) {
-            ls[d & 3] = d < 4 ? pf[d] : ls[d & 3] + pf[d];
-            asm volatile("" ::"v"(ls[d & 3]));
-            if (d & 1) {
-              pb[d >> 4][(d >> 3) & 1][(d & 7) - 1] = (bf16)pf[d - 1];
-              pb[d >> 4][(d >> 3) & 1][d & 7] = (bf16)pf[d];
-            }
-            if ((d & 7) == 7) asm volatile("" ::"v"(pb[d >> 4][(d >> 3) & 1]));
-          };
-          auto expo = [&](int e) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
-            asm volatile("" ::"v"(p));  // keep this exp next to its MFMA
-            pf[e] = p;
-          };
-          if constexpr (kFront) {
-            if (i >= 1 && i <= 4) {
-              retire(2 * (i - 1));
-              retire(2 * (i - 1) + 1);
-            } else if (i >= 5 && i <= 28) {
-              retire(i + 3);
-            }
-            if (i < 4) {
-              expo(2 * i);
-              expo(2 * i + 1);
-            } else if (i < 28) {
-              expo(i + 4);
-            }
-            if (i == 29) {
-              lp01 = ls[0] + ls[1];
-              lp23 = ls[2] + ls[3];
-            }
-            if (i == 30) {
-              lp = lp01 + lp23;
-              need = !(lp <= kMaxPart) || m_run == -INFINITY;
-            }
-          } else {
-            if (i > 0) retire(i - 1);
-            expo(i);
+    for (int i = 0; i < 32; ++i) {
+      if (i + 3 < 32) opq[(i + 3) & 3] = operand(i + 3);
+      if (i == kLoadSlot) issue_loads();
+      // wave priority falls over the tile (2, 1, 0 by thirds): the wave that is ahead yields
+      // issue slots to the one behind, so both reach the tile's barrier closer together
+      if (i == 0) __builtin_amdgcn_s_setprio(2);
+      if (i == 11) __builtin_amdgcn_s_setprio(1);
+      if (i == 22) __builtin_amdgcn_s_setprio(0);
+      const int st = i >> 1;
+      if ((i & 1) == 0) {
+        const int k = st >> 1, kbb = st & 1;
+        s_nxt[kbb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], qf[k], k == 0 ? zero16 : s_nxt[kbb], 0, 0, 0);
+      } else {
+        int db, kbb, s2;
+        pv_order(st, db, kbb, s2);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], pprev[kbb][s2], oacc[db], 0, 0, 0);
+      }
+      // softmax of tile tau, front-loaded: slot i < 4 takes probabilities 2i and 2i+1, slot
+      // 4 <= i < 28 probability i + 4; each is summed and packed one slot after its exp (so no
+      // VALU op waits on the transcendental unit), and slots 29 and 30 form the row sum, so the
+      // rare-path test after the last MFMA has its operands ready.  PRoPE keeps one probability
+      // per slot (its frame-boundary query transform leaves no registers for the extra exps).
+      {
+        auto retire = [&](int d) {
+          ls[d & 3] = d < 4 ? pf[d] : ls[d & 3] + pf[d];
+          asm volatile("" ::"v"(ls[d & 3]));
+          if (d & 1) {
+            pb[d >> 4][(d >> 3) & 1][(d & 7) - 1] = (bf16)pf[d - 1];
+            pb[d >> 4][(d >> 3) & 1][d & 7] = (bf16)pf[d];
           }
+          if ((d & 7) == 7) asm volatile("" ::"v"(pb[d >> 4][(d >> 3) & 1]));
+        };
+        auto expo = [&](int e) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], c2, -m_use));
+          asm volatile("" ::"v"(p));  // keep this exp next to its MFMA
+          pf[e] = p;
+        };
+        if constexpr (kFront) {
+          if (i >= 1 && i <= 4) {
+            retire(2 * (i - 1));
+            retire(2 * (i - 1) + 1);
+          } else if (i >= 5 && i <= 28) {
+            retire(i + 3);
+          }
+          if (i < 4) {
+            expo(2 * i);
+            expo(2 * i + 1);
+          } else if (i < 28) {
+            expo(i + 4);
+          }
+          if (i == 29) {
+            lp01 = ls[0] + ls[1];
+            lp23 = ls[2] + ls[3];
+          }
+          if (i == 30) {
+            lp = lp01 + lp23;
+            need = !(lp <= kMaxPart) || m_run == -INFINITY;
+          }
+        } else {
+          if (i > 0) retire(i - 1);
+          expo(i);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
-      if constexpr (!kFront) {
-        ls[3] += pf[31];
-        pb[1][1][6] = (bf16)pf[30];
-        pb[1][1][7] = (bf16)pf[31];
-        lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
-        need = !(lp <= kMaxPart) || m_run == -INFINITY;
-      }
-      if (__any(need)) {
-        // rare path: both key halves of a query take the same decision; raise the max of each
-        // such query to the tile's true max, recompute its probabilities, rescale O and l
-        const bool needq = pair_max(need ? 1.f : 0.f) > 0.f;
-        float mx = -INFINITY;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (!kFront) {
+      ls[3] += pf[31];
+      pb[1][1][6] = (bf16)pf[30];
+      pb[1][1][7] = (bf16)pf[31];
+      lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+      need = !(lp <= kMaxPart) || m_run == -INFINITY;
+    }
+    if (__any(need)) {
+      // rare path: both key halves of a query take the same decision; raise the max of each
+      // such query to the tile's true max, recompute its probabilities, rescale O and l
+      const bool needq = pair_max(need ? 1.f : 0.f) > 0.f;
+      float mx = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) mx = fmaxf(mx, s_cur[e >> 4][e & 15]);
-        mx = pair_max(mx) * c2;
-        const float m_new = needq ? fmaxf(m_run, mx) : m_run;
-        const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        const float mu = m_new == -INFINITY ? 0.f : m_new;  // = m_use for lanes kept
+      for (int e = 0; e < 32; ++e) mx = fmaxf(mx, s_cur[e >> 4][e & 15]);
+      mx = pair_max(mx) * c2;
+      const float m_new = needq ? fmaxf(m_run, mx) : m_run;
+      const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float mu = m_new == -INFINITY ? 0.f : m_new;  // = m_use for lanes kept
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ls[e] = 0.f;
+      for (int e = 0; e < 4; ++e) ls[e] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) prob(e, mu);
-        lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
-        l_run *= alpha;
+      for (int e = 0; e < 32; ++e) prob(e, mu);
+      lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+      l_run *= alpha;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-        m_run = m_new;
-      }
-      l_run += lp;
-      if (tau + 1 < ntau) {
-        int tok0, key0;
-        if (walk_needs_mask(mw, tok0, key0)) mask_tile(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
-      }
-    }  // !wave_dead
+        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+      m_run = m_new;
+    }
+    l_run += lp;
+    if (tau + 1 < ntau) {
+      int tok0, key0;
+      if (walk_needs_mask(mw, tok0, key0)) mask_tile(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
+    }
     kw.next(a, kbh);
     vw.next(a, kbh);
     mw.next(a, kbh);
