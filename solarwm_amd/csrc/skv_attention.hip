@@ -841,6 +841,12 @@ __device__ inline int pack_fp8x4(float x0, float x1, float x2, float x3) {
   const int v = __builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false);
   return __builtin_amdgcn_cvt_pk_fp8_f32(x2, x3, v, true);
 }
+// The same into a register whose previous contents are overwritten whole by the two converts
+// (low then high half), so no zeroing move is needed.
+__device__ inline int pack_fp8x4_into(int old, float x0, float x1, float x2, float x3) {
+  const int v = __builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, old, false);
+  return __builtin_amdgcn_cvt_pk_fp8_f32(x2, x3, v, true);
+}
 
 __device__ inline void mask_tile64(f32x16 (&s)[2], int hh, int tok0, int T, int key0, int lim) {
 #pragma unroll
@@ -1090,11 +1096,15 @@ void attn_fp8_kernel(AttnArgs a) {
         oacc[i >> 1] = mfma64(op[i & 3], pprev, oacc[i >> 1]);
       }
       if (i == 0) {  // the tile's max, the running max and the exponent bias
-        float mx = -INFINITY;
+        // four independent chains, so the max is not one 16-deep dependency before the MFMAs
+        float mq[4];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int c = 0; c < 4; ++c) {
+          mq[c] = s_cur[c >> 1][(c & 1) * 8];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[kb][r]);
+          for (int r = 1; r < 8; ++r) mq[c] = fmaxf(mq[c], s_cur[c >> 1][(c & 1) * 8 + r]);
+        }
+        float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
         mx = pair_max(mx) * mult;
         const bool raise = mx > m_run + kStale8;
         alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
@@ -1111,14 +1121,14 @@ void attn_fp8_kernel(AttnArgs a) {
         const int d = i - 1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) ls[j] = d == 0 ? pf[4 * d + j] : ls[j] + pf[4 * d + j];
-        pb[d] = pack_fp8x4(pf[4 * d], pf[4 * d + 1], pf[4 * d + 2], pf[4 * d + 3]);
+        pb[d] = pack_fp8x4_into(pb[d], pf[4 * d], pf[4 * d + 1], pf[4 * d + 2], pf[4 * d + 3]);
         asm volatile("" ::"v"(pb[d]));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) ls[j] += pf[28 + j];
-    pb[7] = pack_fp8x4(pf[28], pf[29], pf[30], pf[31]);
+    pb[7] = pack_fp8x4_into(pb[7], pf[28], pf[29], pf[30], pf[31]);
     l_run = fmaf(l_run, alpha, ((ls[0] + ls[1]) + (ls[2] + ls[3])) * inv_pv);
     if (__any(alpha != 1.0f)) {
 #pragma unroll
