@@ -1050,7 +1050,26 @@ void attn_fp8_kernel(AttnArgs a) {
   kw.start(a, kbh, 2);
   vw.start(a, kbh, 0);
   mw.start(a, kbh, 1);
-  float mult = 0.f, log_pv = 0.f, inv_pv = 1.0f;  // per key frame (see below)
+  // Per key frame: the softmax multiplier (K scale folded in) and the log and reciprocal of the
+  // P scale.  Set for the frame of tile tau+1 at the end of step tau, after the wait for the
+  // step's loads, so a register reload here cannot drain loads still in flight.
+  float mult = 0.f, log_pv = 0.f, inv_pv = 1.0f;
+  auto open_scales = [&]() {
+    const int64_t sc = (int64_t)vw.slot * a.B * a.H + sc_bh;
+    // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
+    // masked (-inf) logits stay -inf instead of becoming NaN.  The scales are read through the
+    // constant address space (scalar loads).
+    typedef const __attribute__((address_space(4))) float* cfloat_p;
+    mult = fmaxf(c2q * ((cfloat_p)(uintptr_t)a.kscale)[sc], 1e-30f);
+    // P is stored as p * sv * G: the factor rides in the exponent's bias (one log per key frame
+    // instead of 32 multiplies per tile) and the row sum divides it out once.  An all-zero V
+    // frame (sv = 0) keeps P unscaled: its V codes are all 0, so only the sum sees P.
+    const float pv_raw = ((cfloat_p)(uintptr_t)a.vscale)[sc] * G;
+    const float pv = pv_raw > 0.f ? pv_raw : 1.0f;
+    log_pv = __builtin_amdgcn_logf(pv);
+    inv_pv = __builtin_amdgcn_rcpf(pv);
+  };
+  if (ntau > 0) open_scales();
   // cb = tau & 1, passed as a literal so buffer addresses fold into immediate offsets
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], const i32x8& pprev,
                   i32x8& pb) __attribute__((always_inline)) {
@@ -1058,19 +1077,6 @@ void attn_fp8_kernel(AttnArgs a) {
     if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(cb));
     const char* kl = kb_lds(cb ^ 1) + lane32;  // K(tau+1)
     const char* vl = vb_lds(cb ^ 1) + lane32;  // V(tau-1) (zeros on the first iteration)
-    if (tau == 0 || vw.t == 0) {  // a new key frame: its K and V scales
-      const int64_t sc = (int64_t)vw.slot * a.B * a.H + sc_bh;
-      // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
-      // masked (-inf) logits stay -inf instead of becoming NaN
-      mult = fmaxf(c2q * a.kscale[sc], 1e-30f);
-      // P is stored as p * sv * G: the factor rides in the exponent's bias (one log per key
-      // frame instead of 32 multiplies per tile) and the row sum divides it out once.  An all-zero V frame
-      // (sv = 0) keeps P unscaled: its V codes are all 0, so only the sum sees P.
-      const float pv_raw = a.vscale[sc] * G;
-      const float pv = pv_raw > 0.f ? pv_raw : 1.0f;
-      log_pv = __builtin_amdgcn_logf(pv);
-      inv_pv = __builtin_amdgcn_rcpf(pv);
-    }
 
     // Eight MFMA slots, QK(tau+1) and PV(tau-1) alternating (QK steps in the order (kb, cs) =
     // (0,0), (1,0), (0,1), (1,1), so the two halves of one key block are four slots apart), each
@@ -1145,6 +1151,7 @@ void attn_fp8_kernel(AttnArgs a) {
     vw.next(a, kbh);
     mw.next(a, kbh);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tau + 1 < ntau && vw.t == 0) open_scales();  // tile tau+1 opens a key frame
     __syncthreads();
   };
   int tau = 0;
