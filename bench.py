@@ -437,7 +437,8 @@ def gather_bandwidth(device, iters=20):
 def probe(cfg, device, iters=20):
     """Short fixed sequence for hardware-counter runs (rocprofv3 --pmc): a plain device copy of
     exactly 1 GiB (the FETCH_SIZE / WRITE_SIZE calibration), then steady-state launches of the
-    append kernel (one chunk, Lq tokens) and the attention kernel (Lq x full window)."""
+    append kernel (one chunk, Lq tokens), the attention kernel (Lq x full window) and the
+    config-4 memory-bank gather (8 seeded frames of a 256-slot bank, H=40)."""
     import torch
 
     from solarwm_amd import kernels
@@ -460,7 +461,20 @@ def probe(cfg, device, iters=20):
     for _ in range(iters):
         kernels.attention_frames(q, kpool, vpool, slots, frame_tokens=T)
     torch.cuda.synchronize()
-    log(f"[probe] copy 1 GiB x3, append x{iters} ({Lq} tokens), attention x{iters} (Lq {Lq}, Lk {n * T})")
+    del kpool, vpool
+    # config-4 gather, as gather_bandwidth() times it
+    Tb, Hb, n_bank = C4["T"], C4["heads"], C4["bank"]
+    bk, bv, _, _ = kernels.new_pools(n_bank, 1, Hb, Tb, torch.bfloat16, device)
+    g = torch.Generator().manual_seed(4)
+    idx = torch.randperm(n_bank, generator=g)[:C4["mem_frames"]].tolist()
+    ko = torch.empty(1, len(idx) * Tb, Hb, 128, dtype=torch.bfloat16, device=device)
+    vo = torch.empty_like(ko)
+    launch, _, _ = kernels.prepare_gather(bk, bv, idx, frame_tokens=Tb, k_out=ko, v_out=vo)
+    for _ in range(iters):
+        launch()
+    torch.cuda.synchronize()
+    log(f"[probe] copy 1 GiB x3, append x{iters} ({Lq} tokens), attention x{iters} (Lq {Lq}, Lk {n * T}), "
+        f"gather x{iters} ({len(idx)} of {n_bank} frames, H{Hb})")
 
 
 def steady_state(name, device, fill=7, timed=3, rope=False, prope=False):
