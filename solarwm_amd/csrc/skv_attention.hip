@@ -896,7 +896,7 @@ __device__ inline void qk64(const char* kl, const i32x8 (&q8)[2], const f32x16& 
   }
 }
 
-template <int NW, typename QT>
+template <int NW, typename QT, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fp8_kernel(AttnArgs a) {
   constexpr int kBQ = NW * 32;
@@ -909,10 +909,34 @@ void attn_fp8_kernel(AttnArgs a) {
     const int per = a.n_wg >> 3, rem = a.n_wg & 7;
     logical = xcd * per + min(xcd, rem) + idx;
   }
-  const int qt = logical % a.n_qtiles;
-  const int bh = logical / a.n_qtiles;
+  // Segments: key tiles [tb, te) of q-tile qg, as in attn_kernel (one whole q-tile unless split;
+  // a split share runs its whole q-tiles, then its last segment, then its first).
+  const int nt = a.n_frames * a.ntiles_f;
+  int q_first = logical, nseg = 1;
+  int64_t u0 = 0, u1 = 0;
+  if constexpr (SPLIT) {
+    u0 = (int64_t)logical * a.units / a.n_wg;
+    u1 = (int64_t)(logical + 1) * a.units / a.n_wg;
+    q_first = (int)(u0 / nt);
+    nseg = u1 > u0 ? (int)((u1 - 1) / nt) - q_first + 1 : 0;
+  }
+  for (int k = 0; k < nseg; ++k) {
+  const int seg = nseg == 1 ? 0 : k < nseg - 2 ? k + 1 : k == nseg - 2 ? nseg - 1 : 0;
+  const int qg = q_first + seg;
+  int tb = 0, te = nt;
+  if constexpr (SPLIT) {
+    if (seg == 0) tb = (int)(u0 - (int64_t)q_first * nt);
+    if (seg == nseg - 1) te = (int)(u1 - (int64_t)qg * nt);
+  }
+  if (k > 0) __syncthreads();  // the previous segment's last LDS reads are done
+  const int qt = qg % a.n_qtiles;
+  const int bh = qg / a.n_qtiles;
   const int h = bh % a.H, b = bh / a.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // SPLIT: an opaque copy per segment keeps lane-derived values out of the segment loop's
+  // live range
+  int tid = threadIdx.x;
+  if constexpr (SPLIT) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, w = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
   const int q0 = qt * kBQ;
   const int qrow = q0 + w * 32 + n;
@@ -970,18 +994,19 @@ void attn_fp8_kernel(AttnArgs a) {
     const int jf = lim_hi / a.T;
     ntau = jf >= a.n_frames ? a.n_frames * a.ntiles_f
                             : jf * a.ntiles_f + (lim_hi - jf * a.T + kTile - 1) / kTile;
+    if constexpr (SPLIT) ntau = te - tb;  // no mask: the segment's tiles
   }
 
   const uint8_t* kpool = static_cast<const uint8_t*>(a.kpool);
   const uint8_t* vpool = static_cast<const uint8_t*>(a.vpool);
   const int64_t kbh = (int64_t)(b * a.H + h) * a.Tp * kHeadDim;
   const int64_t sc_bh = (int64_t)b * a.H + h;
-  auto ktile = [&](int tau) {
-    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+  auto ktile = [&](int tau) {  // tile tau of the segment
+    const int x = tb + tau, j = x / a.ntiles_f, t = x - j * a.ntiles_f;
     return kpool + (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
   };
   auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
-    const int j = tau / a.ntiles_f, t = tau - j * a.ntiles_f;
+    const int x = tb + tau, j = x / a.ntiles_f, t = x - j * a.ntiles_f;
     tok0 = t * kTile;
     key0 = j * a.T + tok0;
     tj = a.flen[j];
@@ -1047,9 +1072,9 @@ void attn_fp8_kernel(AttnArgs a) {
   // Tiles addressed in step tau: K(tau+2) (kw), V(tau) and its frame's scales (vw), the mask of
   // QK(tau+1) (mw); the walks advance one tile per step.
   TileWalk kw, vw, mw;
-  kw.start(a, kbh, 2);
-  vw.start(a, kbh, 0);
-  mw.start(a, kbh, 1);
+  kw.start(a, kbh, tb + 2);
+  vw.start(a, kbh, tb);
+  mw.start(a, kbh, tb + 1);
   // Per key frame: the softmax multiplier (K scale folded in) and the log and reciprocal of the
   // P scale.  Set for the frame of tile tau+1 at the end of step tau, after the wait for the
   // step's loads, so a register reload here cannot drain loads still in flight.
@@ -1172,6 +1197,24 @@ void attn_fp8_kernel(AttnArgs a) {
     epilogue(pA);
   }
   const float l_tot = pair_sum(l_run);
+  if (SPLIT && (tb > 0 || te < nt)) {
+    // part of a split q-tile: O / G (the P scale's G divided out), the running max in log2
+    // units and the row sum, the record attn_combine_kernel merges
+    if (qlive) {
+      const float ig = 1.0f / G;
+      const int64_t row = (2 * (int64_t)logical + (seg > 0 ? 1 : 0)) * kBQ + w * 32 + n;
+      float* po = a.part_o + row * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(po + db * 32 + g * 8 + hh * 4) =
+              f32x4{oacc[db][g * 4] * ig, oacc[db][g * 4 + 1] * ig, oacc[db][g * 4 + 2] * ig,
+                    oacc[db][g * 4 + 3] * ig};
+      if (hh == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run, l_tot);
+    }
+    continue;
+  }
   const float inv = l_tot > 0.f ? 1.0f / (l_tot * G) : 0.f;
   if (qlive) {
     QT* op = static_cast<QT*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
@@ -1184,6 +1227,7 @@ void attn_fp8_kernel(AttnArgs a) {
         store4<QT>(op + d0, oacc[db][g * 4 + 0] * inv, oacc[db][g * 4 + 1] * inv,
                    oacc[db][g * 4 + 2] * inv, oacc[db][g * 4 + 3] * inv);
       }
+  }
   }
 }
 
@@ -1301,6 +1345,15 @@ template <int NW>
 static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipStream_t s) {
   dim3 grid(a.n_wg), block(NW * 64);
   if (pool_dtype == SKV_FP8_E4M3) {
+    if constexpr (NW == 8) {
+      if (a.split) {
+        if (q_dtype == SKV_BF16)
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 16 * kOp8, s, a);
+        else
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 16 * kOp8, s, a);
+        return;
+      }
+    }
     if (q_dtype == SKV_BF16)
       hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 16 * kOp8, s, a);
     else
@@ -1510,8 +1563,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   const int nt = n_frames * a.ntiles_f;
   const int64_t qt8 = (int64_t)((q_len + kSplitBQ - 1) / kSplitBQ) * heads * batch;
   const int64_t units8 = qt8 * nt;
-  if (mask_mode == SKV_MASK_NONE && pool_dtype != SKV_FP8_E4M3 && nt >= 8 && units8 >= 4 * n_cu &&
-      n_cu <= kMaxSplitWg) {
+  if (mask_mode == SKV_MASK_NONE && nt >= 8 && units8 >= 4 * n_cu && n_cu <= kMaxSplitWg) {
     auto t_tile = [&](int64_t busy) { return 1.0 + 0.62 * (double)busy / n_cu; };
     auto t_grid = [&](int64_t wg, int per_cu, double per_tile) {  // rounds of nt tiles
       const int64_t slots = (int64_t)n_cu * per_cu, full = wg / slots, last = wg - full * slots;

@@ -1,4 +1,4 @@
-"""GPU parity of the balanced key split of the bf16 attention kernel (one workgroup per CU over
+"""GPU parity of the balanced key split of the attention kernels (one workgroup per CU over
 equal shares of the (q-tile, key tile) units, split q-tiles merged by a second kernel) against
 the float64 oracle (oracle/wan_cache_ref.py attention, attention.py:141-188 of the reference).
 
@@ -121,3 +121,50 @@ def test_split_with_q_norm(gpu):
                                    q_norm=(kernels.rms_rows(qd, eps), w.to(gpu)))
     torch.cuda.synchronize()
     assert_attn_close(got, ref.attention(ref.norm_heads(q, w, eps), k, v))
+
+
+def test_split_fp8_ragged_and_zero_frames(gpu):
+    """The split path of the fp8 cache kernel: frames keep 1..1560 of their keys (shares with no
+    visible key), one K frame and one V frame are all zero (scale 0), and 1% of the channels
+    are x20 outliers.  Compared with the quantisation-aware oracle (fp8 frames and query rows
+    decoded, fp64 softmax); the error is divided by each channel's V RMS."""
+    from .helpers import FP8_NORM_MAX, FP8_NORM_MEAN
+
+    T, n, H, Lq = 1560, 21, 2, 256  # 2 q-tiles x 525 key tiles over 256 workgroups
+    _say("split fp8 attention", H, Lq, T, n)
+    lens = [5, 70, 1560, 64, 65, 1, 1560, 900] + [7] * (n - 8)
+    g = torch.Generator().manual_seed(50)
+    k = torch.randn(1, n * T, H, 128, generator=g)
+    v = torch.randn(1, n * T, H, 128, generator=g)
+    ch = torch.randperm(128, generator=g)[:2]
+    k[..., ch] *= 20.0
+    v[..., ch] *= 20.0
+    k[:, 2 * T : 3 * T] = 0
+    v[:, 6 * T : 7 * T] = 0
+    k, v = k.to(BF), v.to(BF)
+    q = _rand((1, Lq, H, 128), 51)
+    g = torch.Generator().manual_seed(5)
+    slots = torch.randperm(n + 2, generator=g)[:n].tolist()
+    kp, vp, ks, vs = kernels.new_pools(n + 2, 1, H, T, torch.float8_e4m3fn, gpu)
+    kd, vd = k.to(gpu), v.to(gpu)
+    for f in range(n):
+        kernels.append_frames(kd, vd, kp, vp, [slots[f]], frame_tokens=T, src_frame0=f,
+                              kscale=ks, vscale=vs)
+    got = kernels.attention_frames(q.to(gpu), kp, vp, slots, frame_tokens=T, kscale=ks,
+                                   vscale=vs, frame_lens=lens)
+    again = kernels.attention_frames(q.to(gpu), kp, vp, slots, frame_tokens=T, kscale=ks,
+                                     vscale=vs, frame_lens=lens)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
+    kq = ref.fp8_fake_quant_frames(k.float(), T)
+    vq = ref.fp8_fake_quant_frames(v.float(), T)
+    keys = torch.cat([kq[:, j * T : j * T + lens[j]] for j in range(n)], 1)
+    vals = torch.cat([vq[:, j * T : j * T + lens[j]] for j in range(n)], 1)
+    want = ref.attention(ref.fp8_fake_quant_rows(q), keys, vals, round_inputs_to_bf16=False).double()
+    rms_v = torch.cat([v[:, j * T : j * T + lens[j]] for j in range(n)], 1).double()
+    rms_v = rms_v.pow(2).mean(dim=1, keepdim=True).sqrt().clamp_min(1e-6)
+    got = got.cpu().double()
+    assert torch.isfinite(got).all()
+    e = (got - want).abs() / rms_v
+    assert float(e.max()) <= FP8_NORM_MAX, f"normalised max error {float(e.max()):.3e}"
+    assert float(e.mean()) <= FP8_NORM_MEAN, f"normalised mean error {float(e.mean()):.3e}"
