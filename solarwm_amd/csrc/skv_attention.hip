@@ -1306,7 +1306,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 
 using namespace skv;
 
-static int cu_count() {
+int skv::cu_count() {
   static int n = 0;
   if (n == 0) {
     int dev = 0, v = 0;
@@ -1319,10 +1319,10 @@ static int cu_count() {
   return n;
 }
 
-// Workspace of the split path, stream-ordered from the device's default memory pool.  The pool
-// keeps freed memory for reuse (release threshold raised once per device), so repeated calls
-// do not map and unmap pages.
-static bool split_workspace(void** p, size_t bytes, hipStream_t s) {
+// Workspace of the split paths (attention records, fp8 append tile maxima), stream-ordered from
+// the device's default memory pool.  The pool keeps freed memory for reuse (release threshold
+// raised once per device), so repeated calls do not map and unmap pages.
+bool skv::stream_workspace(void** p, size_t bytes, hipStream_t s) {
   static std::mutex mu;
   static bool tuned[64] = {};
   int dev = 0;
@@ -1614,7 +1614,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   if (a.split) {
     // stream-ordered workspace: 2 records per workgroup (O, then max and sum)
     const size_t rec_rows = (size_t)2 * a.n_wg * kSplitBQ;
-    if (!split_workspace(&ws, rec_rows * (kHeadDim + 2) * sizeof(float), s)) {
+    if (!stream_workspace(&ws, rec_rows * (kHeadDim + 2) * sizeof(float), s)) {
       set_error("skv_attention: workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
       return SKV_E_LAUNCH;
     }

@@ -455,6 +455,132 @@ __global__ __launch_bounds__(1024) void append_fp8_kernel(AppendArgs a) {
   }
 }
 
+// fp8 append split over 64-token tiles, for chunks with fewer (frame, batch, head, K|V) units
+// than the chip has CUs several times over (C5: 288 units of 25 tiles on 256 CUs, where one
+// workgroup per unit runs two rounds of long serial streams).  grid.x = units * ntiles, tile
+// fastest, unit u = ((f * B + b) * H + h) * 2 + is_v as in the per-unit kernels.
+//  pass 1 (fp8_tile_absmax_kernel): part[blockIdx.x] = absmax of the tile's values (K after its
+//          RMSNorm); rows >= T are not read.
+//  pass 2 (append_fp8_tile_kernel): amax = max of the unit's tile maxima (the frame's absmax,
+//          as the per-unit kernels reduce it), tile 0 stores the scale amax / 448, every tile
+//          re-reads its rows (L2/MALL resident after pass 1) and stores their codes; rows T..Tp-1
+//          get code 0.  V^T goes through an LDS tile.
+struct TileUnit {
+  int t, is_v, h, b, f;
+  __device__ explicit TileUnit(const AppendArgs& a) {
+    int wg = blockIdx.x;
+    t = wg % a.ntiles;
+    wg /= a.ntiles;
+    is_v = wg & 1;
+    wg >>= 1;
+    h = wg % a.H;
+    wg /= a.H;
+    b = wg % a.B;
+    f = wg / a.B;
+  }
+};
+
+template <typename E>
+__device__ inline const E* tile_src(const AppendArgs& a, const TileUnit& u) {
+  return static_cast<const E*>(u.is_v ? a.vsrc : a.ksrc) + (int64_t)u.b * a.s_sb +
+         (int64_t)u.h * a.s_sh + ((int64_t)(a.src_frame0 + u.f) * a.T + u.t * kTile) * a.s_st;
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void fp8_tile_absmax_kernel(AppendArgs a, float* part) {
+  __shared__ float red[4];
+  const TileUnit u(a);
+  const E* src = tile_src<E>(a, u);
+  const int tid = threadIdx.x, rows = min(kTile, a.T - u.t * kTile);
+  const bool knorm = !u.is_v && a.krms;
+  const int64_t tok0 = (int64_t)(a.src_frame0 + u.f) * a.T + u.t * kTile;
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // 64 rows x 16 vec8 = 4 per thread
+    const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 8;
+    if (row < rows) {
+      Vec8<E> x = Vec8<E>::load(src + (int64_t)row * a.s_st + col);
+      if (knorm) norm8(x, a, u.b, u.h, tok0 + row, col);
+      m = absval8(x, m);
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) part[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+template <typename E>
+__device__ inline u32x2 quant_vec8(const Vec8<E>& v, float inv);
+template <>
+__device__ inline u32x2 quant_vec8<bf16>(const Vec8<bf16>& v, float inv) {
+  return quant8(v.r, inv);
+}
+template <>
+__device__ inline u32x2 quant_vec8<float>(const Vec8<float>& v, float inv) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t code = f32_to_e4m3(fminf(fmaxf(v.get(i) * inv, -448.0f), 448.0f));
+    if (i < 4) lo |= code << (8 * i); else hi |= code << (8 * (i - 4));
+  }
+  return u32x2{lo, hi};
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void append_fp8_tile_kernel(AppendArgs a, const float* part) {
+  constexpr int kRowT = kTile + 4;  // V^T tile row: 64 codes + 4 bytes of skew
+  __shared__ __attribute__((aligned(16))) uint8_t vt8[kHeadDim * kRowT];
+  const TileUnit u(a);
+  const E* src = tile_src<E>(a, u);
+  const int tid = threadIdx.x, rows = min(kTile, a.T - u.t * kTile);
+  const float* pm = part + (int64_t)(blockIdx.x - u.t);
+  float amax = 0.f;
+  for (int i = 0; i < a.ntiles; ++i) amax = fmaxf(amax, pm[i]);
+  const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+  const int64_t slot = a.slots[u.f];
+  if (u.t == 0 && tid == 0) {
+    float* sc = u.is_v ? a.vscale : a.kscale;
+    sc[(slot * a.B + u.b) * a.H + u.h] = amax / 448.0f;
+  }
+  const bool knorm = !u.is_v && a.krms;
+  const int64_t tok0 = (int64_t)(a.src_frame0 + u.f) * a.T + u.t * kTile;
+  uint8_t* pool = static_cast<uint8_t*>(u.is_v ? a.vpool : a.kpool) + slot * a.slot_stride +
+                  (int64_t)(u.b * a.H + u.h) * a.Tp * kHeadDim;
+  u32x2 q[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 8;
+    Vec8<E> x = Vec8<E>::zero();
+    if (row < rows) {
+      x = Vec8<E>::load_nt(src + (int64_t)row * a.s_st + col);
+      if (knorm) norm8(x, a, u.b, u.h, tok0 + row, col);
+    }
+    q[i] = quant_vec8<E>(x, inv);
+  }
+  if (!u.is_v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 8;
+      *reinterpret_cast<u32x2*>(pool + (int64_t)(u.t * kTile + row) * kHeadDim + col) = q[i];
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vt8[(col + e) * kRowT + row] = (uint8_t)(q[i][e >> 2] >> (8 * (e & 3)));
+  }
+  __syncthreads();
+  // channel d, tokens tc .. tc+31 of the tile
+  const int d = tid >> 1, tc = (tid & 1) * 32;
+  const uint32_t* rd = reinterpret_cast<const uint32_t*>(vt8 + d * kRowT + tc);
+  uint8_t* dst = pool + (int64_t)d * a.Tp + u.t * kTile + tc;
+  st_nt(dst, u32x4{rd[0], rd[1], rd[2], rd[3]});
+  st_nt(dst + 16, u32x4{rd[4], rd[5], rd[6], rd[7]});
+}
+
 // Inverse RMS of each token's H x D row (WanRMSNorm's statistic, model.py:69-84):
 // out[b * rows + t] = 1 / sqrt(mean(x^2) + eps) in fp32.  One wave per token: lane l sums the
 // squares of 8-element chunks l, l+64, ... of the row (chunk c = head c / 16, channels
@@ -721,15 +847,34 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fp8) {
-    dim3 grid(n_frames * batch * heads * 2);
-    const bool reg_path = src_dtype == SKV_BF16 && a.ntiles <= kFp8OnChip &&
-                          (int64_t)a.Tp * src_st * 2 < ((int64_t)1 << 31);
-    if (reg_path)
-      hipLaunchKernelGGL(append_fp8_reg_kernel, grid, dim3(1024), 0, s, a);
-    else if (src_dtype == SKV_BF16)
-      hipLaunchKernelGGL(append_fp8_kernel<bf16>, grid, dim3(1024), 0, s, a);
-    else
-      hipLaunchKernelGGL(append_fp8_kernel<float>, grid, dim3(1024), 0, s, a);
+    const int units = n_frames * batch * heads * 2;
+    if (units < 4 * cu_count()) {  // too few units to fill the chip: split them into tiles
+      void* ws = nullptr;
+      if (!stream_workspace(&ws, (size_t)units * a.ntiles * sizeof(float), s)) {
+        set_error("skv_append: workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
+        return SKV_E_LAUNCH;
+      }
+      float* part = static_cast<float*>(ws);
+      dim3 tgrid(units * a.ntiles);
+      if (src_dtype == SKV_BF16) {
+        hipLaunchKernelGGL(fp8_tile_absmax_kernel<bf16>, tgrid, dim3(256), 0, s, a, part);
+        hipLaunchKernelGGL(append_fp8_tile_kernel<bf16>, tgrid, dim3(256), 0, s, a, part);
+      } else {
+        hipLaunchKernelGGL(fp8_tile_absmax_kernel<float>, tgrid, dim3(256), 0, s, a, part);
+        hipLaunchKernelGGL(append_fp8_tile_kernel<float>, tgrid, dim3(256), 0, s, a, part);
+      }
+      (void)hipFreeAsync(ws, s);
+    } else {
+      dim3 grid(units);
+      const bool reg_path = src_dtype == SKV_BF16 && a.ntiles <= kFp8OnChip &&
+                            (int64_t)a.Tp * src_st * 2 < ((int64_t)1 << 31);
+      if (reg_path)
+        hipLaunchKernelGGL(append_fp8_reg_kernel, grid, dim3(1024), 0, s, a);
+      else if (src_dtype == SKV_BF16)
+        hipLaunchKernelGGL(append_fp8_kernel<bf16>, grid, dim3(1024), 0, s, a);
+      else
+        hipLaunchKernelGGL(append_fp8_kernel<float>, grid, dim3(1024), 0, s, a);
+    }
   } else {
     dim3 grid(n_frames * batch * heads * a.ntiles);
     if (src_dtype == SKV_BF16) {

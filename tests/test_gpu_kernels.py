@@ -59,11 +59,14 @@ def test_append_gather_roundtrip_and_layout(gpu, dtype, B, H, T):
 @pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("B,H,T,wide", [(1, 12, 1560, False), (4, 2, 390, False),
                                         (1, 3, 100, False), (2, 2, 1560, True),
-                                        (1, 2, 1700, False), (1, 2, 1153, True)])
+                                        (1, 2, 1700, False), (1, 2, 1153, True),
+                                        (4, 64, 100, False), (4, 64, 1700, True)])
 def test_fp8_append_matches_oracle(gpu, src_dtype, B, H, T, wide):
-    """Frames of up to 25 tiles go through the on-chip kernel (bf16 sources), longer frames and
-    f32 sources through the two-pass kernel; ``wide``: the source is a head slice of a wider
-    tensor (token stride > H * 128)."""
+    """Chunks with fewer than 4 (frame, batch, head, K|V) units per CU go through the tile-split
+    kernels; the B=4, H=64 cases (1024 units) through one workgroup per unit: the on-chip
+    kernel for frames of up to 25 tiles from bf16 sources, the two-pass kernel for longer
+    frames and f32 sources.  ``wide``: the source is a head slice of a wider tensor (token
+    stride > H * 128)."""
     _say("fp8 append", src_dtype, B, H, T, wide)
     x = _rand((B, 2 * T, H + 3 if wide else H, 128), seed=11, dtype=torch.float32)[:, :, :H]
     g = torch.Generator().manual_seed(12)
