@@ -32,14 +32,24 @@ _DTYPE_CODES = {
 
 
 class LaunchTimer:
-    """HIP events around each kernel launch, recorded on the launching stream.
+    """HIP events around kernel launches, recorded on the launching stream.
 
     ``records[kind]`` is a list of ``(start_event, end_event, work)`` where ``work`` is the
-    launch's algorithmic FLOPs (attention) or bytes moved (append / gather).
+    launch's algorithmic FLOPs (attention) or bytes moved (append / gather).  With ``every=n``
+    only launches 0, n, 2n, ... of each kind are bracketed: a timing event waits for the work
+    before it, so events around every launch of a rollout add a gap to each launch.
     """
 
-    def __init__(self):
+    def __init__(self, every: int = 1):
         self.records: dict[str, list] = {"attention": [], "append": [], "gather": []}
+        self.every = max(1, int(every))
+        self.seen: dict[str, int] = {k: 0 for k in self.records}
+
+    def sample(self, kind: str) -> bool:
+        """Whether this launch of ``kind`` is bracketed (counts the launch)."""
+        n = self.seen[kind]
+        self.seen[kind] = n + 1
+        return n % self.every == 0
 
     def summary(self, kind: str) -> tuple[int, float, float]:
         """(launches, total milliseconds, total work) of one kernel kind; synchronises."""
@@ -55,18 +65,19 @@ _timer: LaunchTimer | None = None
 
 
 @contextmanager
-def timed_launches():
-    """Within the block, every append / gather / attention launch is bracketed by events."""
+def timed_launches(every: int = 1):
+    """Within the block, append / gather / attention launches are bracketed by events (every
+    ``every``-th launch of each kind, starting with the first)."""
     global _timer
-    prev, _timer = _timer, LaunchTimer()
+    prev, _timer = _timer, LaunchTimer(every)
     try:
         yield _timer
     finally:
         _timer = prev
 
 
-def _tic():
-    if _timer is None:
+def _tic(kind: str):
+    if _timer is None or not _timer.sample(kind):
         return None
     ev = torch.cuda.Event(enable_timing=True)
     ev.record()
@@ -296,7 +307,7 @@ def prepare_append(
     fn = getattr(lib, fn_name)
 
     def launch() -> None:
-        t0 = _tic()
+        t0 = _tic("append")
         _lib.check(fn_name, fn(*args))
         _toc("append", t0, moved)
 
@@ -369,7 +380,7 @@ def prepare_gather(
     def launch() -> None:
         if n == 0:
             return
-        t0 = _tic()
+        t0 = _tic("gather")
         _lib.check("skv_gather", lib.skv_gather(*args))
         _toc("gather", t0, moved)
 
@@ -447,7 +458,7 @@ def attention_frames(
     osb, ost, osh = _token_major("out", out)
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
     ks, vs = _scales(kpool, kscale, vscale)
-    t0 = _tic()
+    t0 = _tic("attention")
     if q_norm is not None or frame_lens is not None:
         rms_p = rms_sb = w_p = None
         if q_norm is not None:
