@@ -1556,7 +1556,10 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   // (measured on MI355X with 525 tiles per workgroup: 128, 224 and 256 busy CUs take 0.81, 0.92
   // and 1.0 of the full-chip time), modelled as t(busy) ~ 1 + 0.62 * busy / n_cu; the split
   // runs all CUs, plus about three tiles of segment set-up and merge.  Near-full grids (e.g.
-  // 228 q-tiles on 256 CUs) gain too little to pay for the merge and stay unsplit.
+  // 228 q-tiles on 256 CUs) gain too little to pay for the merge and stay unsplit.  A pair of
+  // 4-wave workgroups costs 1.10 of one 8-wave workgroup per tile (fitted to the C3 shape,
+  // H24 x 18480 keys, B 1 and 2), so 4-wave grids split at a smaller margin: the split also
+  // moves them onto the 8-wave kernel (C3: 0.598 -> 0.571 ms, B 2: 1.246 -> 1.154 ms).
   a.split = 0;
   a.units = 0;
   a.part_o = a.part_ml = nullptr;
@@ -1569,9 +1572,9 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
       const int64_t slots = (int64_t)n_cu * per_cu, full = wg / slots, last = wg - full * slots;
       return per_tile * nt * (full * t_tile(n_cu) + (last ? t_tile((last + per_cu - 1) / per_cu) : 0.0));
     };
-    const double t_plain = nw == 8 ? t_grid(a.n_wg, 1, 1.0) : t_grid(a.n_wg, 2, 1.04);
+    const double t_plain = nw == 8 ? t_grid(a.n_wg, 1, 1.0) : t_grid(a.n_wg, 2, 1.10);
     const double t_split = ((double)units8 / n_cu + 3.0) * t_tile(n_cu);
-    if (t_split < 0.85 * t_plain) {
+    if (t_split < (nw == 8 ? 0.85 : 0.97) * t_plain) {
       nw = 8;
       a.split = 1;
       a.n_qtiles = (int)(qt8 / ((int64_t)heads * batch));
