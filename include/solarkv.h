@@ -2,8 +2,13 @@
  * solarkv.h — C ABI of libsolarkv.so, the MI355X (gfx950) block-causal KV-cache path.
  *
  * Every entry point is stream-ordered (it enqueues work on `stream` and returns without a
- * host synchronisation), allocates nothing, and returns 0 on success or a negative SKV_E_*
- * code; skv_last_error() then names the failing argument.  All tensors are owned by the
+ * host synchronisation) and returns 0 on success or a negative SKV_E_* code; skv_last_error()
+ * then names the failing argument.  Two paths take a stream-ordered workspace from the
+ * device's default memory pool (hipMallocAsync / hipFreeAsync on `stream`; the pool keeps the
+ * pages mapped): attention over an under-filled grid (the balanced key split, 2 x n_cu x 256
+ * rows x 130 floats, 68 MB on 256 CUs) and an fp8 append of a chunk with fewer than 4
+ * (frame, batch, head, K|V) units per CU (one float per 64-token tile).  Nothing else
+ * allocates.  All tensors are owned by the
  * caller; pointers are device addresses unless the parameter says "host".
  *
  * Frame-slot pool layout (one pair of pools per transformer layer):
