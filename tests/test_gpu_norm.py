@@ -94,13 +94,15 @@ def test_append_norm_bf16(gpu, use_rope):
             assert ok, ("rope copy", i, err)
 
 
-@pytest.mark.parametrize("src,T", [(BF, 1560), (BF, 100), (BF, 1700), (torch.float32, 390)])
-def test_append_norm_fp8_codes(gpu, src, T):
+@pytest.mark.parametrize("src,T,B,H", [(BF, 1560, 1, 3), (BF, 100, 1, 3), (BF, 1700, 1, 3),
+                                       (torch.float32, 390, 1, 3), (BF, 1560, 4, 128),
+                                       (BF, 100, 4, 128), (torch.float32, 390, 4, 128)])
+def test_append_norm_fp8_codes(gpu, src, T, B, H):
     """fp8 codes and scales of a normalised append equal the oracle's quantisation of the
-    normalised K the bf16 append writes (on-chip kernel with register and LDS tiles, the
-    on-chip kernel with register tiles only, and the two-pass kernel)."""
-    _say("append norm fp8", src, T)
-    B, H = 1, 3
+    normalised K the bf16 append writes.  B=1, H=3 (6 units) runs the tile-split kernels;
+    B=4, H=128 (1024 units, 4 per CU) one workgroup per unit: the on-chip kernel with register
+    and LDS tiles, with register tiles only, and the two-pass kernel (f32 source)."""
+    _say("append norm fp8", src, T, B, H)
     k, v = _rows_scaled((B, T, H, 128), 5, src), _rand((B, T, H, 128), 6, src)
     w = _weight(H * 128, 7)
     kd, vd = k.to(gpu), v.to(gpu)
