@@ -3,13 +3,19 @@
  *
  * Every entry point is stream-ordered (it enqueues work on `stream` and returns without a
  * host synchronisation) and returns 0 on success or a negative SKV_E_* code; skv_last_error()
- * then names the failing argument.  Two paths take a stream-ordered workspace from the
- * device's default memory pool (hipMallocAsync / hipFreeAsync on `stream`; the pool keeps the
- * pages mapped): attention over an under-filled grid (the balanced key split, 2 x n_cu x 256
- * rows x 130 floats, 68 MB on 256 CUs) and an fp8 append of a chunk with fewer than 4
- * (frame, batch, head, K|V) units per CU (one float per 64-token tile).  Nothing else
- * allocates.  All tensors are owned by the
- * caller; pointers are device addresses unless the parameter says "host".
+ * then names the failing argument.  The library never allocates device memory: all tensors,
+ * including the scratch two faster paths use, are owned by the caller, and pointers are device
+ * addresses unless the parameter says "host".  The scratch ("workspace") paths are taken only
+ * through the descriptor entry points when the caller passes a workspace at least as large as
+ * the query functions report:
+ *   - attention over an under-filled grid takes the balanced key split (skv_attention_plan:
+ *     2 x n_cu x 256 rows x 130 floats, 68 MB on 256 CUs);
+ *   - an fp8 append of a chunk with fewer than 4 (frame, batch, head, K|V) units per CU takes
+ *     the tile-grid kernels (skv_append_workspace_size: one float per 64-token tile).
+ * Without a workspace the same calls run the unsplit kernels (same results up to fp32
+ * summation order for attention; bit-identical for the append).  A workspace is read and
+ * written by the launch on `stream` only, so one workspace serves any number of calls on one
+ * stream; calls on different streams need different workspaces.
  *
  * Frame-slot pool layout (one pair of pools per transformer layer):
  *   K pool  [n_slots][B][H][Tp][D]   row-major keys of each frame, D contiguous
@@ -232,9 +238,18 @@ typedef struct skv_append_desc {
   int grid_h, grid_w;
   void* vx_pool;
   const float* kv_xform;
+  void* workspace;         /* device, optional, 4-byte aligned: fp8 tile-grid kernels */
+  int64_t workspace_bytes; /* its size; must cover skv_append_workspace_size */
 } skv_append_desc;
 
 int skv_append_ex(const skv_append_desc* desc, skv_stream_t stream);
+
+/*
+ * Workspace skv_append_ex would use for `desc` (0 when the launch needs none: bf16/f32 pools,
+ * or an fp8 chunk with enough units to fill the chip); validates like skv_append_ex.  No
+ * reference counterpart (the reference append, causal_model.py:2894-2914, is a slice copy).
+ */
+int skv_append_workspace_size(const skv_append_desc* desc, int64_t* bytes);
 
 /*
  * Extended attention: every option of skv_attention / skv_attention_rope / skv_attention_prope
@@ -274,9 +289,28 @@ typedef struct skv_attention_desc {
   const float* out_xform;
   const int32_t* frame_lens; /* host, optional: valid keys of each listed frame (1..frame_tokens;
                                 keys past it are masked), for spans that are not whole frames */
+  void* workspace;            /* device, optional, 16-byte aligned: enables the balanced key split */
+  int64_t workspace_bytes;    /* its size; must cover skv_attention_plan's workspace_bytes */
 } skv_attention_desc;
 
 int skv_attention_ex(const skv_attention_desc* desc, skv_stream_t stream);
+
+/*
+ * The launch skv_attention_ex would make for `desc`, without launching (validates the same way
+ * and returns the same status).  workspace_bytes > 0 means the balanced key split pays for this
+ * shape and needs that much workspace; `split` says whether `desc` as given takes it (it does
+ * exactly when desc->workspace is set and large enough).  No reference counterpart: the
+ * reference attention (attention.py:141-188) has no launch choices to report.
+ */
+typedef struct skv_launch_plan {
+  int waves_per_group;     /* 8 (256 queries per workgroup) or 4 (128) */
+  int split;               /* 1: balanced key split over one workgroup per CU + merge kernel */
+  int n_workgroups;        /* workgroups of the main kernel */
+  int n_qtiles;            /* query tiles (over all batches and heads) */
+  int64_t workspace_bytes; /* workspace the split needs; 0 when it does not pay */
+} skv_launch_plan;
+
+int skv_attention_plan(const skv_attention_desc* desc, skv_launch_plan* plan);
 
 #ifdef __cplusplus
 }

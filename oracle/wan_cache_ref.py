@@ -10,6 +10,9 @@ Pinning (tests/test_oracle.py):
   published C1 known answer (visible key counts 1170..8190, evicted frames {1,2,3}, {4,5,6},
   {7,8,9}, final order [0, 10..29]); a token-labelled brute-force list model of "sink frames +
   the most recent window" on many geometries; recompute and ``none``-pass invariants.
+* ``rollout`` — the C1 known answer reached through the driver with token-labelled K/V on two
+  layers, plus the stage2 call pattern: layers in order within a pass, ``none`` passes leave the
+  committed indices unchanged and see the same window as the chunk's commit pass.
 * ``attention`` — explicit float64 loops of softmax(q kᵀ/√d) v; closed forms (identical keys →
   mean of V; one key → V; key-order invariance).
 * ``inference_window_mask`` / ``block_classes`` — brute-force rule "chunk i sees chunks 0..i"

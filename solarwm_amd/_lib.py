@@ -45,7 +45,7 @@ class AppendDesc(ctypes.Structure):
         ("frame_tokens", _i32),
         ("k_inv_rms", _vp), ("k_rms_stride_b", _i64), ("k_norm_weight", _vp),
         ("kr_pool", _vp), ("rope_hw", _vp), ("grid_h", _i32), ("grid_w", _i32),
-        ("vx_pool", _vp), ("kv_xform", _vp),
+        ("vx_pool", _vp), ("kv_xform", _vp), ("workspace", _vp), ("workspace_bytes", _i64),
     ]
 
 
@@ -63,6 +63,16 @@ class AttentionDesc(ctypes.Structure):
         ("q_inv_rms", _vp), ("q_rms_stride_b", _i64), ("q_norm_weight", _vp),
         ("rope_hw", _vp), ("grid_h", _i32), ("grid_w", _i32), ("rope_t", _vp), ("n_qframes", _i32),
         ("q_xform_t", _vp), ("q_xform_s", _vp), ("out_xform", _vp), ("frame_lens", _i32p),
+        ("workspace", _vp), ("workspace_bytes", _i64),
+    ]
+
+
+class LaunchPlan(ctypes.Structure):
+    """``skv_launch_plan`` (include/solarkv.h): the launch skv_attention_ex would make."""
+
+    _fields_ = [
+        ("waves_per_group", _i32), ("split", _i32), ("n_workgroups", _i32), ("n_qtiles", _i32),
+        ("workspace_bytes", _i64),
     ]
 
 
@@ -111,6 +121,8 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "skv_append_ex": (_i32, [ctypes.POINTER(AppendDesc), _vp]),
     "skv_attention_ex": (_i32, [ctypes.POINTER(AttentionDesc), _vp]),
+    "skv_attention_plan": (_i32, [ctypes.POINTER(AttentionDesc), ctypes.POINTER(LaunchPlan)]),
+    "skv_append_workspace_size": (_i32, [ctypes.POINTER(AppendDesc), ctypes.POINTER(_i64)]),
 }
 
 _lock = threading.Lock()

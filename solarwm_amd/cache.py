@@ -23,11 +23,13 @@ from __future__ import annotations
 
 from collections.abc import Mapping
 from dataclasses import dataclass
+from types import MappingProxyType
 from typing import Any, Iterator, Sequence
 
 import torch
 
 from . import kernels
+from ._readonly import WRITE_HINT, CacheWriteError, readonly
 from .prope import CameraCache, PropeConfig
 from .rope import RopeConfig, RopeTables
 
@@ -340,13 +342,25 @@ class SlotKVCache(Mapping):
 
     With ``camera`` (one ``CameraCache`` shared by every layer of a model, fused PRoPE) ``krpool``
     also carries each frame's P⁻¹ on its spatial channel groups once a camera pass wrote it, and
-    ``vrpool`` holds P⁻¹ v; layer 0 answers the reference's ``"_fused_prope_camera_metadata"``
-    key (``{"viewmats": [B, cache_tokens, 4, 4], "K": [B, cache_tokens, 3, 3]}``).
+    ``vrpool`` holds P⁻¹ v.
+
+    The first layer (``first_layer=True``) answers the reference's
+    ``"_fused_prope_camera_metadata"`` key from allocation on, as the reference allocator
+    preallocates it (stage2.py:1799-1816) and the drivers require it (stage2.py:466-469,
+    :671-672): ``{"viewmats": [B, cache_tokens, 4, 4], "K": [B, cache_tokens, 3, 3]}`` float32,
+    the camera store's rows through the slot table (zeros without a camera store).
+    ``pop("_fused_prope_camera_metadata")`` drops it as the reference does after a commit made
+    without cameras (causal_model.py:2838-2842); a later camera pass recreates it.
+
+    Every tensor the dict hands out is a read-only snapshot: in-place writes through it (the
+    reference's ``.fill_`` of the indices, slice assignment into ``k``/``v``, ``.copy_`` of the
+    camera metadata) raise ``CacheWriteError``, as do ``cache[key] = ...`` and ``del``; the
+    cache changes only through ``attend_cached`` / ``apply_cache_updates`` and the camera calls.
     """
 
     def __init__(self, geom: CacheGeometry, *, dtype: torch.dtype, device: torch.device | str,
                  rope: RopeTables | None = None, camera: CameraCache | None = None,
-                 camera_owner: bool = False):
+                 first_layer: bool = False):
         self.geom = geom
         self.dtype = dtype
         self.device = torch.device(device)
@@ -363,7 +377,9 @@ class SlotKVCache(Mapping):
                 raise ValueError(f"RoPE grid {gh}x{gw} does not tile {geom.frame_tokens}-token frames")
             self.krpool = torch.zeros_like(self.kpool)
         self.camera = camera
-        self.camera_owner = camera_owner
+        self.first_layer = first_layer
+        self.camera_owner = first_layer and camera is not None
+        self.metadata_present = first_layer  # preallocated like stage2.py:1799-1816
         self.vrpool = None
         if camera is not None:
             if rope is None:
@@ -384,6 +400,7 @@ class SlotKVCache(Mapping):
             self.vrpool.zero_()
         if self.camera is not None and self.camera_owner:
             self.camera.reset()
+        self.metadata_present = self.first_layer
         if self.kscale is not None:
             self.kscale.zero_()
             self.vscale.zero_()
@@ -437,19 +454,34 @@ class SlotKVCache(Mapping):
         return {"viewmats": view.repeat_interleave(T, dim=1), "K": ks.repeat_interleave(T, dim=1)}
 
     def _has_camera_key(self) -> bool:
-        return self.camera is not None and self.camera_owner and self.camera.active
+        return self.first_layer and self.metadata_present
+
+    def _camera_metadata_view(self) -> Mapping[str, torch.Tensor]:
+        if self.camera is not None:
+            meta = self.camera_metadata()
+        else:
+            g = self.geom
+            meta = {
+                "viewmats": torch.zeros(g.batch, g.cache_tokens, 4, 4, dtype=torch.float32,
+                                        device=self.device),
+                "K": torch.zeros(g.batch, g.cache_tokens, 3, 3, dtype=torch.float32,
+                                 device=self.device),
+            }
+        return MappingProxyType({
+            name: readonly(t, f"_fused_prope_camera_metadata[{name!r}]") for name, t in meta.items()
+        })
 
     def __getitem__(self, key: str) -> Any:
         if key == "_fused_prope_camera_metadata" and self._has_camera_key():
-            return self.camera_metadata()
+            return self._camera_metadata_view()
         if key == "k":
-            return self.logical_kv()[0]
+            return readonly(self.logical_kv()[0], "cache['k']")
         if key == "v":
-            return self.logical_kv()[1]
+            return readonly(self.logical_kv()[1], "cache['v']")
         if key == "global_end_index":
-            return torch.tensor([self.global_end], dtype=torch.long)
+            return readonly(torch.tensor([self.global_end], dtype=torch.long), key)
         if key == "local_end_index":
-            return torch.tensor([self.local_end], dtype=torch.long)
+            return readonly(torch.tensor([self.local_end], dtype=torch.long), key)
         raise KeyError(key)
 
     def __iter__(self) -> Iterator[str]:
@@ -460,6 +492,42 @@ class SlotKVCache(Mapping):
 
     def __len__(self) -> int:
         return 5 if self._has_camera_key() else 4
+
+    def pop(self, key: str, *default: Any) -> Any:
+        """Only ``"_fused_prope_camera_metadata"`` can be removed (the reference's drop of stale
+        camera metadata, causal_model.py:2838-2842); it also clears the camera store."""
+        if key == "_fused_prope_camera_metadata":
+            if not self._has_camera_key():
+                if default:
+                    return default[0]
+                raise KeyError(key)
+            value = self._camera_metadata_view()
+            if self.camera is not None:
+                self.camera.reset()
+            self.metadata_present = False
+            return value
+        if key in ("k", "v", "global_end_index", "local_end_index"):
+            raise CacheWriteError(f"pop({key!r}): {WRITE_HINT}")
+        if default:
+            return default[0]
+        raise KeyError(key)
+
+    def __setitem__(self, key: str, value: Any) -> None:
+        raise CacheWriteError(f"cache[{key!r}] = ...: {WRITE_HINT}")
+
+    def __delitem__(self, key: str) -> None:
+        raise CacheWriteError(f"del cache[{key!r}]: {WRITE_HINT}")
+
+    def setdefault(self, key: str, default: Any = None) -> Any:
+        if key in self:
+            return self[key]
+        raise CacheWriteError(f"setdefault({key!r}): {WRITE_HINT}")
+
+    def update(self, *args: Any, **kwargs: Any) -> None:
+        raise CacheWriteError(f"update(): {WRITE_HINT}")
+
+    def clear(self) -> None:
+        raise CacheWriteError(f"clear(): {WRITE_HINT} (reset() returns the cache to its allocated state)")
 
 
 def make_kv_cache_allocator(
@@ -508,6 +576,6 @@ def make_kv_cache_allocator(
             raise ValueError("fused PRoPE needs a pre-RoPE cache: pass rope= as well")
         camera = CameraCache(geom.n_slots, batch_size, device, prope) if prope is not None else None
         return [SlotKVCache(geom, dtype=store, device=device, rope=tables, camera=camera,
-                            camera_owner=(i == 0)) for i in range(num_layers)]
+                            first_layer=(i == 0)) for i in range(num_layers)]
 
     return allocate_kv_cache

@@ -33,7 +33,7 @@
 //   * tiles never straddle frames (frames are padded to 64 tokens); padding keys and keys
 //     beyond a query's chunk-causal limit get -inf, decided per tile: full tiles skip the
 //     mask, tiles past every query's limit are not visited.
-#include <mutex>
+
 #include <math.h>
 
 #include "skv_common.h"
@@ -1319,26 +1319,10 @@ int skv::cu_count() {
   return n;
 }
 
-// Workspace of the split paths (attention records, fp8 append tile maxima), stream-ordered from
-// the device's default memory pool.  The pool keeps freed memory for reuse (release threshold
-// raised once per device), so repeated calls do not map and unmap pages.
-bool skv::stream_workspace(void** p, size_t bytes, hipStream_t s) {
-  static std::mutex mu;
-  static bool tuned[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return false;
-  {
-    std::lock_guard<std::mutex> g(mu);
-    if (dev >= 0 && dev < 64 && !tuned[dev]) {
-      hipMemPool_t pool;
-      if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-        uint64_t keep = UINT64_MAX;
-        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-      }
-      tuned[dev] = true;
-    }
-  }
-  return hipMallocAsync(p, bytes, s) == hipSuccess;
+// Bytes of the balanced split's records: 2 per workgroup (one per partial segment) of kSplitBQ
+// rows, each row 128 O floats plus the running max and sum.
+static int64_t split_workspace_bytes(int n_wg) {
+  return (int64_t)2 * n_wg * kSplitBQ * (kHeadDim + 2) * (int64_t)sizeof(float);
 }
 
 template <int NW>
@@ -1418,7 +1402,8 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
                           const float* pq_s, const float* pq_o, skv_stream_t stream,
                           const float* q_inv_rms = nullptr, int64_t q_rms_sb = 0,
                           const float* q_norm_weight = nullptr,
-                          const int32_t* frame_lens = nullptr) {
+                          const int32_t* frame_lens = nullptr, void* workspace = nullptr,
+                          int64_t workspace_bytes = 0, skv_launch_plan* plan = nullptr) {
   if (!q || !k_pool || !v_pool || !frame_slots || !out) {
     set_error("skv_attention: null pointer argument");
     return SKV_E_ARG;
@@ -1505,7 +1490,15 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
       return SKV_E_ARG;
     }
   }
-  if (q_len == 0) return SKV_OK;
+  if (workspace_bytes < 0 || (workspace == nullptr && workspace_bytes != 0)) {
+    set_error("skv_attention_ex: workspace_bytes=%lld without a workspace pointer",
+              (long long)workspace_bytes);
+    return SKV_E_ARG;
+  }
+  if (q_len == 0) {
+    if (plan) *plan = skv_launch_plan{0, 0, 0, 0, 0};
+    return SKV_OK;
+  }
   AttnArgs a;
   a.rope_hw = rope_hw;
   a.rope_t = rope_t;
@@ -1563,6 +1556,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   a.split = 0;
   a.units = 0;
   a.part_o = a.part_ml = nullptr;
+  int64_t split_bytes = 0;
   const int nt = n_frames * a.ntiles_f;
   const int64_t qt8 = (int64_t)((q_len + kSplitBQ - 1) / kSplitBQ) * heads * batch;
   const int64_t units8 = qt8 * nt;
@@ -1574,13 +1568,25 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     };
     const double t_plain = nw == 8 ? t_grid(a.n_wg, 1, 1.0) : t_grid(a.n_wg, 2, 1.10);
     const double t_split = ((double)units8 / n_cu + 3.0) * t_tile(n_cu);
-    if (t_split < (nw == 8 ? 0.85 : 0.97) * t_plain) {
-      nw = 8;
-      a.split = 1;
-      a.n_qtiles = (int)(qt8 / ((int64_t)heads * batch));
-      a.n_wg = n_cu;
-      a.units = units8;
+    if (t_split < (nw == 8 ? 0.85 : 0.97) * t_plain) split_bytes = split_workspace_bytes(n_cu);
+  }
+  // The split needs the caller's workspace (2 records of kSplitBQ rows x (O, max, sum) per
+  // workgroup); without one the launch stays unsplit.  The library never allocates.
+  if (split_bytes > 0 && workspace != nullptr) {
+    if (workspace_bytes < split_bytes) {
+      set_error("skv_attention_ex: workspace of %lld bytes is smaller than the %lld this launch "
+                "needs (skv_attention_plan)", (long long)workspace_bytes, (long long)split_bytes);
+      return SKV_E_ARG;
     }
+    if (reinterpret_cast<uintptr_t>(workspace) % 16) {
+      set_error("skv_attention_ex: workspace must be 16-byte aligned");
+      return SKV_E_ARG;
+    }
+    nw = 8;
+    a.split = 1;
+    a.n_qtiles = (int)(qt8 / ((int64_t)heads * batch));
+    a.n_wg = n_cu;
+    a.units = units8;
   }
   a.slot_stride = (int64_t)batch * heads * a.Tp * kHeadDim;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
@@ -1611,17 +1617,16 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     set_error("skv_attention_ex: the chunk-causal mask needs whole frames (no frame_lens)");
     return SKV_E_UNSUPPORTED;
   }
+  if (plan) {
+    *plan = skv_launch_plan{nw, a.split, a.n_wg, a.n_qtiles * heads * batch, split_bytes};
+    return SKV_OK;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rm = prope ? 2 : rope ? 1 : 0;
-  void* ws = nullptr;
   if (a.split) {
-    // stream-ordered workspace: 2 records per workgroup (O, then max and sum)
+    // 2 records per workgroup: O rows first, then (max, sum) pairs
     const size_t rec_rows = (size_t)2 * a.n_wg * kSplitBQ;
-    if (!stream_workspace(&ws, rec_rows * (kHeadDim + 2) * sizeof(float), s)) {
-      set_error("skv_attention: workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
-      return SKV_E_LAUNCH;
-    }
-    a.part_o = static_cast<float*>(ws);
+    a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + rec_rows * kHeadDim;
   }
   if (nw == 8)
@@ -1634,7 +1639,6 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
       hipLaunchKernelGGL((attn_combine_kernel<bf16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, a);
     else
       hipLaunchKernelGGL((attn_combine_kernel<float>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, a);
-    (void)hipFreeAsync(ws, s);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -1703,7 +1707,8 @@ extern "C" int skv_attention_prope(const void* q, int q_dtype, int64_t q_sb, int
                         q_xform_s, out_xform, stream);
 }
 
-extern "C" int skv_attention_ex(const skv_attention_desc* d, skv_stream_t stream) {
+static int attention_desc(const skv_attention_desc* d, skv_stream_t stream,
+                          skv_launch_plan* plan) {
   clear_error();
   if (!d) {
     set_error("skv_attention_ex: null descriptor");
@@ -1723,5 +1728,19 @@ extern "C" int skv_attention_ex(const skv_attention_desc* d, skv_stream_t stream
                         d->softmax_scale, d->mask_mode, d->q_pos0, d->chunk_tokens, d->out,
                         d->out_sb, d->out_st, d->out_sh, d->rope_hw, d->grid_h, d->grid_w,
                         d->rope_t, d->n_qframes, d->q_xform_t, d->q_xform_s, d->out_xform, stream,
-                        d->q_inv_rms, d->q_rms_stride_b, d->q_norm_weight, d->frame_lens);
+                        d->q_inv_rms, d->q_rms_stride_b, d->q_norm_weight, d->frame_lens,
+                        d->workspace, d->workspace_bytes, plan);
+}
+
+extern "C" int skv_attention_ex(const skv_attention_desc* d, skv_stream_t stream) {
+  return attention_desc(d, stream, nullptr);
+}
+
+extern "C" int skv_attention_plan(const skv_attention_desc* d, skv_launch_plan* plan) {
+  if (!plan) {
+    clear_error();
+    set_error("skv_attention_plan: null plan");
+    return SKV_E_ARG;
+  }
+  return attention_desc(d, nullptr, plan);
 }

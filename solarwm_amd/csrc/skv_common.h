@@ -28,9 +28,6 @@ void clear_error();
 
 // ---- host launch helpers (defined in skv_attention.hip) -----------------------------------
 int cu_count();  // compute units of the current device (256 on MI355X)
-// Scratch memory ordered on stream s (hipMallocAsync from the device's default pool); the
-// caller releases it with hipFreeAsync on the same stream.
-bool stream_workspace(void** p, size_t bytes, hipStream_t s);
 
 // ---- element traits ---------------------------------------------------------------------
 // A "vec8" is 8 consecutive elements of one row; all pool and token layouts keep them

@@ -749,7 +749,9 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
                        const float* rope_hw, int grid_h, int grid_w, void* vr_pool,
                        const float* kv_xform, skv_stream_t stream,
                        const float* k_inv_rms = nullptr, int64_t rms_sb = 0,
-                       const float* k_norm_weight = nullptr) {
+                       const float* k_norm_weight = nullptr, void* workspace = nullptr,
+                       int64_t workspace_bytes = 0, int64_t* ws_query = nullptr) {
+  if (ws_query) *ws_query = 0;
   if (!k_new || !v_new || !k_pool || !v_pool || !dst_slots) {
     set_error("skv_append: null pointer argument");
     return SKV_E_ARG;
@@ -762,6 +764,11 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
       frame_tokens <= 0 || n_slots <= 0 || src_frame0 < 0) {
     set_error("skv_append: bad sizes (n_frames=%d batch=%d heads=%d T=%d n_slots=%d frame0=%d)",
               n_frames, batch, heads, frame_tokens, n_slots, src_frame0);
+    return SKV_E_ARG;
+  }
+  if (workspace_bytes < 0 || (workspace == nullptr && workspace_bytes != 0)) {
+    set_error("skv_append_ex: workspace_bytes=%lld without a workspace pointer",
+              (long long)workspace_bytes);
     return SKV_E_ARG;
   }
   if (n_frames == 0) return SKV_OK;
@@ -845,16 +852,33 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
     }
     a.slots[f] = dst_slots[f];
   }
+  // fp8 chunks with too few (frame, batch, head, K|V) units to fill the chip split them into
+  // 64-token tiles; the tile maxima live in the caller's workspace (one float per tile).
+  const int units = n_frames * batch * heads * 2;
+  const int64_t tile_bytes = fp8 && units < 4 * cu_count()
+                                 ? (int64_t)units * a.ntiles * (int64_t)sizeof(float) : 0;
+  if (ws_query) {
+    *ws_query = tile_bytes;
+    return SKV_OK;
+  }
+  bool tile_split = false;
+  if (tile_bytes > 0 && workspace != nullptr) {
+    if (workspace_bytes < tile_bytes) {
+      set_error("skv_append_ex: workspace of %lld bytes is smaller than the %lld this fp8 append "
+                "needs (skv_append_workspace_size)", (long long)workspace_bytes,
+                (long long)tile_bytes);
+      return SKV_E_ARG;
+    }
+    if (reinterpret_cast<uintptr_t>(workspace) % 4) {
+      set_error("skv_append_ex: workspace must be 4-byte aligned");
+      return SKV_E_ARG;
+    }
+    tile_split = true;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fp8) {
-    const int units = n_frames * batch * heads * 2;
-    if (units < 4 * cu_count()) {  // too few units to fill the chip: split them into tiles
-      void* ws = nullptr;
-      if (!stream_workspace(&ws, (size_t)units * a.ntiles * sizeof(float), s)) {
-        set_error("skv_append: workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
-        return SKV_E_LAUNCH;
-      }
-      float* part = static_cast<float*>(ws);
+    if (tile_split) {
+      float* part = static_cast<float*>(workspace);
       dim3 tgrid(units * a.ntiles);
       if (src_dtype == SKV_BF16) {
         hipLaunchKernelGGL(fp8_tile_absmax_kernel<bf16>, tgrid, dim3(256), 0, s, a, part);
@@ -863,7 +887,6 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
         hipLaunchKernelGGL(fp8_tile_absmax_kernel<float>, tgrid, dim3(256), 0, s, a, part);
         hipLaunchKernelGGL(append_fp8_tile_kernel<float>, tgrid, dim3(256), 0, s, a, part);
       }
-      (void)hipFreeAsync(ws, s);
     } else {
       dim3 grid(units);
       const bool reg_path = src_dtype == SKV_BF16 && a.ntiles <= kFp8OnChip &&
@@ -946,7 +969,7 @@ extern "C" int skv_append_prope(const void* k_new, const void* v_new, int src_dt
                      stream);
 }
 
-extern "C" int skv_append_ex(const skv_append_desc* d, skv_stream_t stream) {
+static int append_desc(const skv_append_desc* d, skv_stream_t stream, int64_t* ws_query) {
   clear_error();
   if (!d) {
     set_error("skv_append_ex: null descriptor");
@@ -960,7 +983,21 @@ extern "C" int skv_append_ex(const skv_append_desc* d, skv_stream_t stream) {
                      d->src_frame0, d->k_pool, d->v_pool, d->k_scale, d->v_scale, d->pool_dtype,
                      d->n_slots, d->dst_slots, d->n_frames, d->batch, d->heads, d->head_dim,
                      d->frame_tokens, d->kr_pool, d->rope_hw, d->grid_h, d->grid_w, d->vx_pool,
-                     d->kv_xform, stream, d->k_inv_rms, d->k_rms_stride_b, d->k_norm_weight);
+                     d->kv_xform, stream, d->k_inv_rms, d->k_rms_stride_b, d->k_norm_weight,
+                     d->workspace, d->workspace_bytes, ws_query);
+}
+
+extern "C" int skv_append_ex(const skv_append_desc* d, skv_stream_t stream) {
+  return append_desc(d, stream, nullptr);
+}
+
+extern "C" int skv_append_workspace_size(const skv_append_desc* d, int64_t* bytes) {
+  if (!bytes) {
+    clear_error();
+    set_error("skv_append_workspace_size: null bytes");
+    return SKV_E_ARG;
+  }
+  return append_desc(d, nullptr, bytes);
 }
 
 extern "C" int skv_rms_rows(const void* x, int dtype, int64_t sb, int64_t st, int64_t sh,

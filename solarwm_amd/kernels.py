@@ -204,6 +204,24 @@ def _norm_args(name: str, norm, batch: int, rows: int, heads: int, device):
     return inv.data_ptr(), inv.stride(0), w.data_ptr()
 
 
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> tuple[int, int]:
+    """(pointer, bytes) of this device and current stream's scratch tensor, grown to at least
+    ``nbytes``.  The kernels' split paths keep their partial results there; launches on one
+    stream run in order, so every call on that stream shares it."""
+    if nbytes <= 0:
+        return 0, 0
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           _stream(device))
+    t = _workspaces.get(key)
+    if t is None or t.numel() < nbytes:
+        t = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+        _workspaces[key] = t
+    return t.data_ptr(), t.numel()
+
+
 def prepare_append(
     k_new: torch.Tensor,
     v_new: torch.Tensor,
@@ -221,6 +239,7 @@ def prepare_append(
     vr_pool: torch.Tensor | None = None,
     kv_xform: torch.Tensor | None = None,
     k_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
+    use_workspace: bool = True,
 ):
     """Validate an append once and return a zero-argument launcher that enqueues it on the stream
     current now (repeated launches skip the Python-side checks).
@@ -231,7 +250,9 @@ def prepare_append(
     the P⁻¹ of each written frame's camera) and ``vr_pool`` (shaped like ``vpool``), PRoPE is
     applied too: ``kr_pool`` gets P⁻¹ on its spatial channel groups and ``vr_pool`` gets P⁻¹ v.
     ``k_norm = (inv_rms, weight)`` stores RMS-normalised K (``rms_rows`` of ``k_new`` and the
-    norm's float32 weight); every copy and fp8 code derives from the normalised value."""
+    norm's float32 weight); every copy and fp8 code derives from the normalised value.
+    ``use_workspace=False`` keeps an fp8 append of few units on the per-unit kernels (no
+    scratch); by default it takes the tile-grid kernels with this stream's workspace."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("k_new", k_new)
@@ -251,10 +272,15 @@ def prepare_append(
     ks, vs = _scales(kpool, kscale, vscale)
     slots = _lib.int32_array(dst_slots)
     moved = 2 * n * frame_tokens * b * h * HEAD_DIM * (k_new.element_size() + kpool.element_size())
+    desc = _lib.AppendDesc(
+        k_new=k_new.data_ptr(), v_new=v_new.data_ptr(), src_dtype=dtype_code(k_new.dtype),
+        src_sb=sb, src_st=st, src_sh=sh, src_frame0=src_frame0, k_pool=kpool.data_ptr(),
+        v_pool=vpool.data_ptr(), k_scale=ks, v_scale=vs, pool_dtype=dtype_code(kpool.dtype),
+        n_slots=n_slots, dst_slots=slots, n_frames=n, batch=b, heads=h, head_dim=HEAD_DIM,
+        frame_tokens=frame_tokens)
     if kv_xform is not None or vr_pool is not None:
         if kr_pool is None or vr_pool is None or kv_xform is None:
             raise ValueError("PRoPE append needs kr_pool, vr_pool and kv_xform")
-        _check_rope_hw(kr_pool, kpool, rope_hw, grid_hw, frame_tokens)
         _require_cuda("vr_pool", vr_pool)
         if vr_pool.shape != vpool.shape or vr_pool.dtype != vpool.dtype or not vr_pool.is_contiguous():
             raise ValueError("vr_pool must be a contiguous tensor shaped and typed like the V pool")
@@ -262,58 +288,33 @@ def prepare_append(
         if (kv_xform.dtype != torch.float32 or tuple(kv_xform.shape) != (n, b, 4, 4)
                 or not kv_xform.is_contiguous()):
             raise ValueError(f"kv_xform must be contiguous float32 [{n}, {b}, 4, 4]")
-        fn_name = "skv_append_prope"
-        args = (
-            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
-            kpool.data_ptr(), vpool.data_ptr(), dtype_code(kpool.dtype), n_slots, slots, n, b, h,
-            HEAD_DIM, frame_tokens, kr_pool.data_ptr(), vr_pool.data_ptr(), rope_hw.data_ptr(),
-            grid_hw[0], grid_hw[1], kv_xform.data_ptr(), _stream(kpool.device),
-        )
-        moved += 2 * n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
-    elif kr_pool is None:
-        fn_name = "skv_append"
-        args = (
-            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
-            kpool.data_ptr(), vpool.data_ptr(), ks, vs, dtype_code(kpool.dtype), n_slots, slots,
-            n, b, h, HEAD_DIM, frame_tokens, _stream(kpool.device),
-        )
-    else:
+        desc.vx_pool, desc.kv_xform = vr_pool.data_ptr(), kv_xform.data_ptr()
+        moved += n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
+    if kr_pool is not None:
         _check_rope_hw(kr_pool, kpool, rope_hw, grid_hw, frame_tokens)
-        fn_name = "skv_append_rope"
-        args = (
-            k_new.data_ptr(), v_new.data_ptr(), dtype_code(k_new.dtype), sb, st, sh, src_frame0,
-            kpool.data_ptr(), vpool.data_ptr(), dtype_code(kpool.dtype), n_slots, slots, n, b, h,
-            HEAD_DIM, frame_tokens, kr_pool.data_ptr(), rope_hw.data_ptr(), grid_hw[0],
-            grid_hw[1], _stream(kpool.device),
-        )
+        desc.kr_pool, desc.rope_hw = kr_pool.data_ptr(), rope_hw.data_ptr()
+        desc.grid_h, desc.grid_w = int(grid_hw[0]), int(grid_hw[1])
         moved += n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
     if k_norm is not None:
-        # the same append through the descriptor entry point, with the RMSNorm of K
         rms_p, rms_sb, w_p = _norm_args("k_norm", k_norm, b, (src_frame0 + n) * frame_tokens, h,
                                         kpool.device)
-        desc = _lib.AppendDesc(
-            k_new=k_new.data_ptr(), v_new=v_new.data_ptr(), src_dtype=dtype_code(k_new.dtype),
-            src_sb=sb, src_st=st, src_sh=sh, src_frame0=src_frame0, k_pool=kpool.data_ptr(),
-            v_pool=vpool.data_ptr(), k_scale=ks, v_scale=vs, pool_dtype=dtype_code(kpool.dtype),
-            n_slots=n_slots, dst_slots=slots, n_frames=n, batch=b, heads=h, head_dim=HEAD_DIM,
-            frame_tokens=frame_tokens, k_inv_rms=rms_p, k_rms_stride_b=rms_sb, k_norm_weight=w_p,
-            kr_pool=kr_pool.data_ptr() if kr_pool is not None else None,
-            rope_hw=rope_hw.data_ptr() if kr_pool is not None else None,
-            grid_h=grid_hw[0] if kr_pool is not None else 0,
-            grid_w=grid_hw[1] if kr_pool is not None else 0,
-            vx_pool=vr_pool.data_ptr() if kv_xform is not None else None,
-            kv_xform=kv_xform.data_ptr() if kv_xform is not None else None)
-        fn_name, args = "skv_append_ex", (ctypes.byref(desc), _stream(kpool.device))
-    fn = getattr(lib, fn_name)
+        desc.k_inv_rms, desc.k_rms_stride_b, desc.k_norm_weight = rms_p, rms_sb, w_p
+    if use_workspace and kpool.dtype == torch.float8_e4m3fn:
+        need = ctypes.c_int64(0)
+        _lib.check("skv_append_workspace_size",
+                   lib.skv_append_workspace_size(ctypes.byref(desc), ctypes.byref(need)))
+        desc.workspace, desc.workspace_bytes = workspace(kpool.device, need.value)
+    args = (ctypes.byref(desc), _stream(kpool.device))
+    fn = lib.skv_append_ex
 
     def launch() -> None:
         t0 = _tic("append")
-        _lib.check(fn_name, fn(*args))
+        _lib.check("skv_append_ex", fn(*args))
         _toc("append", t0, moved)
 
     launch.bytes_moved = moved
     launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots, kr_pool, rope_hw, vr_pool,
-                   kv_xform, k_norm, args)
+                   kv_xform, k_norm, desc, args)
     return launch
 
 
@@ -405,6 +406,111 @@ def gather_frames(
     return k_out, v_out
 
 
+def attention_desc(
+    q: torch.Tensor,
+    kpool: torch.Tensor,
+    vpool: torch.Tensor,
+    frame_slots: Sequence[int],
+    *,
+    frame_tokens: int,
+    softmax_scale: float | None = None,
+    kscale: torch.Tensor | None = None,
+    vscale: torch.Tensor | None = None,
+    mask_mode: int = _lib.SKV_MASK_NONE,
+    q_pos0: int = 0,
+    chunk_tokens: int = 0,
+    out: torch.Tensor | None = None,
+    rope: tuple[torch.Tensor, tuple[int, int], torch.Tensor] | None = None,
+    prope: tuple[torch.Tensor, tuple[int, int], torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+    q_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
+    frame_lens: Sequence[int] | None = None,
+) -> tuple[_lib.AttentionDesc, torch.Tensor, tuple]:
+    """Validate an attention launch and return ``(descriptor, out, keep-alive objects)`` for
+    ``skv_attention_ex`` (no workspace set).  Arguments as :func:`attention_frames`."""
+    n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
+    sb, st, sh = _token_major("q", q)
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"q dtype {q.dtype} unsupported (float32 or bfloat16)")
+    if q.shape[0] != b or q.shape[2] != h:
+        raise ValueError(f"q batch/heads {tuple(q.shape)} do not match the pool ({b}, {h})")
+    if q.device != kpool.device:
+        raise ValueError("q and pools must be on the same device")
+    if len(frame_slots) == 0:
+        raise RuntimeError("attention over an empty key window")
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    osb, ost, osh = _token_major("out", out)
+    scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
+    ks, vs = _scales(kpool, kscale, vscale)
+    table = _lib.int32_array(frame_slots)
+    d = _lib.AttentionDesc(
+        q=q.data_ptr(), q_dtype=dtype_code(q.dtype), q_sb=sb, q_st=st, q_sh=sh,
+        k_pool=kpool.data_ptr(), v_pool=vpool.data_ptr(), k_scale=ks, v_scale=vs,
+        pool_dtype=dtype_code(kpool.dtype), n_slots=n_slots, frame_slots=table,
+        n_frames=len(frame_slots), batch=b, heads=h, head_dim=HEAD_DIM, q_len=q.shape[1],
+        frame_tokens=frame_tokens, softmax_scale=scale, mask_mode=mask_mode, q_pos0=q_pos0,
+        chunk_tokens=chunk_tokens, out=out.data_ptr(), out_sb=osb, out_st=ost, out_sh=osh)
+    keep = [table]
+    if q_norm is not None:
+        d.q_inv_rms, d.q_rms_stride_b, d.q_norm_weight = _norm_args("q_norm", q_norm, b, q.shape[1],
+                                                                    h, q.device)
+    if frame_lens is not None:
+        if len(frame_lens) != len(frame_slots):
+            raise ValueError("frame_lens needs one entry per listed frame")
+        flens = _lib.int32_array(frame_lens)
+        d.frame_lens = flens
+        keep.append(flens)
+    nq = q.shape[1] // frame_tokens
+    if rope is not None and prope is not None:
+        raise ValueError("give rope= or prope=, not both")
+    if rope is not None or prope is not None:
+        rhw, ghw = (rope or prope)[0], (rope or prope)[1]
+        _check_rope_hw(kpool, kpool, rhw, ghw, frame_tokens)
+        if q.shape[1] != nq * frame_tokens:
+            raise ValueError(f"RoPE queries must be whole frames (Lq={q.shape[1]})")
+        d.rope_hw, d.grid_h, d.grid_w, d.n_qframes = rhw.data_ptr(), int(ghw[0]), int(ghw[1]), nq
+    if rope is not None:
+        rt = rope[2]
+        _require_cuda("rope_t", rt)
+        if (tuple(rt.shape) != (nq, len(frame_slots), 22, 2) or rt.dtype != torch.float32
+                or not rt.is_contiguous()):
+            raise ValueError(f"rope_t must be contiguous float32 [{nq}, {len(frame_slots)}, 22, 2]"
+                             f", got {rt.dtype} {tuple(rt.shape)}")
+        d.rope_t = rt.data_ptr()
+    if prope is not None:
+        xt, xs, xo = prope[2], prope[3], prope[4]
+        for name, t, shape in (("q_xform_t", xt, (b, len(frame_slots), nq, 11, 4, 4)),
+                               ("q_xform_s", xs, (b, nq, 4, 4)), ("out_xform", xo, (b, nq, 4, 4))):
+            _require_cuda(name, t)
+            if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous float32 {list(shape)}, got "
+                                 f"{t.dtype} {tuple(t.shape)}")
+        d.q_xform_t, d.q_xform_s, d.out_xform = xt.data_ptr(), xs.data_ptr(), xo.data_ptr()
+    return d, out, tuple(keep)
+
+
+def cu_count(device: torch.device) -> int:
+    """Compute units of ``device`` (the split path runs one workgroup per CU)."""
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
+def attention_plan(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
+                   frame_slots: Sequence[int], *, use_workspace: bool = True,
+                   **kw) -> dict[str, int]:
+    """The launch :func:`attention_frames` makes for these arguments (``skv_attention_plan``):
+    ``waves_per_group``, ``split``, ``n_workgroups``, ``n_qtiles``, ``workspace_bytes``."""
+    lib = _lib.load()
+    d, _, keep = attention_desc(q, kpool, vpool, frame_slots, **kw)
+    plan = _lib.LaunchPlan()
+    _lib.check("skv_attention_plan", lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)))
+    if use_workspace and plan.workspace_bytes > 0:
+        d.workspace, d.workspace_bytes = workspace(q.device, plan.workspace_bytes)
+        _lib.check("skv_attention_plan", lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)))
+    return {name: int(getattr(plan, name)) for name, _ in _lib.LaunchPlan._fields_}
+
+
 def attention_frames(
     q: torch.Tensor,
     kpool: torch.Tensor,
@@ -423,6 +529,7 @@ def attention_frames(
     prope: tuple[torch.Tensor, tuple[int, int], torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     q_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
     frame_lens: Sequence[int] | None = None,
+    use_workspace: bool = True,
 ) -> torch.Tensor:
     """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D].
 
@@ -439,119 +546,27 @@ def attention_frames(
     and the norm's float32 weight), before RoPE / PRoPE.
 
     ``frame_lens``: valid keys of each listed frame (``1..frame_tokens``), for windows that mix
-    whole frames with shorter spans; keys past a frame's length are masked (mask NONE only)."""
+    whole frames with shorter spans; keys past a frame's length are masked (mask NONE only).
+
+    Under-filled grids take the balanced key split with this stream's workspace
+    (``use_workspace=False`` keeps them on the unsplit kernel)."""
     lib = _lib.load()
-    n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
-    sb, st, sh = _token_major("q", q)
-    if q.dtype not in (torch.float32, torch.bfloat16):
-        raise ValueError(f"q dtype {q.dtype} unsupported (float32 or bfloat16)")
-    if q.shape[0] != b or q.shape[2] != h:
-        raise ValueError(f"q batch/heads {tuple(q.shape)} do not match the pool ({b}, {h})")
-    if q.device != kpool.device:
-        raise ValueError("q and pools must be on the same device")
-    if len(frame_slots) == 0:
-        raise RuntimeError("attention over an empty key window")
-    if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    if tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype:
-        raise ValueError("out must match q's shape and dtype")
-    osb, ost, osh = _token_major("out", out)
-    scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
-    ks, vs = _scales(kpool, kscale, vscale)
+    d, out, keep = attention_desc(
+        q, kpool, vpool, frame_slots, frame_tokens=frame_tokens, softmax_scale=softmax_scale,
+        kscale=kscale, vscale=vscale, mask_mode=mask_mode, q_pos0=q_pos0,
+        chunk_tokens=chunk_tokens, out=out, rope=rope, prope=prope, q_norm=q_norm,
+        frame_lens=frame_lens)
+    if use_workspace:
+        plan = _lib.LaunchPlan()
+        _lib.check("skv_attention_plan", lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)))
+        if plan.workspace_bytes > 0:
+            d.workspace, d.workspace_bytes = workspace(q.device, plan.workspace_bytes)
     t0 = _tic("attention")
-    if q_norm is not None or frame_lens is not None:
-        rms_p = rms_sb = w_p = None
-        if q_norm is not None:
-            rms_p, rms_sb, w_p = _norm_args("q_norm", q_norm, b, q.shape[1], h, q.device)
-        flens = None
-        if frame_lens is not None:
-            if len(frame_lens) != len(frame_slots):
-                raise ValueError("frame_lens needs one entry per listed frame")
-            flens = _lib.int32_array(frame_lens)
-        d = _lib.AttentionDesc(
-            q=q.data_ptr(), q_dtype=dtype_code(q.dtype), q_sb=sb, q_st=st, q_sh=sh,
-            k_pool=kpool.data_ptr(), v_pool=vpool.data_ptr(), k_scale=ks, v_scale=vs,
-            pool_dtype=dtype_code(kpool.dtype), n_slots=n_slots,
-            frame_slots=_lib.int32_array(frame_slots), n_frames=len(frame_slots), batch=b, heads=h,
-            head_dim=HEAD_DIM, q_len=q.shape[1], frame_tokens=frame_tokens, softmax_scale=scale,
-            mask_mode=mask_mode, q_pos0=q_pos0, chunk_tokens=chunk_tokens, out=out.data_ptr(),
-            out_sb=osb, out_st=ost, out_sh=osh, q_inv_rms=rms_p, q_rms_stride_b=rms_sb or 0,
-            q_norm_weight=w_p, frame_lens=flens)
-        nq = q.shape[1] // frame_tokens
-        if rope is not None or prope is not None:
-            rhw, ghw = (rope or prope)[0], (rope or prope)[1]
-            _check_rope_hw(kpool, kpool, rhw, ghw, frame_tokens)
-            if q.shape[1] != nq * frame_tokens:
-                raise ValueError(f"RoPE queries must be whole frames (Lq={q.shape[1]})")
-            d.rope_hw, d.grid_h, d.grid_w, d.n_qframes = rhw.data_ptr(), int(ghw[0]), int(ghw[1]), nq
-        if rope is not None:
-            rt = rope[2]
-            if tuple(rt.shape) != (nq, len(frame_slots), 22, 2) or rt.dtype != torch.float32:
-                raise ValueError("rope_t must be float32 [n_qframes, n_frames, 22, 2]")
-            d.rope_t = rt.data_ptr()
-        if prope is not None:
-            xt, xs, xo = prope[2], prope[3], prope[4]
-            for name, t, shape in (("q_xform_t", xt, (b, len(frame_slots), nq, 11, 4, 4)),
-                                   ("q_xform_s", xs, (b, nq, 4, 4)), ("out_xform", xo, (b, nq, 4, 4))):
-                if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
-                    raise ValueError(f"{name} must be contiguous float32 {list(shape)}")
-            d.q_xform_t, d.q_xform_s, d.out_xform = xt.data_ptr(), xs.data_ptr(), xo.data_ptr()
-        _lib.check("skv_attention_ex", lib.skv_attention_ex(ctypes.byref(d), _stream(q.device)))
-    elif prope is not None:
-        rope_hw, grid_hw, xt, xs, xo = prope
-        _check_rope_hw(kpool, kpool, rope_hw, grid_hw, frame_tokens)
-        nq = q.shape[1] // frame_tokens
-        if q.shape[1] != nq * frame_tokens:
-            raise ValueError(f"PRoPE queries must be whole frames (Lq={q.shape[1]})")
-        for name, t, shape in (("q_xform_t", xt, (b, len(frame_slots), nq, 11, 4, 4)),
-                               ("q_xform_s", xs, (b, nq, 4, 4)), ("out_xform", xo, (b, nq, 4, 4))):
-            _require_cuda(name, t)
-            if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
-                raise ValueError(f"{name} must be contiguous float32 {list(shape)}, got "
-                                 f"{t.dtype} {tuple(t.shape)}")
-        _lib.check(
-            "skv_attention_prope",
-            lib.skv_attention_prope(
-                q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(),
-                dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots), len(frame_slots),
-                b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode, q_pos0, chunk_tokens,
-                out.data_ptr(), osb, ost, osh, rope_hw.data_ptr(), int(grid_hw[0]),
-                int(grid_hw[1]), xt.data_ptr(), xs.data_ptr(), xo.data_ptr(), nq,
-                _stream(q.device),
-            ),
-        )
-    elif rope is None:
-        _lib.check(
-            "skv_attention",
-            lib.skv_attention(
-                q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(),
-                ks, vs, dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots),
-                len(frame_slots), b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode,
-                q_pos0, chunk_tokens, out.data_ptr(), osb, ost, osh, _stream(q.device),
-            ),
-        )
-    else:
-        rope_hw, grid_hw, rope_t = rope
-        _check_rope_hw(kpool, kpool, rope_hw, grid_hw, frame_tokens)
-        nq = q.shape[1] // frame_tokens
-        _require_cuda("rope_t", rope_t)
-        if (q.shape[1] != nq * frame_tokens or rope_t.dtype != torch.float32
-                or tuple(rope_t.shape) != (nq, len(frame_slots), 22, 2) or not rope_t.is_contiguous()):
-            raise ValueError(
-                f"rope_t must be contiguous float32 [{nq}, {len(frame_slots)}, 22, 2] and q whole "
-                f"frames (got {tuple(rope_t.shape)}, Lq={q.shape[1]})")
-        _lib.check(
-            "skv_attention_rope",
-            lib.skv_attention_rope(
-                q.data_ptr(), dtype_code(q.dtype), sb, st, sh, kpool.data_ptr(), vpool.data_ptr(),
-                dtype_code(kpool.dtype), n_slots, _lib.int32_array(frame_slots), len(frame_slots),
-                b, h, HEAD_DIM, q.shape[1], frame_tokens, scale, mask_mode, q_pos0, chunk_tokens,
-                out.data_ptr(), osb, ost, osh, rope_hw.data_ptr(), int(grid_hw[0]),
-                int(grid_hw[1]), rope_t.data_ptr(), nq, _stream(q.device),
-            ),
-        )
+    _lib.check("skv_attention_ex", lib.skv_attention_ex(ctypes.byref(d), _stream(q.device)))
     # algorithmic FLOPs: QKᵀ and PV over every key (masking is not discounted)
-    _toc("attention", t0, 4.0 * b * h * q.shape[1] * len(frame_slots) * frame_tokens * HEAD_DIM)
+    _toc("attention", t0, 4.0 * d.batch * d.heads * q.shape[1] * len(frame_slots) * frame_tokens
+         * HEAD_DIM)
+    del keep
     return out
 
 

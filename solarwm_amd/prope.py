@@ -140,7 +140,7 @@ class CameraCache:
         self.viewmats = torch.zeros(n_slots, batch, 4, 4, dtype=torch.float32, device=self.device)
         self.ks = torch.zeros(n_slots, batch, 3, 3, dtype=torch.float32, device=self.device)
         self.p_inv = torch.zeros(n_slots, batch, 4, 4, dtype=torch.float32, device=self.device)
-        self.active = False  # the reference creates its camera state on the first camera pass
+        self.active = False  # no camera-conditioned frame has been written yet
 
     def reset(self) -> None:
         self.viewmats.zero_()
@@ -201,7 +201,8 @@ def stage_camera_cache(kv_cache: Sequence[Any], cam_viewmats: torch.Tensor, cam_
                        frame_tokens=T, per_frame=per_frame, check=check_frame_constant)
     vq = vq.to(device=dev, dtype=torch.float32)
     kq = kq.to(device=dev, dtype=torch.float32)
-    cam.active = True  # the reference creates its camera state here (causal_model.py:2005-2019)
+    cam.active = True  # camera-conditioned frames from here on (causal_model.py:2005-2019)
+    c0.metadata_present = True  # a dropped camera state is recreated (causal_model.py:2008-2011)
     tr = cam.cfg.camera_translation_transform
     p_q, p_q_inv = projection(transform_relative_viewmats(vq, tr), kq)  # [B, nb, 4, 4]
 
@@ -264,6 +265,7 @@ def commit_camera_cache(update: CameraPass | None) -> None:
 
 
 def drop_camera_cache(kv_cache: Sequence[Any]) -> None:
-    """A commit made without cameras drops the camera metadata (causal_model.py:2838-2842)."""
-    if kv_cache and kv_cache[0].camera is not None:
-        kv_cache[0].camera.reset()
+    """A commit made without cameras drops the camera metadata (causal_model.py:2838-2842);
+    the same as ``kv_cache[0].pop("_fused_prope_camera_metadata", None)``."""
+    if kv_cache:
+        kv_cache[0].pop("_fused_prope_camera_metadata", None)

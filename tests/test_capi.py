@@ -144,7 +144,8 @@ def test_prope_argument_errors_do_not_launch():
 
 
 @pytest.mark.parametrize("cname,pyname", [("skv_append_desc", "AppendDesc"),
-                                          ("skv_attention_desc", "AttentionDesc")])
+                                          ("skv_attention_desc", "AttentionDesc"),
+                                          ("skv_launch_plan", "LaunchPlan")])
 def test_descriptor_layout_matches_header(tmp_path, cname, pyname):
     """The ctypes mirrors of the descriptor structs have the C compiler's size and offsets."""
     import shutil
@@ -197,3 +198,84 @@ def test_extended_entry_points_reject_bad_options():
     assert st == _lib.SKV_E_UNSUPPORTED
     st = lib.skv_rms_rows(fake, _lib.SKV_BF16, 8, 8, 8, 1, 4, 1, 128, -1.0, fake, None)
     assert st == _lib.SKV_E_ARG
+
+
+def _attn_desc(B, H, Lq, T, nf, pool=_lib.SKV_BF16, mask=_lib.SKV_MASK_NONE):
+    fake = ctypes.c_void_p(0x1000)
+    slots = _slots(*range(nf))
+    d = _lib.AttentionDesc(q=fake, q_dtype=_lib.SKV_BF16, q_sb=8, q_st=8, q_sh=8, k_pool=fake,
+                           v_pool=fake, pool_dtype=pool, n_slots=nf + 3, frame_slots=slots,
+                           n_frames=nf, batch=B, heads=H, head_dim=128, q_len=Lq, frame_tokens=T,
+                           softmax_scale=0.1, mask_mode=mask, chunk_tokens=Lq, out=fake, out_sb=8,
+                           out_st=8, out_sh=8)
+    if pool == _lib.SKV_FP8_E4M3:
+        d.k_scale = d.v_scale = fake
+    return d, slots
+
+
+def _plan(d):
+    lib = _lib.load()
+    plan = _lib.LaunchPlan()
+    assert lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)) == _lib.SKV_OK
+    return plan
+
+
+SPLIT_BYTES = 2 * 256 * 256 * 130 * 4  # 2 records x 256 rows x (128 O + max + sum) per CU
+
+
+@pytest.mark.parametrize("name,B,H,Lq,T,nf,pool,want", [
+    # the benchmark's launch shapes (256-CU MI355X): (waves per group, split, workgroups)
+    ("c2", 1, 12, 4680, 1560, 21, _lib.SKV_BF16, (8, 0, 228)),
+    ("c3", 1, 24, 2640, 880, 21, _lib.SKV_BF16, (8, 1, 256)),
+    ("c4", 1, 40, 4680, 1560, 29, _lib.SKV_BF16, (8, 0, 760)),
+    ("c5", 4, 12, 4680, 1560, 21, _lib.SKV_FP8_E4M3, (8, 0, 912)),
+    ("one_frame", 1, 12, 1560, 1560, 21, _lib.SKV_BF16, (8, 1, 256)),
+    ("one_frame_fp8", 4, 12, 1560, 1560, 21, _lib.SKV_FP8_E4M3, (8, 1, 256)),
+])
+def test_launch_plans_of_benchmark_shapes(name, B, H, Lq, T, nf, pool, want):
+    """skv_attention_plan reports the launcher's choice without launching (the device count
+    falls back to MI355X's 256 CUs when no GPU is visible); the split is taken only with a
+    workspace of the reported size."""
+    lib = _lib.load()
+    d, _keep = _attn_desc(B, H, Lq, T, nf, pool)
+    bare = _plan(d)
+    assert bare.split == 0 and bare.workspace_bytes == (SPLIT_BYTES if want[1] else 0)
+    if want[1]:
+        d.workspace, d.workspace_bytes = 0x2000, bare.workspace_bytes
+    plan = _plan(d)
+    assert (plan.waves_per_group, plan.split, plan.n_workgroups) == want, name
+    if want[1]:
+        d.workspace_bytes = bare.workspace_bytes - 4
+        assert lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(_lib.LaunchPlan())) == _lib.SKV_E_ARG
+        assert b"smaller" in lib.skv_last_error()
+        d.workspace, d.workspace_bytes = 0x2008, bare.workspace_bytes
+        assert lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(_lib.LaunchPlan())) == _lib.SKV_E_ARG
+        assert b"aligned" in lib.skv_last_error()
+
+
+def test_masked_launches_never_split():
+    d, _keep = _attn_desc(1, 12, 1560, 1560, 21, mask=_lib.SKV_MASK_CHUNK_CAUSAL)
+    d.workspace, d.workspace_bytes = 0x2000, SPLIT_BYTES
+    plan = _plan(d)
+    assert plan.split == 0 and plan.workspace_bytes == 0
+
+
+def test_append_workspace_query():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    slots = _slots(0, 1, 2)
+
+    def need(B, H, T, pool):
+        d = _lib.AppendDesc(k_new=fake, v_new=fake, src_dtype=_lib.SKV_BF16, src_sb=8, src_st=8,
+                            src_sh=8, k_pool=fake, v_pool=fake, k_scale=fake, v_scale=fake,
+                            pool_dtype=pool, n_slots=8, dst_slots=slots, n_frames=3, batch=B,
+                            heads=H, head_dim=128, frame_tokens=T)
+        out = ctypes.c_int64(-1)
+        assert lib.skv_append_workspace_size(ctypes.byref(d), ctypes.byref(out)) == _lib.SKV_OK
+        return out.value
+
+    # C5: 3 frames x 4 streams x 12 heads x (K, V) = 288 units of 25 tiles, one float per tile
+    assert need(4, 12, 1560, _lib.SKV_FP8_E4M3) == 288 * 25 * 4
+    assert need(4, 12, 1560, _lib.SKV_BF16) == 0
+    assert need(16, 24, 1560, _lib.SKV_FP8_E4M3) == 0  # 2304 units fill the chip per unit
+    assert lib.skv_append_workspace_size(None, None) == _lib.SKV_E_ARG

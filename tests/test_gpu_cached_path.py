@@ -178,6 +178,8 @@ def test_fp8_cache_rollout_vs_bf16_oracle(gpu):
             torch.cuda.synchronize()
             rms_v = seen["v"].double().pow(2).mean(dim=1, keepdim=True).sqrt().clamp_min(1e-6)
             e = (x.cpu().double() - want.double()).abs() / rms_v
+            _say(f"fp8 rollout c={c} {policy}: normalised max {float(e.max()):.3e} "
+                 f"mean {float(e.mean()):.3e}")
             assert float(e.max()) <= FP8_NORM_MAX and float(e.mean()) <= FP8_NORM_MEAN, (
                 c, policy, float(e.max()), float(e.mean()))
             if policy == "commit":

@@ -266,12 +266,18 @@ def _outlier_kv(shape, seed):
     return x.to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("B,H,Lq,T,n", [(4, 3, 390, 390, 21), (1, 12, 1170, 390, 6), (2, 1, 37, 1560, 2),
-                                        (1, 24, 2640, 880, 7)])
+@pytest.mark.parametrize("B,H,Lq,T,n", [
+    (4, 3, 390, 390, 21), (1, 12, 1170, 390, 6), (2, 1, 37, 1560, 2), (1, 24, 2640, 880, 7),
+    pytest.param(1, 12, 1170, 390, 3, marks=pytest.mark.skip(
+        reason="quantisation floor: over a 1170-key window the e4m3 cache itself (the "
+               "quantisation-aware oracle, no kernel) is 3.3e-2 max-abs from the bf16 oracle, "
+               "above the 3e-2 bar; tests/test_oracle.py::test_fp8_quantisation_floor_short_window "
+               "measures it and test_fp8_attention_outliers_vs_quantised_oracle bounds the "
+               "kernel's own error")),
+])
 def test_fp8_attention_unit_scale_vs_bf16_oracle(gpu, B, H, Lq, T, n):
     """N(0,1) K/V: the fp8 cache path meets the north-star fp8 bar (stated for the 21-frame
-    config-5 window) against the bf16 oracle; windows here hold 2340 to 8190 keys (a 1170-key
-    window measured 3.9e-2 max-abs: fewer keys make the softmax sharper)."""
+    config-5 window) against the bf16 oracle on windows of 2340 to 8190 keys."""
     _say("fp8 attention unit scale", B, H, Lq, T, n)
     from .helpers import FP8_MAX_ABS, FP8_MEAN_ABS
 
@@ -299,6 +305,7 @@ def assert_fp8_close_normalised(got, q, k, v, T, mask=None):
     got = got.detach().cpu().double()
     assert torch.isfinite(got).all()
     e = (got - want).abs() / rms_v
+    _say(f"fp8 normalised error: max {float(e.max()):.3e} mean {float(e.mean()):.3e}")
     assert float(e.max()) <= FP8_NORM_MAX, f"normalised max error {float(e.max()):.3e}"
     assert float(e.mean()) <= FP8_NORM_MEAN, f"normalised mean error {float(e.mean()):.3e}"
 

@@ -52,10 +52,15 @@ def test_split_vs_oracle(gpu, B, H, Lq, T, n, dtype):
     q = _rand((B, Lq, H, 128), 1, dtype)
     k, v = _rand((B, n * T, H, 128), 2), _rand((B, n * T, H, 128), 3)
     kp, vp, slots = _pools(k, v, T, gpu)
+    plan = kernels.attention_plan(q.to(gpu), kp, vp, slots, frame_tokens=T)
+    assert plan["split"] == 1 and plan["n_workgroups"] == kernels.cu_count(gpu), plan
     out = kernels.attention_frames(q.to(gpu), kp, vp, slots, frame_tokens=T)
+    plain = kernels.attention_frames(q.to(gpu), kp, vp, slots, frame_tokens=T, use_workspace=False)
     torch.cuda.synchronize()
     assert out.dtype == dtype
-    assert_attn_close(out, ref.attention(q, k.to(dtype), v.to(dtype)))
+    want = ref.attention(q, k.to(dtype), v.to(dtype))
+    assert_attn_close(out, want)
+    assert_attn_close(plain, want)
 
 
 def test_split_ragged_frames_with_fully_masked_shares(gpu):
