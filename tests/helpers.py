@@ -6,9 +6,14 @@ import torch
 MAX_ABS, MEAN_ABS = 2e-2, 1e-3
 # Bar for attention over an fp8-e4m3 cache against the bf16-cache oracle (N(0,1) K/V).
 FP8_MAX_ABS, FP8_MEAN_ABS = 3e-2, 3e-3
-# fp8 cache with outlier channels: error against the quantisation-aware oracle divided by each
-# channel's V RMS (e4m3 keeps 3 mantissa bits, so absolute errors scale with the channel).
-FP8_NORM_MAX, FP8_NORM_MEAN = 0.5, 1e-2
+# fp8 cache with outlier channels: error against the quantisation-aware oracle (the cache's e4m3
+# K/V frames and per-row e4m3 queries decoded, float64 softmax) divided by each channel's V RMS
+# (e4m3 keeps 3 mantissa bits, so absolute errors scale with the channel).  What remains is the
+# kernel's own arithmetic, mostly the e4m3 rounding of P: measured on MI355X at most 0.154 max and
+# 6.1e-3 mean over every fp8 GPU test (windows of 2 to 21 frames, the C5 shape included).  One
+# frame decoded with 1.25x or 2x its scale measures 0.31 to 4.5 max (tests/test_oracle.py plants
+# it), so these bars reject a kernel that mixes up frame scales.
+FP8_NORM_MAX, FP8_NORM_MEAN = 0.25, 8e-3
 
 
 def assert_attn_close(got, want, max_abs=MAX_ABS, mean_abs=MEAN_ABS):

@@ -553,9 +553,9 @@ def _scaled_frame(x, T, frame, factor):
                                         (1, 12, 1170, 390, 6), (2, 1, 37, 1560, 2),
                                         (1, 2, 256, 390, 21)])
 def test_fp8_normalised_bars_reject_a_wrong_frame_scale(B, H, Lq, T, n):
-    """A planted mistake in the oracle: one frame's V (or K) decoded with twice its scale.  The
-    normalised error against the correct quantisation-aware oracle must exceed the fp8 bars, so
-    a kernel that mixed up frame scales could not pass the GPU tests."""
+    """Planted mistakes in the oracle: one frame's V decoded with 2x or 1.25x its scale, or its K
+    with 2x.  The normalised error against the correct quantisation-aware oracle must exceed
+    the fp8 bars, so a kernel that mixed up frame scales could not pass the GPU tests."""
     from tests.helpers import FP8_NORM_MAX, FP8_NORM_MEAN
 
     q = _seeded((B, Lq, H, 128), 1)
@@ -565,7 +565,8 @@ def test_fp8_normalised_bars_reject_a_wrong_frame_scale(B, H, Lq, T, n):
     want = ref.attention(qq, kq, vq, round_inputs_to_bf16=False).double()
     rms_v = v.double().pow(2).mean(dim=1, keepdim=True).sqrt()
     frame = n // 2
-    for kk, vv in ((kq, _scaled_frame(vq, T, frame, 2.0)), (_scaled_frame(kq, T, frame, 2.0), vq)):
+    for kk, vv in ((kq, _scaled_frame(vq, T, frame, 2.0)), (_scaled_frame(kq, T, frame, 2.0), vq),
+                   (kq, _scaled_frame(vq, T, frame, 1.25))):
         got = ref.attention(qq, kk, vv, round_inputs_to_bf16=False).double()
         e = (got - want).abs() / rms_v
         assert float(e.max()) > FP8_NORM_MAX or float(e.mean()) > FP8_NORM_MEAN, (
