@@ -312,6 +312,21 @@ typedef struct skv_launch_plan {
 
 int skv_attention_plan(const skv_attention_desc* desc, skv_launch_plan* plan);
 
+/*
+ * skv_attention_ex_noalloc — skv_attention_ex that allocates nothing and takes no workspace:
+ * the balanced key split keeps its partial results in a static device array of
+ * SKV_NOALLOC_SCRATCH_BYTES per GPU (2 records x 256 rows x 130 floats for each of up to 256
+ * CUs), held by every GPU that calls it until the process ends.  desc->workspace must be NULL
+ * and workspace_bytes 0; a launch whose split would need more scratch (a device with more than
+ * 256 CUs) returns SKV_E_UNSUPPORTED.  Results equal skv_attention_ex's with a workspace.  All
+ * calls on one GPU share its array, so calls that overlap on one GPU (different streams) race;
+ * calls on one stream are ordered and safe.  No counterpart in the reference: it exists for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops that
+ * forbid allocation).
+ */
+#define SKV_NOALLOC_SCRATCH_BYTES 68157440
+int skv_attention_ex_noalloc(const skv_attention_desc* desc, skv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,7 @@ SKV_E_LAUNCH = -3
 
 SKV_MAX_APPEND_FRAMES = 64
 SKV_MAX_FRAMES = 256
+SKV_NOALLOC_SCRATCH_BYTES = 68157440
 
 # Every symbol include/solarkv.h declares, with (restype, argtypes).
 _i32, _i64, _f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -122,6 +123,7 @@ SIGNATURES: dict[str, tuple] = {
     "skv_append_ex": (_i32, [ctypes.POINTER(AppendDesc), _vp]),
     "skv_attention_ex": (_i32, [ctypes.POINTER(AttentionDesc), _vp]),
     "skv_attention_plan": (_i32, [ctypes.POINTER(AttentionDesc), ctypes.POINTER(LaunchPlan)]),
+    "skv_attention_ex_noalloc": (_i32, [ctypes.POINTER(AttentionDesc), _vp]),
     "skv_append_workspace_size": (_i32, [ctypes.POINTER(AppendDesc), ctypes.POINTER(_i64)]),
 }
 

@@ -1736,6 +1736,15 @@ extern "C" int skv_attention_ex(const skv_attention_desc* d, skv_stream_t stream
   return attention_desc(d, stream, nullptr);
 }
 
+int skv::attention_with_workspace(const skv_attention_desc* d, void* ws, int64_t ws_bytes,
+                                  skv_stream_t stream, skv_launch_plan* plan) {
+  if (!d) return attention_desc(d, stream, plan);
+  skv_attention_desc local = *d;
+  local.workspace = ws;
+  local.workspace_bytes = ws ? ws_bytes : 0;
+  return attention_desc(&local, stream, plan);
+}
+
 extern "C" int skv_attention_plan(const skv_attention_desc* d, skv_launch_plan* plan) {
   if (!plan) {
     clear_error();

@@ -28,6 +28,10 @@ void clear_error();
 
 // ---- host launch helpers (defined in skv_attention.hip) -----------------------------------
 int cu_count();  // compute units of the current device (256 on MI355X)
+// skv_attention_ex (or, with plan != nullptr, skv_attention_plan) on a copy of `d` whose
+// workspace is (ws, ws_bytes); ws == nullptr means none.  Clears and sets the error state.
+int attention_with_workspace(const skv_attention_desc* d, void* ws, int64_t ws_bytes,
+                             skv_stream_t stream, skv_launch_plan* plan);
 
 // ---- element traits ---------------------------------------------------------------------
 // A "vec8" is 8 consecutive elements of one row; all pool and token layouts keep them
