@@ -824,9 +824,11 @@ void attn_kernel(AttnArgs a) {
 //   * K rows are staged in the order key_perm64(kb, r), which puts key 32 hh + 16 kb + i of the
 //     tile in accumulator register i of lane half hh, so the scores of a lane are already in
 //     P^T's operand order;
-//   * LDS: one 2 KB operand block per (kb, cs) for K and per db for V^T (lane n*32 .. +32),
-//     written by direct buffer->LDS loads: DMA lane i of part p fills operand lane 32 p + i / 2,
-//     bytes 16 (i & 1) .. +16.
+//   * LDS: one 2 KB operand block per (kb, cs) for K and per db for V^T, stored as two 1 KB
+//     halves: half q holds bytes 16 q .. +16 of every operand lane, lane L at 16 L.  Both
+//     ds_read_b128 of an operand then read 64 consecutive 16 B pieces (no bank conflicts; a
+//     lane-contiguous 32 B layout costs a 2-way conflict on every read).  Direct buffer->LDS
+//     loads fill them: DMA lane i of part q writes operand lane i, bytes 16 q .. +16.
 constexpr int kOp8 = 2048;
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
@@ -858,9 +860,10 @@ __device__ inline void mask_tile64(f32x16 (&s)[2], int hh, int tok0, int T, int 
     }
 }
 
+// the lane's 32-byte operand: p = block + 16 * lane (first half), second half 1 KB further
 __device__ inline i32x8 lds_op32(const char* p) {
   const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
-  const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 1024);
   return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
                (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
@@ -1020,14 +1023,14 @@ void attn_fp8_kernel(AttnArgs a) {
 #pragma unroll
   for (int j = 0; j < kDma; ++j) {
     const int c = wu * kDma + j, p = c & 1;
-    if (c < 8) {
+    if (c < 8) {  // operand lane `lane` = (row n, channels cs*64 + 32 hh ..), bytes 16 p ..
       const int blk = c >> 1;
-      stage.goff[j] = (uint32_t)(key_perm64(blk >> 1, lane >> 1) * kHeadDim + (blk & 1) * 64 + 32 * p +
-                           16 * (lane & 1));
+      stage.goff[j] = (uint32_t)(key_perm64(blk >> 1, lane & 31) * kHeadDim + (blk & 1) * 64 +
+                                 32 * (lane >> 5) + 16 * p);
       stage.loff[j] = blk * kOp8 + p * 1024;
-    } else {
+    } else {  // operand lane `lane` = (channel 32 db + n, keys 32 hh ..), bytes 16 p ..
       const int db = (c - 8) >> 1;
-      stage.goff[j] = (uint32_t)((32 * db + (lane >> 1)) * a.Tp + 32 * p + 16 * (lane & 1));
+      stage.goff[j] = (uint32_t)((32 * db + (lane & 31)) * a.Tp + 32 * (lane >> 5) + 16 * p);
       stage.loff[j] = db * kOp8 + p * 1024;
     }
   }
@@ -1040,7 +1043,7 @@ void attn_fp8_kernel(AttnArgs a) {
     sv_max = fmaxf(sv_max, a.vscale[(int64_t)a.slots[j] * a.B * a.H + sc_bh]);
   const float G = sv_max > 0.f ? 110.0f / sv_max : 1.0f;
   const float c2q = a.scale_log2 * q_scale;
-  const int lane32 = lane * 32;
+  const int lane16 = lane * 16;
 
   f32x16 oacc[4];
 #pragma unroll
@@ -1064,7 +1067,7 @@ void attn_fp8_kernel(AttnArgs a) {
       *reinterpret_cast<u32x4*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    qk64(kb_lds(0) + lane32, q8, zero16, sA);
+    qk64(kb_lds(0) + lane16, q8, zero16, sA);
     int tok0, key0, tj;
     if (tile_needs_mask(0, tok0, key0, tj)) mask_tile64(sA, hh, tok0, tj, key0, lim_lane);
     __syncthreads();
@@ -1100,8 +1103,8 @@ void attn_fp8_kernel(AttnArgs a) {
                   i32x8& pb) __attribute__((always_inline)) {
     if (tau + 2 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb));
     if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(cb));
-    const char* kl = kb_lds(cb ^ 1) + lane32;  // K(tau+1)
-    const char* vl = vb_lds(cb ^ 1) + lane32;  // V(tau-1) (zeros on the first iteration)
+    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1)
+    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
 
     // Eight MFMA slots, QK(tau+1) and PV(tau-1) alternating (QK steps in the order (kb, cs) =
     // (0,0), (1,0), (0,1), (1,1), so the two halves of one key block are four slots apart), each
@@ -1186,7 +1189,7 @@ void attn_fp8_kernel(AttnArgs a) {
   }
   // PV(ntau-1)
   auto epilogue = [&](const i32x8& pprev) __attribute__((always_inline)) {
-    const char* vl = vb_lds((ntau - 1) & 1) + lane32;
+    const char* vl = vb_lds((ntau - 1) & 1) + lane16;
 #pragma unroll
     for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
   };
