@@ -130,22 +130,37 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const int64_t src_base = (int64_t)b * a.s_sb + (int64_t)h * a.s_sh +
                            (int64_t)(a.src_frame0 + f) * a.T * a.s_st;
   if (tid < 128) {
-    const E* ks = static_cast<const E*>(a.ksrc);
-    E* kp = static_cast<E*>(a.kpool) + slot * a.slot_stride +
-            ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
-    // 64 rows x 16 vec8 = 1024 vec8, 8 per thread
+    const E* __restrict__ ks = static_cast<const E*>(a.ksrc);
+    E* __restrict__ kp = static_cast<E*>(a.kpool) + slot * a.slot_stride +
+                         ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+    // 64 rows x 16 vec8 = 1024 vec8, 8 per thread.  All eight loads are issued before any store
+    // (rows past T read the frame's last row and are then zeroed, so no load sits behind a
+    // branch): the source is usually cold in HBM, and loads interleaved with stores would wait
+    // for each other's round trips.
+    const int col = (tid & 15) * 8;
+    Vec8<E> kv[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const int c = tid + 128 * r;
-      const int row = c >> 4, col = (c & 15) * 8;
+      const int row = (tid >> 4) + 8 * r;
+      const int srow = min(tok0 + row, a.T - 1);
+      kv[r] = Vec8<E>::load_nt(ks + src_base + (int64_t)srow * a.s_st + col);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int row = (tid >> 4) + 8 * r;
       const bool live = tok0 + row < a.T;
-      Vec8<E> kv = live ? Vec8<E>::load(ks + src_base + (int64_t)(tok0 + row) * a.s_st + col)
-                        : Vec8<E>::zero();
-      if (a.krms && live) norm8(kv, a, b, h, (int64_t)(a.src_frame0 + f) * a.T + tok0 + row, col);
-      kv.store_nt(kp + row * kHeadDim + col);
+      if (!live) kv[r] = Vec8<E>::zero();
+      if (a.krms && live) norm8(kv[r], a, b, h, (int64_t)(a.src_frame0 + f) * a.T + tok0 + row, col);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int row = (tid >> 4) + 8 * r;
+      const bool live = tok0 + row < a.T;
+      Vec8<E> kv_r = kv[r];
+      kv_r.store_nt(kp + row * kHeadDim + col);
       if constexpr (XM > 0) {
         if (live && col + 8 > 2 * kRopeT) {
-          Vec8<float> y = to_f32(kv);
+          Vec8<float> y = to_f32(kv_r);
           rope_spatial8(y, col, tok0 + row, a.gh, a.gw, a.rope_hw);
           if constexpr (XM == 2) {
             const float* m = a.kv_xf + ((int64_t)f * a.B + b) * 16;
@@ -153,16 +168,16 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
             for (int gg = 0; gg < 2; ++gg)
               if (col + 4 * gg >= 2 * kRopeT) xform4(y, gg, m);
           }
-          kv = from_f32<E>(y);
+          kv_r = from_f32<E>(y);
         }
-        kv.store_nt(static_cast<E*>(a.krpool) + (kp - static_cast<E*>(a.kpool)) + row * kHeadDim + col);
+        kv_r.store_nt(static_cast<E*>(a.krpool) + (kp - static_cast<E*>(a.kpool)) + row * kHeadDim + col);
       }
     }
     return;
   }
-  const E* vs = static_cast<const E*>(a.vsrc);
-  E* vp = static_cast<E*>(a.vpool) + slot * a.slot_stride +
-          (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
+  const E* __restrict__ vs = static_cast<const E*>(a.vsrc);
+  E* __restrict__ vp = static_cast<E*>(a.vpool) + slot * a.slot_stride +
+                       (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
   const int i = tid - 128;
   // tokens tb*8.., channels db*8..: each wave instruction covers 128 B of 8 token rows on the
   // read side and 128 B of 8 V^T rows on the write side
@@ -170,11 +185,13 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   if constexpr (sizeof(E) == 2) {
     u32x4 in[8], out[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int tok = tok0 + tb * 8 + r;
-      in[r] = tok < a.T ? *reinterpret_cast<const u32x4*>(vs + src_base + (int64_t)tok * a.s_st + db * 8)
-                        : u32x4{0u, 0u, 0u, 0u};
+    for (int r = 0; r < 8; ++r) {  // unconditional loads (clamped row), zeroed past T
+      const int tok = min(tok0 + tb * 8 + r, a.T - 1);
+      in[r] = ld_nt(vs + src_base + (int64_t)tok * a.s_st + db * 8);
     }
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      if (tok0 + tb * 8 + r >= a.T) in[r] = u32x4{0u, 0u, 0u, 0u};
     transpose8x8_b16(in, out);
 #pragma unroll
     for (int c = 0; c < 8; ++c)
@@ -202,10 +219,12 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     Vec8<E> in[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const int tok = tok0 + tb * 8 + r;
-      in[r] = tok < a.T ? Vec8<E>::load(vs + src_base + (int64_t)tok * a.s_st + db * 8)
-                        : Vec8<E>::zero();
+      const int tok = min(tok0 + tb * 8 + r, a.T - 1);
+      in[r] = Vec8<E>::load_nt(vs + src_base + (int64_t)tok * a.s_st + db * 8);
     }
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      if (tok0 + tb * 8 + r >= a.T) in[r] = Vec8<E>::zero();
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       Vec8<E> o;
@@ -641,21 +660,24 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
   const int tok0 = t * kTile;
   const int64_t obase = (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)f * a.T * a.o_st;
   if (tid < 128) {
-    const E* kp = static_cast<const E*>(a.kpool) + slot * a.slot_stride +
-                  ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
-    E* ko = static_cast<E*>(a.kout) + obase;
+    const E* __restrict__ kp = static_cast<const E*>(a.kpool) + slot * a.slot_stride +
+                               ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
+    E* __restrict__ ko = static_cast<E*>(a.kout) + obase;
+    // every row of a slot (padding included) is readable: all loads first, then the stores
+    const int col = (tid & 15) * 8;
+    Vec8<E> kv[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) kv[r] = Vec8<E>::load_nt(kp + ((tid >> 4) + 8 * r) * kHeadDim + col);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const int c = tid + 128 * r;
-      const int row = c >> 4, col = (c & 15) * 8;
-      if (tok0 + row < a.T)
-        Vec8<E>::load_nt(kp + row * kHeadDim + col).store_nt(ko + (int64_t)(tok0 + row) * a.o_st + col);
+      const int row = (tid >> 4) + 8 * r;
+      if (tok0 + row < a.T) kv[r].store_nt(ko + (int64_t)(tok0 + row) * a.o_st + col);
     }
     return;
   }
-  const E* vp = static_cast<const E*>(a.vpool) + slot * a.slot_stride +
-                (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
-  E* vo = static_cast<E*>(a.vout) + obase;
+  const E* __restrict__ vp = static_cast<const E*>(a.vpool) + slot * a.slot_stride +
+                             (int64_t)(b * a.H + h) * kHeadDim * a.Tp + tok0;
+  E* __restrict__ vo = static_cast<E*>(a.vout) + obase;
   const int i = tid - 128;
   const int tb = i & 7, db = i >> 3;  // tokens tb*8.., channels db*8..
   const int tokb = tok0 + tb * 8;
