@@ -518,8 +518,16 @@ def append_bandwidth(cfg, device, iters=48, min_source_bytes=768 << 20):
     ms = _back_to_back_ms(launch, iters)
     moved = launches[0].bytes_moved
     del kpool, vpool, launches
+    # the same bytes as one plain device copy (torch copy_ of the chunk's K+V bytes from the
+    # same rotating cold sources): what a transfer of this size reaches on this GPU
+    flat = torch.empty(chunk_bytes // 2, dtype=torch.bfloat16, device=device)
+    srcs = [torch.randn(chunk_bytes // 2, generator=g, device=device, dtype=torch.bfloat16)
+            for _ in range(n_src)]
+    it2 = iter(range(1 << 30))
+    copy_ms = _back_to_back_ms(lambda: flat.copy_(srcs[next(it2) % n_src]), iters)
+    del flat, srcs
     torch.cuda.empty_cache()
-    return moved / (ms / 1e3) / 1e9, ms, n_src, n_src * chunk_bytes
+    return moved / (ms / 1e3) / 1e9, ms, n_src, n_src * chunk_bytes, 2 * chunk_bytes / (copy_ms / 1e3) / 1e9
 
 
 def gather_bandwidth(device, iters=24):
@@ -1158,11 +1166,14 @@ def main():
         },
     }
 
-    app_gbps, app_ms, n_src, src_bytes = append_bandwidth(cfg, dev)
+    app_gbps, app_ms, n_src, src_bytes, copy_gbps = append_bandwidth(cfg, dev)
     result["append_gbps"] = round(app_gbps, 1)
     result["append_frac_hbm"] = round(app_gbps / HBM_PEAK_GBPS, 4)
     result["append_avg_launch_us"] = round(app_ms * 1e3, 2)
     result["append_sources"] = f"{n_src} rotating source chunks, {src_bytes / 1e6:.0f} MB (read cold)"
+    result["append_copy_ceiling_gbps"] = round(copy_gbps, 1)
+    result["append_copy_ceiling_note"] = ("torch copy_ of the same K+V bytes from the same cold "
+                                          "sources: the rate a transfer of this size reaches")
     log(f"[bench] append ({cfg['chunk_f']} frames, back to back, {n_src} cold sources): "
         f"{app_gbps:.0f} GB/s, {app_ms * 1e3:.1f} us")
 

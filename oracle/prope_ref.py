@@ -26,6 +26,10 @@ Pinning (tests/test_oracle_prope.py):
 * ``stage_fused_camera_cache`` / ``commit_fused_camera_cache`` — token-labelled cameras follow
   exactly the rows the K/V cache moves (rolling, direct insert, recompute), and the staged
   buffer leaves the committed state untouched until commit.
+* ``prope_branch_forward`` — identity cameras reduce it to the main branch's cached attention
+  with an immediate commit (token-labelled cache contents equal, C1 known answer through it);
+  one camera for every token gives plain cached attention's output; a common world change of
+  all cameras leaves the output unchanged; a ``none`` forward leaves the cache untouched.
 """
 
 from __future__ import annotations
@@ -237,3 +241,38 @@ def fused_prope_attention(q, k, v, *, q_viewmats, q_ks, kv_viewmats, kv_ks, attn
         q, k, v, q_viewmats=q_viewmats, q_ks=q_ks, kv_viewmats=kv_viewmats, kv_ks=kv_ks,
         transform=transform, emulate_bf16=emulate_bf16)
     return out_fn(attn_fn(qo, ko, vo))
+
+
+# ---------------------------------------------------------------------------------------------
+# the PRoPE self-attention branch with its own cache (CausalPropeSelfAttention.forward,
+# causal_model.py:1296-1525; camera_attention_mode "parallel")
+# ---------------------------------------------------------------------------------------------
+def prope_branch_forward(q, k, v, cache: dict[str, Any], *, viewmats, ks, current_start: int,
+                         frame_seqlen: int, sink_size: int, local_attn_size: int,
+                         cache_update_policy: str = "commit_detached", transform: str = "linear",
+                         attn_fn: Callable | None = None, emulate_bf16: bool = False,
+                         sink_recache_after_switch: bool = False) -> torch.Tensor:
+    """One forward of the branch after its projections and norms, over a dense cache dict
+    (``k``, ``v``, ``global_end_index``, ``local_end_index``: the layer's ``prope_*`` entries).
+
+    PRoPE with the chunk's own cameras (``viewmats`` [B, L, 4, 4], ``ks`` [B, L, 3, 3] per token
+    of the chunk; camera_prope.py:34-90) maps q, k, v to Pᵀq, P⁻¹k, P⁻¹v; the transformed K/V go
+    through the cache exactly as the main branch's (the index arithmetic of :1368-1502 is the
+    same as :1028-1133, restated in ``wan_cache_ref.cached_self_attention``); the attention over
+    sink | window (:1480-1505) is mapped back with P.  A non-``none`` policy writes the cache and
+    advances the indices in the same forward (:1428-1451, :1512-1514), i.e. the deferred update
+    of the main branch applied at once."""
+    from oracle import wan_cache_ref as ref
+
+    qo, ko, vo, out_fn = prope_qkv_separate(
+        q, k, v, q_viewmats=viewmats, q_ks=ks, kv_viewmats=viewmats, kv_ks=ks,
+        transform=transform, emulate_bf16=emulate_bf16)
+    dt = cache["k"].dtype
+    x, upd = ref.cached_self_attention(
+        qo.to(dt), ko.to(dt), vo.to(dt), cache, current_start=current_start,
+        frame_seqlen=frame_seqlen, sink_size=sink_size, local_attn_size=local_attn_size,
+        sink_recache_after_switch=sink_recache_after_switch,
+        attn_fn=attn_fn if attn_fn is not None else ref.attention)
+    if cache_update_policy != "none":
+        ref.apply_cache_updates([cache], [(0, upd)])
+    return out_fn(x)

@@ -14,9 +14,13 @@ Public surface (the reference's call signatures, solar/backends/wan22/runtime):
   :func:`attend_cached`)
 * ``norm_q=`` / ``norm_k=`` of :func:`attend_cached` — q/k RMSNorm fused into the kernels
 * :func:`make_crossattn_cache_allocator`, :func:`cross_attend` — the cross-attention K/V cache
+* ``prope_branch=`` of the allocator, :func:`prope_branch_attention` — the cache of the PRoPE
+  self-attention branch (camera_attention_mode "parallel")
+* :mod:`solarwm_amd.driver` — the sampler's pass/commit driver and the block loop
 """
 
-from .attention import apply_cache_updates, attend_cached, attention, chunk_causal_attention
+from .attention import (apply_cache_updates, attend_cached, attention, chunk_causal_attention,
+                        prope_branch_attention)
 from .crossattn import CrossAttnCache, cross_attend, make_crossattn_cache_allocator
 from .cache import CacheGeometry, CachePlan, SlotKVCache, make_kv_cache_allocator, plan_cached_forward
 from .prope import PropeConfig, commit_camera_cache, drop_camera_cache, stage_camera_cache
@@ -39,5 +43,6 @@ __all__ = [
     "make_crossattn_cache_allocator",
     "make_kv_cache_allocator",
     "plan_cached_forward",
+    "prope_branch_attention",
     "stage_camera_cache",
 ]

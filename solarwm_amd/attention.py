@@ -23,7 +23,7 @@ import torch
 
 from . import _lib, kernels
 from .cache import CacheUpdate, SlotKVCache
-from .prope import CameraPass
+from .prope import CameraPass, commit_camera_cache, stage_camera_cache
 from .rope import positions as rope_positions
 
 
@@ -259,6 +259,49 @@ def attend_cached(
     )
     update = kv_cache.stage(plan, temp)
     return x, (plan.current_end, plan.local_end_index, update)
+
+
+def prope_branch_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_cache: SlotKVCache,
+    current_start: int,
+    cam_viewmats: torch.Tensor,
+    cam_K: torch.Tensor,
+    *,
+    cache_update_policy: str = "commit_detached",
+    sink_recache_after_switch: bool = False,
+    per_frame: bool = False,
+    softmax_scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The cache branch of the PRoPE self-attention branch (``CausalPropeSelfAttention.forward``
+    with a ``kv_cache``, causal_model.py:1296-1525), after its projections and q/k RMSNorm.
+
+    ``q``, ``k``, ``v`` [B, Lq, H, D] and the chunk's cameras (per token ``[B, L, 4, 4]`` /
+    ``[B, L, 3, 3]``, current chunk or full trajectory, one camera per latent frame; or per frame
+    with ``per_frame``).  The reference applies PRoPE to the chunk (q -> P_qᵀ q, k, v -> P⁻¹ k,
+    P⁻¹ v with the chunk's own cameras, camera_prope.py:34-90), caches the transformed K/V in the
+    layer's ``prope_k`` / ``prope_v`` with the same index arithmetic as the main cache, attends
+    over sink | window and maps the output back with P_q; a non-``none`` policy commits at once
+    (the branch writes its cache inside its forward, causal_model.py:1428-1451, :1512-1514).
+    Here the layer's branch cache (``prope_branch=`` of the allocator) keeps each frame's camera
+    per slot; the kernels apply P⁻¹ at append and the query-side matrices and P_q inside the
+    attention, with no RoPE.  Returns the output before the branch's ``out_proj``."""
+    br = kv_cache.branch
+    if br is None:
+        raise ValueError("this cache has no PRoPE branch cache (allocate with prope_branch=)")
+    cam = stage_camera_cache([br], cam_viewmats, cam_K, int(current_start), q.shape[1],
+                             sink_recache_after_switch=sink_recache_after_switch,
+                             per_frame=per_frame)
+    x, (current_end, local_end, update) = attend_cached(
+        q, k, v, br, current_start, sink_recache_after_switch=sink_recache_after_switch,
+        softmax_scale=softmax_scale, out=out, camera=cam)
+    if cache_update_policy != "none":
+        br.commit(update, current_end, local_end)
+        commit_camera_cache(cam)
+    return x
 
 
 def apply_cache_updates(

@@ -30,11 +30,13 @@ import torch
 
 from . import kernels
 from ._readonly import WRITE_HINT, CacheWriteError, readonly
-from .prope import CameraCache, PropeConfig
+from .prope import GROUPS_T, CameraCache, PropeConfig
 from .rope import RopeConfig, RopeTables
 
 # causal_model.py:572-574: local_attn_size == -1 means a fixed 39600-token attention budget.
 UNBOUNDED_ATTENTION_TOKENS = 39600
+# the PRoPE self-attention branch's entries of a layer's cache dict (causal_model.py:1675-1681)
+BRANCH_KEYS = ("prope_k", "prope_v", "prope_global_end_index", "prope_local_end_index")
 
 
 @dataclass(frozen=True)
@@ -388,6 +390,9 @@ class SlotKVCache(Mapping):
                 raise ValueError(f"fused PRoPE needs frames of at least {kernels.TILE} tokens")
             self.vrpool = torch.zeros_like(self.vpool)
         self.slots = SlotTable(geom)
+        # the PRoPE self-attention branch's cache of this layer (make_kv_cache_allocator's
+        # prope_branch=): the reference's prope_k / prope_v / prope_*_end_index keys
+        self.branch: SlotKVCache | None = None
 
     def reset(self) -> None:
         """Return to the freshly allocated state (every position reads as zeros)."""
@@ -404,6 +409,8 @@ class SlotKVCache(Mapping):
         if self.kscale is not None:
             self.kscale.zero_()
             self.vscale.zero_()
+        if self.branch is not None:
+            self.branch.reset()
 
     @property
     def global_end(self) -> int:
@@ -453,6 +460,25 @@ class SlotKVCache(Mapping):
         ks = self.camera.ks.index_select(0, idx).transpose(0, 1)
         return {"viewmats": view.repeat_interleave(T, dim=1), "K": ks.repeat_interleave(T, dim=1)}
 
+    def branch_kv(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The PRoPE branch's cache rows as the reference holds them (causal_model.py:1428-1451:
+        P⁻¹ k and P⁻¹ v with each frame's camera), materialised through the branch's slot table:
+        V from its transformed pool, K from its transformed pool with P⁻¹ also applied to the
+        temporal channel groups (the pool keeps those raw for the kernel's per-frame query
+        matrices); fp32 products, one rounding."""
+        br = self.branch
+        T = br.geom.frame_tokens
+        kx, vx = kernels.gather_frames(br.krpool, br.vrpool, br.table, frame_tokens=T)
+        idx = torch.tensor(br.table, dtype=torch.long, device=br.camera.device)
+        p_inv = br.camera.p_inv.index_select(0, idx).transpose(0, 1)  # [B, frames, 4, 4]
+        b, n, h, _ = kx.shape
+        nf = n // T
+        tg = kx[..., : 4 * GROUPS_T].float().reshape(b, nf, T, h, GROUPS_T, 4)
+        tg = torch.einsum("bfij,bfthgj->bfthgi", p_inv, tg).reshape(b, n, h, 4 * GROUPS_T)
+        kx = kx.clone()
+        kx[..., : 4 * GROUPS_T] = tg.to(kx.dtype)
+        return kx, vx
+
     def _has_camera_key(self) -> bool:
         return self.first_layer and self.metadata_present
 
@@ -482,16 +508,26 @@ class SlotKVCache(Mapping):
             return readonly(torch.tensor([self.global_end], dtype=torch.long), key)
         if key == "local_end_index":
             return readonly(torch.tensor([self.local_end], dtype=torch.long), key)
+        if self.branch is not None and key in BRANCH_KEYS:
+            if key == "prope_k":
+                return readonly(self.branch_kv()[0], "cache['prope_k']")
+            if key == "prope_v":
+                return readonly(self.branch_kv()[1], "cache['prope_v']")
+            end = (self.branch.global_end if key == "prope_global_end_index"
+                   else self.branch.local_end)
+            return readonly(torch.tensor([end], dtype=torch.long), key)
         raise KeyError(key)
 
     def __iter__(self) -> Iterator[str]:
         keys = ("k", "v", "global_end_index", "local_end_index")
+        if self.branch is not None:
+            keys += BRANCH_KEYS
         if self._has_camera_key():
             keys += ("_fused_prope_camera_metadata",)
         return iter(keys)
 
     def __len__(self) -> int:
-        return 5 if self._has_camera_key() else 4
+        return len(tuple(iter(self)))
 
     def pop(self, key: str, *default: Any) -> Any:
         """Only ``"_fused_prope_camera_metadata"`` can be removed (the reference's drop of stale
@@ -506,7 +542,8 @@ class SlotKVCache(Mapping):
                 self.camera.reset()
             self.metadata_present = False
             return value
-        if key in ("k", "v", "global_end_index", "local_end_index"):
+        if key in ("k", "v", "global_end_index", "local_end_index") or (
+                self.branch is not None and key in BRANCH_KEYS):
             raise CacheWriteError(f"pop({key!r}): {WRITE_HINT}")
         if default:
             return default[0]
@@ -543,6 +580,7 @@ def make_kv_cache_allocator(
     cache_dtype: torch.dtype | None = None,
     rope: RopeConfig | None = None,
     prope: PropeConfig | None = None,
+    prope_branch: PropeConfig | None = None,
 ):
     """Return ``allocate_kv_cache(batch_size, *, dtype, device) -> list[SlotKVCache]``.
 
@@ -553,7 +591,11 @@ def make_kv_cache_allocator(
     as the reference's cache branch does); its tables are shared by all layers.  ``prope`` (with
     ``rope``) makes the caches camera-aware for the fused PRoPE mode: one camera cache shared by
     all layers (exposed on layer 0, as the reference keeps it), staged per forward with
-    ``prope.stage_camera_cache``.
+    ``prope.stage_camera_cache``.  ``prope_branch`` gives every layer the cache of the PRoPE
+    self-attention branch (``CausalPropeSelfAttention``, camera_attention_mode "parallel",
+    causal_model.py:1238-1525): same geometry, K/V stored with each frame's P⁻¹, its own
+    indices and camera store, exposed as the ``prope_*`` keys and driven by
+    :func:`solarwm_amd.prope_branch_attention` (bf16 caches).
     """
     if local_attn_size <= 0:
         raise ValueError("the slot cache needs a positive local_attn_size (cache frames)")
@@ -575,7 +617,18 @@ def make_kv_cache_allocator(
         if prope is not None and rope is None:
             raise ValueError("fused PRoPE needs a pre-RoPE cache: pass rope= as well")
         camera = CameraCache(geom.n_slots, batch_size, device, prope) if prope is not None else None
-        return [SlotKVCache(geom, dtype=store, device=device, rope=tables, camera=camera,
-                            first_layer=(i == 0)) for i in range(num_layers)]
+        caches = [SlotKVCache(geom, dtype=store, device=device, rope=tables, camera=camera,
+                              first_layer=(i == 0)) for i in range(num_layers)]
+        if prope_branch is not None:
+            if store != torch.bfloat16:
+                raise ValueError(f"the PRoPE branch cache needs bf16, got {store}")
+            ident = RopeTables(RopeConfig(grid_hw=(1, frame_sequence_length), identity=True),
+                               device)
+            for c in caches:
+                c.branch = SlotKVCache(
+                    geom, dtype=store, device=device, rope=ident,
+                    camera=CameraCache(geom.n_slots, batch_size, device, prope_branch),
+                    first_layer=True)
+        return caches
 
     return allocate_kv_cache

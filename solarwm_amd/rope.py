@@ -38,6 +38,9 @@ class RopeConfig:
     rope_train_frames: int | None = None
     theta: float = 10000.0
     table_len: int = 1024  # rope_params(1024, ...)
+    # every angle 0: the kernels' RoPE paths then apply no rotation (the PRoPE self-attention
+    # branch, which has no RoPE, runs on them this way)
+    identity: bool = False
 
     def __post_init__(self):
         gh, gw = self.grid_hw
@@ -57,7 +60,7 @@ def spatial_table(cfg: RopeConfig, device) -> torch.Tensor:
     """float32 [(H + W) * 21 * 2]: cos, sin of h * w_j for h < H, then of w * w_j for w < W
     (the height and width parts use the same 42-dim frequencies)."""
     gh, gw = cfg.grid_hw
-    inv = _inv_freq(2 * SPATIAL_PAIRS, cfg.theta)
+    inv = _inv_freq(2 * SPATIAL_PAIRS, cfg.theta) * (0.0 if cfg.identity else 1.0)
     ang = torch.cat([torch.outer(torch.arange(gh, dtype=torch.float64), inv),
                      torch.outer(torch.arange(gw, dtype=torch.float64), inv)])
     tab = torch.stack([torch.cos(ang), torch.sin(ang)], dim=-1)
@@ -68,7 +71,7 @@ def temporal_table(q_positions: Sequence[int], k_positions: Sequence[int], cfg: 
                    device) -> torch.Tensor:
     """float32 [n_q, n_k, 22, 2]: cos, sin of (q_positions[f] - k_positions[j]) * w_i (the
     44-dim temporal frequencies), computed in float64."""
-    inv = _inv_freq(2 * TEMPORAL_PAIRS, cfg.theta)
+    inv = _inv_freq(2 * TEMPORAL_PAIRS, cfg.theta) * (0.0 if cfg.identity else 1.0)
     d = (torch.tensor(list(q_positions), dtype=torch.float64)[:, None]
          - torch.tensor(list(k_positions), dtype=torch.float64)[None, :])
     ang = d[..., None] * inv
@@ -87,6 +90,8 @@ def positions(cfg: RopeConfig, *, num_sink_frames: int, num_local_frames: int,
     """
     nb, nl = num_new_frames, num_local_frames
     ns = num_sink_frames if sink_branch else 0
+    if cfg.identity:  # no rotation: every position is 0
+        return [0] * nb, [0] * (num_sink_frames + nl)
     pmax = min(max(1, nb, max_attention_size // max(1, frame_tokens)), cfg.table_len)
     if cfg.use_echorope:
         q_last = min(max(0, ns + nl - nb) + nb - 1, pmax - 1)

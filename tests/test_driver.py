@@ -277,3 +277,20 @@ def test_cached_forward_drops_camera_metadata_on_camera_free_commit():
     driver.cached_forward(caches, _plan_only_block(0, 6), cache_update_policy="commit_detached",
                           fused_prope=True)
     assert META not in caches[0]
+
+
+def test_prope_branch_cache_keys_and_writes():
+    from solarwm_amd import PropeConfig
+
+    caches = _alloc(layers=2, T=64, cap=4, chunk=2, prope_branch=PropeConfig())(
+        1, dtype=torch.bfloat16, device="cpu")
+    assert caches[0].branch is not None and caches[1].branch is not caches[0].branch
+    for c in caches:
+        assert {"prope_k", "prope_v", "prope_global_end_index", "prope_local_end_index"} <= set(c)
+        assert int(c["prope_global_end_index"]) == 0 and int(c["prope_local_end_index"]) == 0
+    with pytest.raises(CacheWriteError):
+        caches[1]["prope_local_end_index"].fill_(3)  # causal_model.py:1512-1514
+    with pytest.raises(CacheWriteError):
+        caches[1].pop("prope_k")
+    plain = _alloc(layers=1, T=64, cap=4, chunk=2)(1, dtype=torch.bfloat16, device="cpu")[0]
+    assert "prope_k" not in plain  # the reference block runs the branch cache-free then

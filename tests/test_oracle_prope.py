@@ -230,3 +230,103 @@ def test_camera_cache_rejects_history_without_metadata():
         pr.slice_current_camera_tokens(cam, current_start=5 * T, num_new_tokens=T + 1)
     full = torch.arange(10.0).view(1, 10, 1, 1)
     assert torch.equal(pr.slice_current_camera_tokens(full, current_start=4, num_new_tokens=3), full[:, 4:7])
+
+
+# ---------------------------------------------------------------------------------------------
+# the PRoPE self-attention branch with its own cache (causal_model.py:1296-1525)
+# ---------------------------------------------------------------------------------------------
+def _labelled_chunk(start, n, heads=1):
+    ids = torch.arange(start, start + n, dtype=F64)
+    return ids.view(1, n, 1, 1).expand(1, n, heads, 4).clone()
+
+
+def _frame_ids(k_labels, T):
+    row = k_labels[0, :, 0, 0]
+    return [int(row[f * T]) // T for f in range(row.shape[0] // T)]
+
+
+def test_branch_with_identity_cameras_is_the_main_cache_with_immediate_commit():
+    """Identity cameras: the branch's cache rows are the raw token ids, committed by the branch
+    forward itself; the C1 known answer (390-token frames, chunk 3, 21-frame cache, sink 1,
+    10 chunks x (none, commit)) comes out of its cache."""
+    T, chunk_f, cap_f, sink_f = 390, 3, 21, 1
+    Lq = chunk_f * T
+    cache = ref.allocate_kv_cache(1, 1, cap_f * T, 1, 4, F64)[0]
+    eye = torch.eye(4, dtype=F64).expand(1, Lq, 4, 4)
+    seen = []
+
+    def rec(q, k, v):
+        seen.append(k[0, :, 0, 0].clone())
+        return torch.zeros_like(q)
+
+    for c in range(10):
+        for policy in ("none", "commit_detached"):
+            before = {key: val.clone() for key, val in cache.items()}
+            x = _labelled_chunk(c * Lq, Lq)
+            pr.prope_branch_forward(x, x, x, cache, viewmats=eye, ks=None, current_start=c * Lq,
+                                    frame_seqlen=T, sink_size=sink_f, local_attn_size=cap_f,
+                                    cache_update_policy=policy, attn_fn=rec)
+            if policy == "none":
+                assert all(torch.equal(before[k], cache[k]) for k in before)
+            else:
+                assert int(cache["global_end_index"]) == (c + 1) * Lq
+    lk = [len(s) for s in seen[1::2]]
+    assert lk == [1170, 2340, 3510, 4680, 5850, 7020, 8190, 8190, 8190, 8190]
+    assert _frame_ids(cache["k"], T) == [0] + list(range(10, 30))
+
+
+def _f64_attention(q, k, v):
+    return ref.attention(q, k, v, round_inputs_to_bf16=False)
+
+
+def _branch_rollout(cams_fn, n_chunks=3, T=8, H=2, cap_f=5, sink_f=1, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    Lq = 2 * T
+    cache = ref.allocate_kv_cache(1, 1, cap_f * T, H, 128, F64)[0]
+    outs = []
+    for c in range(n_chunks):
+        q, k, v = (torch.randn(1, Lq, H, 128, generator=g, dtype=F64) for _ in range(3))
+        vm, kk = cams_fn(c, Lq)
+        outs.append(pr.prope_branch_forward(
+            q, k, v, cache, viewmats=vm, ks=kk, current_start=c * Lq, frame_seqlen=T,
+            sink_size=sink_f, local_attn_size=cap_f, attn_fn=_f64_attention))
+    return outs, cache
+
+
+def test_branch_with_one_camera_for_every_token_is_plain_cached_attention():
+    """One camera P for all tokens: (Pᵀq)·(P⁻¹k) = q·k and P Σ p P⁻¹v = Σ p v, so the branch's
+    outputs equal the main branch's cached attention on the raw inputs."""
+    cam = rand_se3(1, 7, t_scale=2.0)
+    kk = intrinsics(1)
+    outs, _ = _branch_rollout(lambda c, L: (cam.expand(1, L, 4, 4), kk.expand(1, L, 3, 3)))
+    g = torch.Generator().manual_seed(0)
+    T, Lq, cache = 8, 16, ref.allocate_kv_cache(1, 1, 40, 2, 128, F64)[0]
+    for c in range(3):
+        q, k, v = (torch.randn(1, Lq, 2, 128, generator=g, dtype=F64) for _ in range(3))
+        want, upd = ref.cached_self_attention(q, k, v, cache, current_start=c * Lq, frame_seqlen=T,
+                                              sink_size=1, local_attn_size=5,
+                                              attn_fn=_f64_attention)
+        ref.apply_cache_updates([cache], [(0, upd)])
+        assert torch.allclose(outs[c], want, atol=1e-10), c
+
+
+def test_branch_is_invariant_to_a_common_world_change():
+    """Scores and outputs depend on relative poses only (linear translation mode): moving every
+    camera by one world transform leaves every output unchanged, while different poses per frame
+    do change them."""
+    poses = rand_se3(16, 11, t_scale=1.5, angle=0.4)
+    world = rand_se3(1, 12, t_scale=3.0)[0]
+    kk = intrinsics(1)
+
+    def cams(moved):
+        def fn(c, L):
+            per_frame = poses[2 * c : 2 * c + 2] @ (world if moved else torch.eye(4, dtype=F64))
+            return per_frame.repeat_interleave(L // 2, dim=0)[None], kk.expand(1, L, 3, 3)
+        return fn
+
+    a, _ = _branch_rollout(cams(False))
+    b, _ = _branch_rollout(cams(True))
+    flat, _ = _branch_rollout(lambda c, L: (torch.eye(4, dtype=F64).expand(1, L, 4, 4), kk.expand(1, L, 3, 3)))
+    for x, y, z in zip(a, b, flat):
+        assert torch.allclose(x, y, atol=1e-9)
+    assert not torch.allclose(a[-1], flat[-1], atol=1e-3)
