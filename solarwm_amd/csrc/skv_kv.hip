@@ -514,13 +514,19 @@ __global__ __launch_bounds__(256) void fp8_tile_absmax_kernel(AppendArgs a, floa
   const bool knorm = !u.is_v && a.krms;
   const int64_t tok0 = (int64_t)(a.src_frame0 + u.f) * a.T + u.t * kTile;
   float m = 0.f;
+  // 64 rows x 16 vec8 = 4 per thread, all loads issued first (rows past T read the last valid
+  // row and are skipped below); plain loads, so the second pass can find the tile in L2/MALL
+  Vec8<E> x[4];
+  const int col = (tid & 15) * 8;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // 64 rows x 16 vec8 = 4 per thread
-    const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 8;
+  for (int i = 0; i < 4; ++i)
+    x[i] = Vec8<E>::load(src + (int64_t)min((tid >> 4) + 16 * i, rows - 1) * a.s_st + col);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (tid >> 4) + 16 * i;
     if (row < rows) {
-      Vec8<E> x = Vec8<E>::load(src + (int64_t)row * a.s_st + col);
-      if (knorm) norm8(x, a, u.b, u.h, tok0 + row, col);
-      m = absval8(x, m);
+      if (knorm) norm8(x[i], a, u.b, u.h, tok0 + row, col);
+      m = absval8(x[i], m);
     }
   }
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
@@ -567,15 +573,19 @@ __global__ __launch_bounds__(256) void append_fp8_tile_kernel(AppendArgs a, cons
   uint8_t* pool = static_cast<uint8_t*>(u.is_v ? a.vpool : a.kpool) + slot * a.slot_stride +
                   (int64_t)(u.b * a.H + u.h) * a.Tp * kHeadDim;
   u32x2 q[4];
+  Vec8<E> x[4];
+  {
+    const int col = (tid & 15) * 8;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 8;
-    Vec8<E> x = Vec8<E>::zero();
-    if (row < rows) {
-      x = Vec8<E>::load_nt(src + (int64_t)row * a.s_st + col);
-      if (knorm) norm8(x, a, u.b, u.h, tok0 + row, col);
+    for (int i = 0; i < 4; ++i)  // all loads first; rows past T become code 0 below
+      x[i] = Vec8<E>::load_nt(src + (int64_t)min((tid >> 4) + 16 * i, rows - 1) * a.s_st + col);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (tid >> 4) + 16 * i;
+      if (row >= rows) x[i] = Vec8<E>::zero();
+      else if (knorm) norm8(x[i], a, u.b, u.h, tok0 + row, col);
+      q[i] = quant_vec8<E>(x[i], inv);
     }
-    q[i] = quant_vec8<E>(x, inv);
   }
   if (!u.is_v) {
 #pragma unroll
