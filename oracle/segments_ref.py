@@ -22,7 +22,6 @@ equals dense attention under the mask built from the same spans.
 
 from __future__ import annotations
 
-from typing import Sequence
 
 import torch
 
@@ -187,6 +186,3 @@ def memory_kv_attention(q, k, v, history_k, history_v, *, text_rows, frame_rows,
         outs.append(attention(q[:, qs:qe], kq, vq, **kw))
     return torch.cat(outs, dim=1)
 
-
-def spans_of(segments: Sequence) -> list[tuple[int, int]]:
-    return [iv for _, _, ivs in segments for iv in ivs]

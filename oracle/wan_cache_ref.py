@@ -15,6 +15,8 @@ Pinning (tests/test_oracle.py):
   committed indices unchanged and see the same window as the chunk's commit pass.
 * ``attention`` — explicit float64 loops of softmax(q kᵀ/√d) v; closed forms (identical keys →
   mean of V; one key → V; key-order invariance).
+* ``sdpa_fallback_attention`` — the same float64 loops within the bf16 attention bars; values
+  paired with the wrong keys fail them.
 * ``inference_window_mask`` / ``block_classes`` — brute-force rule "chunk i sees chunks 0..i"
   and per-block full/partial/empty from the dense mask.
 * ``fp8_quantize`` — every e4m3fn code decoded from sign/exponent/mantissa; each quantised value

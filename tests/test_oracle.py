@@ -231,6 +231,25 @@ def test_attention_matches_explicit_loops():
     assert np.allclose(got, _loops_attention(q, k, v, 0.7, mask), atol=1e-12)
 
 
+def test_sdpa_fallback_matches_float64_attention():
+    """``sdpa_fallback_attention`` (the reference's bf16 SDPA fallback, attention.py:172-188, the
+    timed CPU baseline) against the float64 loops: bf16 out, [B, L, H, D] layout kept, within the
+    bf16 attention bars; values paired with the wrong keys (V in reverse token order) fail them."""
+    from tests.helpers import MAX_ABS, MEAN_ABS
+
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(1, 6, 3, 16, generator=g).bfloat16()
+    k = torch.randn(1, 9, 3, 16, generator=g).bfloat16()
+    v = torch.randn(1, 9, 3, 16, generator=g).bfloat16()
+    got = ref.sdpa_fallback_attention(q, k, v)
+    assert got.dtype == torch.bfloat16 and got.shape == q.shape
+    want = torch.from_numpy(_loops_attention(q.float(), k.float(), v.float(), 16 ** -0.5))
+    err = (got.double() - want).abs()
+    assert float(err.max()) <= MAX_ABS and float(err.mean()) <= MEAN_ABS
+    wrong = torch.from_numpy(_loops_attention(q.float(), k.float(), v.float().flip(1), 16 ** -0.5))
+    assert float((got.double() - wrong).abs().max()) > MAX_ABS
+
+
 def test_attention_closed_forms():
     g = torch.Generator().manual_seed(1)
     q = torch.randn(2, 7, 3, 16, generator=g)
