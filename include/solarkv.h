@@ -304,8 +304,11 @@ int skv_attention_ex(const skv_attention_desc* desc, skv_stream_t stream);
  */
 typedef struct skv_launch_plan {
   int waves_per_group;     /* 8 (256 queries per workgroup) or 4 (128) */
-  int split;               /* 1: balanced key split over one workgroup per CU + merge kernel */
-  int n_workgroups;        /* workgroups of the main kernel */
+  int split;               /* 0: none; 1: balanced key split of every query tile over one
+                              workgroup per CU + merge kernel; 2: the grid's full rounds run
+                              unsplit and only the last, partly filled round's query tiles
+                              are split over the CUs (+ merge kernel) */
+  int n_workgroups;        /* workgroups of the attention kernel launches (both, for split 2) */
   int n_qtiles;            /* query tiles (over all batches and heads) */
   int64_t workspace_bytes; /* workspace the split needs; 0 when it does not pay */
 } skv_launch_plan;

@@ -87,6 +87,9 @@ struct AttnArgs {
   // merges the records of each split q-tile.
   int split;
   int64_t units;
+  // q-tile (in (b, h)-major order) that unit 0 / workgroup 0 of this grid starts at: 0, except
+  // for the tail launch of a grid whose last round is split (the full rounds run unsplit first)
+  int qt_base;
   float* part_o;   // [2*n_wg][256][128] unnormalised O
   float* part_ml;  // [2*n_wg][256][2] (running max in log2 units, row sum)
 };
@@ -323,8 +326,8 @@ void attn_kernel(AttnArgs a) {
     if (seg == nseg - 1) te = (int)(u1 - (int64_t)qg * nt);
   }
   if (k > 0) __syncthreads();  // the previous segment's last LDS reads are done
-  const int qt = qg % a.n_qtiles;
-  const int bh = qg / a.n_qtiles;
+  const int qt = (qg + a.qt_base) % a.n_qtiles;
+  const int bh = (qg + a.qt_base) / a.n_qtiles;
   const int h = bh % a.H, b = bh / a.H;
 
   // SPLIT: an opaque copy per segment, so lane-derived values are recomputed here instead of
@@ -868,6 +871,17 @@ __device__ inline i32x8 lds_op32(const char* p) {
                (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
+// max(a, b, c) without the IEEE quieting of the inputs (no input is a signalling NaN)
+__device__ inline float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ inline float pair_max_raw(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max3_raw(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
+}
+
 __device__ inline f32x16 mfma64(const i32x8& a, const i32x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
@@ -932,8 +946,8 @@ void attn_fp8_kernel(AttnArgs a) {
     if (seg == nseg - 1) te = (int)(u1 - (int64_t)qg * nt);
   }
   if (k > 0) __syncthreads();  // the previous segment's last LDS reads are done
-  const int qt = qg % a.n_qtiles;
-  const int bh = qg / a.n_qtiles;
+  const int qt = (qg + a.qt_base) % a.n_qtiles;
+  const int bh = (qg + a.qt_base) / a.n_qtiles;
   const int h = bh % a.H, b = bh / a.H;
   // SPLIT: an opaque copy per segment keeps lane-derived values out of the segment loop's
   // live range
@@ -1130,16 +1144,21 @@ void attn_fp8_kernel(AttnArgs a) {
         oacc[i >> 1] = mfma64(op[i & 3], pprev, oacc[i >> 1]);
       }
       if (i == 0) {  // the tile's max, the running max and the exponent bias
-        // four independent chains, so the max is not one 16-deep dependency before the MFMAs
-        float mq[4];
+        // two independent chains of 3-input maxima (8 each), so the max is not one 16-deep
+        // dependency before the MFMAs.  Inline asm: fmaxf would first quiet every score with a
+        // v_max_f32 x, x (IEEE maxnum), 11 more instructions per tile; MFMA results are never
+        // signalling NaNs.
+        float mq[2];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          mq[c] = s_cur[c >> 1][(c & 1) * 8];
+        for (int c = 0; c < 2; ++c) {
+          const f32x16& sc = s_cur[c];
+          mq[c] = max3_raw(sc[0], sc[1], sc[2]);
 #pragma unroll
-          for (int r = 1; r < 8; ++r) mq[c] = fmaxf(mq[c], s_cur[c >> 1][(c & 1) * 8 + r]);
+          for (int r = 3; r < 15; r += 2) mq[c] = max3_raw(mq[c], sc[r], sc[r + 1]);
+          mq[c] = max3_raw(mq[c], sc[15], sc[15]);
         }
-        float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
-        mx = pair_max(mx) * mult;
+        float mx = max3_raw(mq[0], mq[1], mq[1]);
+        mx = pair_max_raw(mx) * mult;
         const bool raise = mx > m_run + kStale8;
         alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
         m_run = raise ? mx : m_run;
@@ -1269,7 +1288,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   }
   __syncthreads();
   const int nr = n_rec;
-  const int qt = qg % a.n_qtiles, bh = qg / a.n_qtiles;
+  const int qt = (qg + a.qt_base) % a.n_qtiles, bh = (qg + a.qt_base) / a.n_qtiles;
   const int h = bh % a.H, b = bh / a.H;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = (lane & 31) * 4;
@@ -1558,8 +1577,10 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   // moves them onto the 8-wave kernel (C3: 0.598 -> 0.571 ms, B 2: 1.246 -> 1.154 ms).
   a.split = 0;
   a.units = 0;
+  a.qt_base = 0;
   a.part_o = a.part_ml = nullptr;
   int64_t split_bytes = 0;
+  int split_mode = 0;  // 1: every q-tile shares the CUs; 2: only the last round's q-tiles do
   const int nt = n_frames * a.ntiles_f;
   const int64_t qt8 = (int64_t)((q_len + kSplitBQ - 1) / kSplitBQ) * heads * batch;
   const int64_t units8 = qt8 * nt;
@@ -1571,7 +1592,19 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     };
     const double t_plain = nw == 8 ? t_grid(a.n_wg, 1, 1.0) : t_grid(a.n_wg, 2, 1.10);
     const double t_split = ((double)units8 / n_cu + 3.0) * t_tile(n_cu);
-    if (t_split < (nw == 8 ? 0.85 : 0.97) * t_plain) split_bytes = split_workspace_bytes(n_cu);
+    if (t_split < (nw == 8 ? 0.85 : 0.97) * t_plain) {
+      split_bytes = split_workspace_bytes(n_cu);
+      split_mode = 1;
+    } else if (nw == 8 && a.n_wg > n_cu && a.n_wg % n_cu != 0) {
+      // tail split: the full rounds run unsplit, the q-tiles of the last, partly filled round
+      // share all CUs (C5: 912 q-tiles = 3 rounds + 144; the 4th round would run at 56% fill)
+      const int64_t full = a.n_wg / n_cu, last = a.n_wg - full * n_cu;
+      const double t_tail = full * nt * t_tile(n_cu) + ((double)last * nt / n_cu + 3.0) * t_tile(n_cu);
+      if (t_tail < 0.97 * t_plain) {
+        split_bytes = split_workspace_bytes(n_cu);
+        split_mode = 2;
+      }
+    }
   }
   // The split needs the caller's workspace (2 records of kSplitBQ rows x (O, max, sum) per
   // workgroup); without one the launch stays unsplit.  The library never allocates.
@@ -1585,11 +1618,15 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
       set_error("skv_attention_ex: workspace must be 16-byte aligned");
       return SKV_E_ARG;
     }
-    nw = 8;
-    a.split = 1;
-    a.n_qtiles = (int)(qt8 / ((int64_t)heads * batch));
-    a.n_wg = n_cu;
-    a.units = units8;
+    if (split_mode == 1) {
+      nw = 8;
+      a.split = 1;
+      a.n_qtiles = (int)(qt8 / ((int64_t)heads * batch));
+      a.n_wg = n_cu;
+      a.units = units8;
+    } else {
+      a.split = 2;  // launched below as an unsplit grid of the full rounds, then the tail
+    }
   }
   a.slot_stride = (int64_t)batch * heads * a.Tp * kHeadDim;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
@@ -1620,28 +1657,46 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     set_error("skv_attention_ex: the chunk-causal mask needs whole frames (no frame_lens)");
     return SKV_E_UNSUPPORTED;
   }
+  const int64_t full_wg = a.split == 2 ? (int64_t)(a.n_wg / n_cu) * n_cu : 0;
   if (plan) {
-    *plan = skv_launch_plan{nw, a.split, a.n_wg, a.n_qtiles * heads * batch, split_bytes};
+    *plan = skv_launch_plan{nw, a.split, a.split == 2 ? (int)full_wg + n_cu : a.n_wg,
+                            a.n_qtiles * heads * batch, split_bytes};
     return SKV_OK;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rm = prope ? 2 : rope ? 1 : 0;
+  auto combine = [&](const AttnArgs& c, int n_q) {
+    if (q_dtype == SKV_BF16)
+      hipLaunchKernelGGL((attn_combine_kernel<bf16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
+    else
+      hipLaunchKernelGGL((attn_combine_kernel<float>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
+  };
   if (a.split) {
-    // 2 records per workgroup: O rows first, then (max, sum) pairs
-    const size_t rec_rows = (size_t)2 * a.n_wg * kSplitBQ;
+    // 2 records per split workgroup (n_cu of them): O rows first, then (max, sum) pairs
+    const size_t rec_rows = (size_t)2 * n_cu * kSplitBQ;
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + rec_rows * kHeadDim;
   }
-  if (nw == 8)
-    launch<8>(a, q_dtype, pool_dtype, rm, s);
-  else
-    launch<4>(a, q_dtype, pool_dtype, rm, s);
-  if (a.split) {
-    const int n_q = a.n_qtiles * heads * batch;
-    if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_combine_kernel<bf16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, a);
+  if (a.split == 2) {
+    // the full rounds unsplit, then the last round's q-tiles [full_wg, n_wg) over every CU
+    const int n_tail = a.n_wg - (int)full_wg;
+    AttnArgs m = a;
+    m.split = 0;
+    m.n_wg = (int)full_wg;
+    launch<8>(m, q_dtype, pool_dtype, rm, s);
+    AttnArgs t = a;
+    t.split = 1;
+    t.n_wg = n_cu;
+    t.units = (int64_t)n_tail * nt;
+    t.qt_base = (int)full_wg;
+    launch<8>(t, q_dtype, pool_dtype, rm, s);
+    combine(t, n_tail);
+  } else {
+    if (nw == 8)
+      launch<8>(a, q_dtype, pool_dtype, rm, s);
     else
-      hipLaunchKernelGGL((attn_combine_kernel<float>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, a);
+      launch<4>(a, q_dtype, pool_dtype, rm, s);
+    if (a.split) combine(a, a.n_qtiles * heads * batch);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

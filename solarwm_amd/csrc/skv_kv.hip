@@ -673,11 +673,14 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     const E* __restrict__ kp = static_cast<const E*>(a.kpool) + slot * a.slot_stride +
                                ((int64_t)(b * a.H + h) * a.Tp + tok0) * kHeadDim;
     E* __restrict__ ko = static_cast<E*>(a.kout) + obase;
-    // every row of a slot (padding included) is readable: all loads first, then the stores
+    // all loads first, then the stores; padding rows re-read the frame's last row (same line,
+    // no HBM traffic) and are not stored
     const int col = (tid & 15) * 8;
+    const int last = a.T - 1 - tok0;
     Vec8<E> kv[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) kv[r] = Vec8<E>::load_nt(kp + ((tid >> 4) + 8 * r) * kHeadDim + col);
+    for (int r = 0; r < 8; ++r)
+      kv[r] = Vec8<E>::load_nt(kp + min((tid >> 4) + 8 * r, last) * kHeadDim + col);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int row = (tid >> 4) + 8 * r;
@@ -691,11 +694,14 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
   const int i = tid - 128;
   const int tb = i & 7, db = i >> 3;  // tokens tb*8.., channels db*8..
   const int tokb = tok0 + tb * 8;
+  // a vector of padding tokens only re-reads the frame's last vector (its values are not
+  // stored): vectors that start at or past T cost no HBM traffic
+  const int tcol = min(tokb, ((a.T - 1) >> 3) << 3) - tok0;
   if constexpr (sizeof(E) == 2) {
     u32x4 in[8], out[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r)
-      in[r] = ld_nt(vp + (int64_t)(db * 8 + r) * a.Tp + tb * 8);
+      in[r] = ld_nt(vp + (int64_t)(db * 8 + r) * a.Tp + tcol);
     transpose8x8_b16(in, out);
 #pragma unroll
     for (int c = 0; c < 8; ++c)
@@ -704,7 +710,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
   } else {
     Vec8<E> in[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) in[r] = Vec8<E>::load_nt(vp + (int64_t)(db * 8 + r) * a.Tp + tb * 8);
+    for (int r = 0; r < 8; ++r) in[r] = Vec8<E>::load_nt(vp + (int64_t)(db * 8 + r) * a.Tp + tcol);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       Vec8<E> o;

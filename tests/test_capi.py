@@ -228,7 +228,7 @@ SPLIT_BYTES = 2 * 256 * 256 * 130 * 4  # 2 records x 256 rows x (128 O + max + s
     ("c2", 1, 12, 4680, 1560, 21, _lib.SKV_BF16, (8, 0, 228)),
     ("c3", 1, 24, 2640, 880, 21, _lib.SKV_BF16, (8, 1, 256)),
     ("c4", 1, 40, 4680, 1560, 29, _lib.SKV_BF16, (8, 0, 760)),
-    ("c5", 4, 12, 4680, 1560, 21, _lib.SKV_FP8_E4M3, (8, 0, 912)),
+    ("c5", 4, 12, 4680, 1560, 21, _lib.SKV_FP8_E4M3, (8, 2, 1024)),
     ("one_frame", 1, 12, 1560, 1560, 21, _lib.SKV_BF16, (8, 1, 256)),
     ("one_frame_fp8", 4, 12, 1560, 1560, 21, _lib.SKV_FP8_E4M3, (8, 1, 256)),
 ])
