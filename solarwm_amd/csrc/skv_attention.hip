@@ -818,8 +818,13 @@ void attn_kernel(AttnArgs a) {
 // 32 hh .. 32 hh + 31 (32 bytes).
 //   * Q is quantised in-kernel per query row (scale = absmax/448); the K frame scale and the Q
 //     row scale fold into the softmax FMA: x = acc * (log2e*scale*sq*sk) - m;
-//   * P is quantised as P * sv * G (sv = the tile's V frame scale, G = 110 / max_window(sv), so
-//     P <= 2^kStale8 = 4 maps below 448) and O is divided by G * sum(P) at the end;
+//   * P is quantised as P * sv * G (sv = the tile's V frame scale, G = 28 / max_window(sv), so
+//     P <= 16 maps below 448) and O is divided by G * sum(P) at the end;
+//   * the running max is speculative, as in attn_kernel: probabilities are formed against the
+//     max of the earlier tiles, and a lane whose four partial sums of 8 scaled probabilities
+//     P * sv * G are not all <= 448 (so one of them might not fit e4m3), or whose max is still
+//     -inf, sends the wave to a rare path that raises the max to the tile's true max and
+//     recomputes the tile (P up to 16 x the row max's fits without it);
 //   * per 64-key tile and wave: 4 QK MFMAs (2 key blocks kb x 2 channel halves cs; A = K rows,
 //     B = the lane's 32 quantised Q channels cs*64 + 32 hh ..) and 4 PV MFMAs (one per
 //     32-channel block db; A = V^T row 32 db + n, keys 32 hh .. +31; B = P^T, the lane's
@@ -1051,11 +1056,11 @@ void attn_fp8_kernel(AttnArgs a) {
   auto kb_lds = [&](int i) { return lds + i * kBuf; };
   auto vb_lds = [&](int i) { return lds + (2 + i) * kBuf; };
 
-  constexpr float kStale8 = 2.0f;
+  constexpr float kMaxPart8 = 448.0f;  // bound on every partial sum of scaled probabilities
   float sv_max = 0.f;
   for (int j = 0; j < a.n_frames; ++j)
     sv_max = fmaxf(sv_max, a.vscale[(int64_t)a.slots[j] * a.B * a.H + sc_bh]);
-  const float G = sv_max > 0.f ? 110.0f / sv_max : 1.0f;
+  const float G = sv_max > 0.f ? 28.0f / sv_max : 1.0f;
   const float c2q = a.scale_log2 * q_scale;
   const int lane16 = lane * 16;
 
@@ -1127,7 +1132,7 @@ void attn_fp8_kernel(AttnArgs a) {
     // when its exps have finished.
     i32x8 op[4];
     float pf[32], ls[4];
-    float alpha = 1.0f, bias = 0.f;
+    const float bias = log_pv - (m_run == -INFINITY ? 0.f : m_run);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
       op[i] = (i & 1) ? lds_op32(vl + (i >> 1) * kOp8) : lds_op32(kl + korder64(i >> 1) * kOp8);
@@ -1142,27 +1147,6 @@ void attn_fp8_kernel(AttnArgs a) {
         s_nxt[kb] = mfma64(op[i & 3], q8[cs], cs == 0 ? zero16 : s_nxt[kb]);
       } else {
         oacc[i >> 1] = mfma64(op[i & 3], pprev, oacc[i >> 1]);
-      }
-      if (i == 0) {  // the tile's max, the running max and the exponent bias
-        // two independent chains of 3-input maxima (8 each), so the max is not one 16-deep
-        // dependency before the MFMAs.  Inline asm: fmaxf would first quiet every score with a
-        // v_max_f32 x, x (IEEE maxnum), 11 more instructions per tile; MFMA results are never
-        // signalling NaNs.
-        float mq[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const f32x16& sc = s_cur[c];
-          mq[c] = max3_raw(sc[0], sc[1], sc[2]);
-#pragma unroll
-          for (int r = 3; r < 15; r += 2) mq[c] = max3_raw(mq[c], sc[r], sc[r + 1]);
-          mq[c] = max3_raw(mq[c], sc[15], sc[15]);
-        }
-        float mx = max3_raw(mq[0], mq[1], mq[1]);
-        mx = pair_max_raw(mx) * mult;
-        const bool raise = mx > m_run + kStale8;
-        alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
-        m_run = raise ? mx : m_run;
-        bias = log_pv - (m_run == -INFINITY ? 0.f : m_run);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -1182,13 +1166,50 @@ void attn_fp8_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) ls[j] += pf[28 + j];
     pb[7] = pack_fp8x4_into(pb[7], pf[28], pf[29], pf[30], pf[31]);
-    l_run = fmaf(l_run, alpha, ((ls[0] + ls[1]) + (ls[2] + ls[3])) * inv_pv);
-    if (__any(alpha != 1.0f)) {
+    {
+      const float lmax = max3_raw(max3_raw(ls[0], ls[1], ls[2]), ls[3], ls[3]);
+      const bool need = !(lmax <= kMaxPart8) || m_run == -INFINITY;
+      if (__any(need)) {
+        // rare path: both key halves of a query take the same decision; raise the max of each
+        // such query to the tile's true max and recompute its probabilities, sums and packs
+        const bool needq = pair_max(need ? 1.f : 0.f) > 0.f;
+        float mq[2];
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+        for (int c = 0; c < 2; ++c) {
+          const f32x16& sc = s_cur[c];
+          mq[c] = max3_raw(sc[0], sc[1], sc[2]);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+          for (int r = 3; r < 15; r += 2) mq[c] = max3_raw(mq[c], sc[r], sc[r + 1]);
+          mq[c] = max3_raw(mq[c], sc[15], sc[15]);
+        }
+        const float mx = pair_max_raw(max3_raw(mq[0], mq[1], mq[1])) * mult;
+        const float m_new = needq ? fmaxf(m_run, mx) : m_run;
+        const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float bias2 = log_pv - (m_new == -INFINITY ? 0.f : m_new);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ls[j] = 0.f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          float q4[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int e = 4 * d + j;
+            q4[j] = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], mult, bias2));
+            ls[j] += q4[j];
+          }
+          pb[d] = pack_fp8x4_into(pb[d], q4[0], q4[1], q4[2], q4[3]);
+        }
+        l_run *= alpha;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+        }
+        m_run = m_new;
+      }
     }
+    l_run = fmaf(((ls[0] + ls[1]) + (ls[2] + ls[3])), inv_pv, l_run);
     if (tau + 1 < ntau) {
       const int tok0 = mw.t * kTile, key0 = mw.j * a.T + tok0;
       if ((tok0 + kTile > mw.flen) || (key0 + kTile > lim_lo))
