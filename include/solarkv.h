@@ -42,7 +42,10 @@ typedef void* skv_stream_t; /* a hipStream_t; NULL = the null stream */
 enum skv_dtype {
   SKV_F32 = 0,
   SKV_BF16 = 1,
-  SKV_FP8_E4M3 = 2 /* OCP e4m3fn, pools only */
+  SKV_FP8_E4M3 = 2, /* OCP e4m3fn, pools only */
+  SKV_F16 = 3       /* IEEE binary16: f16 pools filled from f16 sources (plain append, no
+                       norm / RoPE / PRoPE), gathered, and attended with f16 MFMAs (plain
+                       attention; queries and outputs f16 or f32) */
 };
 
 enum skv_mask_mode {

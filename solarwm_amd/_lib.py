@@ -16,6 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsolarkv.so"
 SKV_F32 = 0
 SKV_BF16 = 1
 SKV_FP8_E4M3 = 2
+SKV_F16 = 3
 
 SKV_MASK_NONE = 0
 SKV_MASK_CHUNK_CAUSAL = 1

@@ -74,15 +74,22 @@ def attention(
         raise ValueError(f"head_dim must be {kernels.HEAD_DIM}")
     if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
         raise ValueError("q, k, v must be [B, L, H, D] with matching B, H and k.shape == v.shape")
-    # attention.py:69-73 casts non-half inputs to `dtype` and q, k to v's dtype.  The kernels
-    # compute in bf16 and round fp32 operands to bf16 on load, which is that cast for
-    # dtype=bfloat16; fp16 arithmetic is not provided.
-    if torch.float16 in (q.dtype, k.dtype, v.dtype) or (
-        dtype == torch.float16 and v.dtype == torch.float32
-    ):
-        raise NotImplementedError("float16 attention is not provided (bf16 matrix path only)")
-    kv_dtype = v.dtype
-    qh, kh, vh = q.to(kv_dtype), k.to(kv_dtype), v
+    # attention.py:69-87: inputs that are not half precision are cast to `dtype`, then q and k
+    # to v's dtype, and the kernel computes in that dtype.  bf16 runs the bf16 MFMA kernel (fp32
+    # inputs with dtype=bfloat16 are passed as fp32 and rounded to bf16 on load, the same
+    # rounding); fp16 runs the same kernel on fp16 pools with fp16 MFMAs.
+    half = (torch.float16, torch.bfloat16)
+
+    def to_half(x):
+        return x if x.dtype in half else x.to(dtype)
+
+    if v.dtype in half or dtype == torch.float16:
+        vh = to_half(v)
+        kv_dtype = vh.dtype
+        qh, kh = to_half(q).to(kv_dtype), to_half(k).to(kv_dtype)
+    else:  # fp32 inputs, dtype=bfloat16: the kernels round them to bf16 on load
+        kv_dtype = v.dtype
+        qh, kh, vh = q.to(kv_dtype), k.to(kv_dtype), v
     if q_scale is not None:
         qh = (qh.float() * q_scale).to(kv_dtype)
     if q_lens is None and k_lens is None:

@@ -202,6 +202,14 @@ __device__ inline void store4<float>(float* p, float x0, float x1, float x2, flo
   *reinterpret_cast<f32x4*>(p) = f32x4{x0, x1, x2, x3};
 }
 
+template <>
+__device__ inline void store4<f16>(f16* p, float x0, float x1, float x2, float x3) {
+  typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+  f16x4 v;
+  v[0] = (f16)x0; v[1] = (f16)x1; v[2] = (f16)x2; v[3] = (f16)x3;
+  *reinterpret_cast<f16x4*>(p) = v;
+}
+
 // Stage one 64-key tile of K (or V^T) into a 16 KB LDS buffer: wave w writes operand blocks
 // [w*kBpw, (w+1)*kBpw) of the 16.  K block b = (kb = b/8, k-step s = b%8); V^T block
 // b = (db = b/4, kb*2+s2 = b%4).  bf16 pools use direct 16 B global->LDS loads (no registers);
@@ -261,16 +269,40 @@ struct TileLoader {
   }
 };
 
+// MFMA operand element of a pool type: f16 pools multiply in f16, every other pool (bf16, and
+// fp32 rounded to bf16 on staging) in bf16.
+template <typename KT>
+struct OpOf {
+  using E = bf16;
+  using x8 = bf16x8;
+  template <typename V>
+  __device__ static x8 from(const V& v) { return v.to_bf16(); }
+};
+template <>
+struct OpOf<f16> {
+  using E = f16;
+  using x8 = f16x8;
+  template <typename V>
+  __device__ static x8 from(const V& v) { return v.to_f16(); }
+};
+__device__ inline f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ inline f32x16 mfma32(const f16x8& a, const f16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 // S^T (64 keys x 32 queries of this wave) = K Q^T from a K tile in LDS.
-__device__ inline void qk_tile(const char* kl, const bf16x8 (&qf)[8], f32x16 (&s)[2]) {
+template <typename X8>
+__device__ inline void qk_tile(const char* kl, const X8 (&qf)[8], f32x16 (&s)[2]) {
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const bf16x8 ak = *reinterpret_cast<const bf16x8*>(kl + (kb * 8 + k) * kBlockBytes);
-      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, qf[k], s[kb], 0, 0, 0);
+      const X8 ak = *reinterpret_cast<const X8*>(kl + (kb * 8 + k) * kBlockBytes);
+      s[kb] = mfma32(ak, qf[k], s[kb]);
     }
   }
 }
@@ -290,6 +322,8 @@ template <int NW, typename QT, typename KT, int RM, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   constexpr int kBQ = NW * 32;
+  using ET = typename OpOf<KT>::E;     // MFMA operand element
+  using etx8 = typename OpOf<KT>::x8;
   // LDS: K tiles in [0, 32 KB) (two buffers), V^T tiles in [32 KB, 64 KB) (two buffers).
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr int kHalf = 16 * kBlockBytes;
@@ -341,12 +375,12 @@ void attn_kernel(AttnArgs a) {
   const bool qlive = qrow < a.Lq;
 
   // Q^T operand: lane (n, hh) holds q[qrow][k*16 + hh*8 .. +7] for k = 0..7.
-  bf16x8 qf[8];
+  etx8 qf[8];
   // RM = 0: Q as given.  RM = 1 (RoPE): the query's height/width pairs are rotated once here;
   // its temporal pairs (0..21, in qf[0..2]) are kept unrotated in qt0 and turned by
   // (p_query - p_key) per key frame below.  RM = 2 (RoPE + PRoPE): as RM = 1, the spatial
   // groups then take P_q^T, and the temporal groups take the per-key-frame matrix W below.
-  [[maybe_unused]] bf16x8 qt0[3];
+  [[maybe_unused]] etx8 qt0[3];
   [[maybe_unused]] int qfi = 0;  // query frame of this lane's row
   {
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
@@ -386,7 +420,7 @@ void attn_kernel(AttnArgs a) {
           for (int gg = 0; gg < 2; ++gg)
             if (4 * k + 2 * hh + gg >= kGroupsT) xform4(y, gg, ps);
         }
-        qf[k] = y.to_bf16();
+        qf[k] = OpOf<KT>::from(y);
       }
 #pragma unroll
       for (int k = 0; k < 3; ++k) qt0[k] = qf[k];
@@ -397,12 +431,12 @@ void attn_kernel(AttnArgs a) {
         Vec8<float> y;
 #pragma unroll
         for (int e = 0; e < 8; ++e) y.set(e, (float)x.get(e) * qn * qw[k * 16 + e]);
-        qf[k] = y.to_bf16();
+        qf[k] = OpOf<KT>::from(y);
       }
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        qf[k] = qlive ? Vec8<QT>::load(qp + k * 16).to_bf16() : Vec8<bf16>::zero().to_bf16();
+        qf[k] = OpOf<KT>::from(qlive ? Vec8<QT>::load(qp + k * 16) : Vec8<QT>::zero());
     }
   }
   // PRoPE: W of key frame j for query frames [qf_lo, qf_lo + count) -> LDS buffer j & 1 (waves
@@ -469,7 +503,7 @@ void attn_kernel(AttnArgs a) {
         y.set(2 * m, u * c - v * sn);
         y.set(2 * m + 1, u * sn + v * c);
       }
-      qf[k] = y.to_bf16();
+      qf[k] = OpOf<KT>::from(y);
     }
   };
 
@@ -535,11 +569,11 @@ void attn_kernel(AttnArgs a) {
   // Score and probability registers ping-pong between two sets (A, B) across iterations, so no
   // loop-carried copy is needed.
   f32x16 sA[2], sB[2];
-  bf16x8 pA[2][2], pB[2][2];
+  etx8 pA[2][2], pB[2][2];
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y) pA[x][y] = Vec8<bf16>::zero().to_bf16();
+    for (int y = 0; y < 2; ++y) pA[x][y] = OpOf<KT>::from(Vec8<float>::zero());
   f32x16 (&s_cur)[2] = sA;
   if (ntau > 0) {
     loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
@@ -575,24 +609,24 @@ void attn_kernel(AttnArgs a) {
   vw.start(a, kbh, tb);
   mw.start(a, kbh, tb + 1);
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
-                  bf16x8 (&pprev)[2][2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+                  etx8 (&pprev)[2][2], etx8 (&pb)[2][2]) __attribute__((always_inline)) {
     const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
     const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
     // operand of MFMA slot i: even i -> QK step i/2 (k = i/4, kb = (i/2)&1), odd i -> PV step i/2
-    auto operand = [&](int i) -> bf16x8 {
+    auto operand = [&](int i) -> etx8 {
       const int st = i >> 1;
       if ((i & 1) == 0) {
         const int k = st >> 1, kbb = st & 1;
-        return *reinterpret_cast<const bf16x8*>(kl + (kbb * 8 + k) * kBlockBytes);
+        return *reinterpret_cast<const etx8*>(kl + (kbb * 8 + k) * kBlockBytes);
       }
       int db, kbb, s2;
       pv_order(st, db, kbb, s2);
-      return *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
+      return *reinterpret_cast<const etx8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
     };
     // the first three operands are requested before this step's loads are issued, so their LDS
     // latency overlaps the load set-up (PRoPE: after the query transform below, which needs the
     // registers)
-    bf16x8 opq[4];
+    etx8 opq[4];
     if constexpr (RM != 2) {
 #pragma unroll
       for (int i = 0; i < 3; ++i) opq[i] = operand(i);
@@ -627,8 +661,8 @@ void attn_kernel(AttnArgs a) {
       pf[e] = p;
       ls[e & 3] += p;
       if (e & 1) {
-        pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (bf16)pf[e - 1];
-        pb[e >> 4][(e >> 3) & 1][e & 7] = (bf16)p;
+        pb[e >> 4][(e >> 3) & 1][(e & 7) - 1] = (ET)pf[e - 1];
+        pb[e >> 4][(e >> 3) & 1][e & 7] = (ET)p;
       }
     };
     constexpr bool kFront = RM != 2;  // softmax schedule, below
@@ -646,11 +680,11 @@ void attn_kernel(AttnArgs a) {
       const int st = i >> 1;
       if ((i & 1) == 0) {
         const int k = st >> 1, kbb = st & 1;
-        s_nxt[kbb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], qf[k], k == 0 ? zero16 : s_nxt[kbb], 0, 0, 0);
+        s_nxt[kbb] = mfma32(opq[i & 3], qf[k], k == 0 ? zero16 : s_nxt[kbb]);
       } else {
         int db, kbb, s2;
         pv_order(st, db, kbb, s2);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opq[i & 3], pprev[kbb][s2], oacc[db], 0, 0, 0);
+        oacc[db] = mfma32(opq[i & 3], pprev[kbb][s2], oacc[db]);
       }
       // softmax of tile tau, front-loaded: slot i < 4 takes probabilities 2i and 2i+1, slot
       // 4 <= i < 28 probability i + 4; each is summed and packed one slot after its exp (so no
@@ -662,8 +696,8 @@ void attn_kernel(AttnArgs a) {
           ls[d & 3] = d < 4 ? pf[d] : ls[d & 3] + pf[d];
           asm volatile("" ::"v"(ls[d & 3]));
           if (d & 1) {
-            pb[d >> 4][(d >> 3) & 1][(d & 7) - 1] = (bf16)pf[d - 1];
-            pb[d >> 4][(d >> 3) & 1][d & 7] = (bf16)pf[d];
+            pb[d >> 4][(d >> 3) & 1][(d & 7) - 1] = (ET)pf[d - 1];
+            pb[d >> 4][(d >> 3) & 1][d & 7] = (ET)pf[d];
           }
           if ((d & 7) == 7) asm volatile("" ::"v"(pb[d >> 4][(d >> 3) & 1]));
         };
@@ -702,8 +736,8 @@ void attn_kernel(AttnArgs a) {
     }
     if constexpr (!kFront) {
       ls[3] += pf[31];
-      pb[1][1][6] = (bf16)pf[30];
-      pb[1][1][7] = (bf16)pf[31];
+      pb[1][1][6] = (ET)pf[30];
+      pb[1][1][7] = (ET)pf[31];
       lp = (ls[0] + ls[1]) + (ls[2] + ls[3]);
       need = !(lp <= kMaxPart) || m_run == -INFINITY;
     }
@@ -749,7 +783,7 @@ void attn_kernel(AttnArgs a) {
     step(tau + 1, 1, sB, sA, pB, pA);
   }
   // Epilogue: PV(ntau-1).
-  auto epilogue = [&](const bf16x8 (&pprev)[2][2]) __attribute__((always_inline)) {
+  auto epilogue = [&](const etx8 (&pprev)[2][2]) __attribute__((always_inline)) {
     const char* vl = vb_lds((ntau - 1) & 1) + lane16;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -757,9 +791,9 @@ void attn_kernel(AttnArgs a) {
       for (int kbb = 0; kbb < 2; ++kbb)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x8 av =
-              *reinterpret_cast<const bf16x8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pprev[kbb][s2], oacc[db], 0, 0, 0);
+          const etx8 av =
+              *reinterpret_cast<const etx8*>(vl + (db * 4 + kbb * 2 + s2) * kBlockBytes);
+          oacc[db] = mfma32(av, pprev[kbb][s2], oacc[db]);
         }
   };
   if (tau < ntau) {
@@ -1371,6 +1405,20 @@ static int64_t split_workspace_bytes(int n_wg) {
 template <int NW>
 static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipStream_t s) {
   dim3 grid(a.n_wg), block(NW * 64);
+  if (pool_dtype == SKV_F16) {  // plain attention, f16 MFMAs; q f16 or f32 (checked by the caller)
+    const size_t lds = 2 * kTileBytes;
+    const bool qh = q_dtype == SKV_F16;
+    if constexpr (NW == 8) {
+      if (a.split) {
+        if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true>), grid, block, lds, s, a);
+        return;
+      }
+    }
+    if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0>), grid, block, lds, s, a);
+    else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0>), grid, block, lds, s, a);
+    return;
+  }
   if (pool_dtype == SKV_FP8_E4M3) {
     if constexpr (NW == 8) {
       if (a.split) {
@@ -1477,12 +1525,22 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     set_error("skv_attention: chunk-causal mask needs chunk_tokens > 0 and q_pos0 >= 0");
     return SKV_E_ARG;
   }
-  if (!(q_dtype == SKV_BF16 || q_dtype == SKV_F32)) {
+  if (!(q_dtype == SKV_BF16 || q_dtype == SKV_F32 || q_dtype == SKV_F16)) {
     set_error("skv_attention: q_dtype=%d unsupported", q_dtype);
     return SKV_E_UNSUPPORTED;
   }
-  if (!(pool_dtype == SKV_BF16 || pool_dtype == SKV_F32 || pool_dtype == SKV_FP8_E4M3)) {
+  if (!(pool_dtype == SKV_BF16 || pool_dtype == SKV_F32 || pool_dtype == SKV_FP8_E4M3 ||
+        pool_dtype == SKV_F16)) {
     set_error("skv_attention: pool_dtype=%d unsupported", pool_dtype);
+    return SKV_E_UNSUPPORTED;
+  }
+  // f16 pools take f16 or f32 queries, f16 queries need f16 pools (the reference casts q to the
+  // key/value dtype before its kernel, attention.py:86-87)
+  const bool q_ok = pool_dtype == SKV_F16 ? (q_dtype == SKV_F16 || q_dtype == SKV_F32)
+                                          : q_dtype != SKV_F16;
+  if (!q_ok) {
+    set_error("skv_attention: q_dtype=%d with pool_dtype=%d unsupported (f16 pools take f16 or "
+              "f32 queries; f16 queries need f16 pools)", q_dtype, pool_dtype);
     return SKV_E_UNSUPPORTED;
   }
   if (pool_dtype == SKV_FP8_E4M3 && (!k_scale || !v_scale)) {
@@ -1689,6 +1747,8 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   auto combine = [&](const AttnArgs& c, int n_q) {
     if (q_dtype == SKV_BF16)
       hipLaunchKernelGGL((attn_combine_kernel<bf16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
+    else if (q_dtype == SKV_F16)
+      hipLaunchKernelGGL((attn_combine_kernel<f16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
     else
       hipLaunchKernelGGL((attn_combine_kernel<float>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
   };

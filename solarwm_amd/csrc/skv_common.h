@@ -11,6 +11,8 @@ namespace skv {
 
 typedef __bf16 bf16;
 typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -113,9 +115,40 @@ struct Vec8<float> {
     o[4] = (bf16)b[0]; o[5] = (bf16)b[1]; o[6] = (bf16)b[2]; o[7] = (bf16)b[3];
     return o;
   }
+  // Round-to-nearest-even, the rounding of torch's .to(torch.float16).
+  __device__ f16x8 to_f16() const {
+    f16x8 o;
+    o[0] = (f16)a[0]; o[1] = (f16)a[1]; o[2] = (f16)a[2]; o[3] = (f16)a[3];
+    o[4] = (f16)b[0]; o[5] = (f16)b[1]; o[6] = (f16)b[2]; o[7] = (f16)b[3];
+    return o;
+  }
   __device__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
   __device__ void set(int i, float x) {
     if (i < 4) a[i] = x; else b[i - 4] = x;
+  }
+};
+
+// IEEE binary16 (fp16 attention: f16 pools, queries and outputs)
+template <>
+struct Vec8<f16> {
+  u32x4 r;
+  __device__ static Vec8 load(const f16* p) {
+    Vec8 v;
+    v.r = *reinterpret_cast<const u32x4*>(p);
+    return v;
+  }
+  __device__ void store(f16* p) const { *reinterpret_cast<u32x4*>(p) = r; }
+  __device__ static Vec8 zero() {
+    Vec8 v;
+    v.r = u32x4{0u, 0u, 0u, 0u};
+    return v;
+  }
+  __device__ f16x8 to_f16() const { return __builtin_bit_cast(f16x8, r); }
+  __device__ f16 get(int i) const { return __builtin_bit_cast(f16x8, r)[i]; }
+  __device__ void set(int i, f16 x) {
+    f16x8 t = __builtin_bit_cast(f16x8, r);
+    t[i] = x;
+    r = __builtin_bit_cast(u32x4, t);
   }
 };
 

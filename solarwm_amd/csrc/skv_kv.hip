@@ -811,10 +811,16 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   }
   if (n_frames == 0) return SKV_OK;
   const bool fp8 = pool_dtype == SKV_FP8_E4M3;
-  if (!(src_dtype == SKV_BF16 || src_dtype == SKV_F32) ||
-      !(pool_dtype == src_dtype || fp8)) {
+  if (!(src_dtype == SKV_BF16 || src_dtype == SKV_F32 || src_dtype == SKV_F16) ||
+      !(pool_dtype == src_dtype || (fp8 && src_dtype != SKV_F16))) {
     set_error("skv_append: src_dtype=%d pool_dtype=%d unsupported (pool must equal src or be fp8)",
               src_dtype, pool_dtype);
+    return SKV_E_UNSUPPORTED;
+  }
+  // f16 chunks move bit for bit through the bf16 kernel (a plain append converts nothing); the
+  // K norm and the RoPE / PRoPE copies compute, so they stay bf16 / f32 only
+  if (src_dtype == SKV_F16 && (kr_pool || vr_pool || kv_xform || k_inv_rms)) {
+    set_error("skv_append: f16 pools take plain appends only (no K norm, RoPE or PRoPE copies)");
     return SKV_E_UNSUPPORTED;
   }
   if (kr_pool) {
@@ -938,7 +944,7 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
     }
   } else {
     dim3 grid(n_frames * batch * heads * a.ntiles);
-    if (src_dtype == SKV_BF16) {
+    if (src_dtype == SKV_BF16 || src_dtype == SKV_F16) {
       if (kv_xform)
         hipLaunchKernelGGL((append_kernel<bf16, 2>), grid, dim3(256), 0, s, a);
       else if (kr_pool)
@@ -1101,11 +1107,12 @@ extern "C" int skv_gather(const void* k_pool, const void* v_pool, int pool_dtype
     return SKV_E_ARG;
   }
   if (n_frames == 0) return SKV_OK;
-  if (!(pool_dtype == SKV_BF16 || pool_dtype == SKV_F32 || pool_dtype == SKV_FP8_E4M3)) {
+  if (!(pool_dtype == SKV_BF16 || pool_dtype == SKV_F32 || pool_dtype == SKV_FP8_E4M3 ||
+        pool_dtype == SKV_F16)) {
     set_error("skv_gather: pool_dtype=%d unsupported", pool_dtype);
     return SKV_E_UNSUPPORTED;
   }
-  const int esz = pool_dtype == SKV_F32 ? 4 : (pool_dtype == SKV_BF16 ? 2 : 1);
+  const int esz = pool_dtype == SKV_F32 ? 4 : (pool_dtype == SKV_FP8_E4M3 ? 1 : 2);
   if (out_sb % 8 || out_st % 8 || out_sh % 8 || !aligned8(k_out, esz) || !aligned8(v_out, esz)) {
     set_error("skv_gather: output strides/pointers must be multiples of 8 elements");
     return SKV_E_ARG;
@@ -1134,7 +1141,7 @@ extern "C" int skv_gather(const void* k_pool, const void* v_pool, int pool_dtype
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(n_frames * batch * heads * a.ntiles);
-  if (pool_dtype == SKV_BF16)
+  if (pool_dtype == SKV_BF16 || pool_dtype == SKV_F16)  // 16-bit codes move bit for bit
     hipLaunchKernelGGL(gather_kernel<bf16>, grid, dim3(256), 0, s, a);
   else if (pool_dtype == SKV_F32)
     hipLaunchKernelGGL(gather_kernel<float>, grid, dim3(256), 0, s, a);

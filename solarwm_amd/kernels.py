@@ -28,6 +28,7 @@ _DTYPE_CODES = {
     torch.float32: _lib.SKV_F32,
     torch.bfloat16: _lib.SKV_BF16,
     torch.float8_e4m3fn: _lib.SKV_FP8_E4M3,
+    torch.float16: _lib.SKV_F16,
 }
 
 
@@ -100,7 +101,7 @@ def dtype_code(dtype: torch.dtype) -> int:
     try:
         return _DTYPE_CODES[dtype]
     except KeyError:
-        raise ValueError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float8_e4m3fn")
+        raise ValueError(f"unsupported dtype {dtype}; expected float32, bfloat16, float16 or float8_e4m3fn")
 
 
 def _stream(device: torch.device) -> int:
@@ -429,8 +430,12 @@ def attention_desc(
     ``skv_attention_ex`` (no workspace set).  Arguments as :func:`attention_frames`."""
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("q", q)
-    if q.dtype not in (torch.float32, torch.bfloat16):
-        raise ValueError(f"q dtype {q.dtype} unsupported (float32 or bfloat16)")
+    if q.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"q dtype {q.dtype} unsupported (float32, bfloat16 or float16)")
+    if (q.dtype == torch.float16) != (kpool.dtype == torch.float16) and not (
+            kpool.dtype == torch.float16 and q.dtype == torch.float32):
+        raise ValueError("float16 pools take float16 or float32 queries; float16 queries need "
+                         "float16 pools")
     if q.shape[0] != b or q.shape[2] != h:
         raise ValueError(f"q batch/heads {tuple(q.shape)} do not match the pool ({b}, {h})")
     if q.device != kpool.device:
