@@ -820,7 +820,9 @@ def segments_leg(device, iters=5):
     """Segmented attention at the config-2 head shape (H12, 1560 tok/frame):
     * teacher forcing over [clean | noisy] x 6 frames (2 chunks of 3, sink 1 chunk, 1 prior clean
       chunk; causal_model.py:337-471): ours (one launch per query chunk over its frame list)
-      vs SDPA with the dense boolean mask (FlexAttention needs Triton, absent here);
+      vs the reference's op, FlexAttention with a block mask of the same rule
+      (causal_model.py:984-989; torch.compile'd, timed after compiling), and vs SDPA with the
+      dense boolean mask (its fallback);
     * H3 rollout window (sgf_attention.py:236-258): a 5-frame chunk over a 1000-token prefix,
       5 history chunks and itself: ours (chunk-list cache, ragged prefix) vs torch.cat + flash
       SDPA.
@@ -864,7 +866,26 @@ def segments_leg(device, iters=5):
             mask[f0 * T : (f0 + nb) * T, fr * T : (fr + 1) * T] = True
     mask = mask.to(device)
     qt, kt, vt = (x.transpose(1, 2).contiguous() for x in (q, k, v))
-    ref_tf = timed(lambda: torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask))
+    sdpa_tf = timed(lambda: torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask))
+    flex_tf, flex_note = None, None
+    try:
+        from torch.nn.attention.flex_attention import create_block_mask, flex_attention
+
+        allowed = torch.zeros(2 * F // nb, 2 * F, dtype=torch.bool)
+        for f0, frames in lists:
+            for fr in frames:
+                allowed[f0 // nb, fr] = True
+        allowed = allowed.to(device)
+
+        def mask_mod(b, h, q_idx, kv_idx):
+            return allowed[q_idx // (nb * T), kv_idx // T]
+
+        block_mask = create_block_mask(mask_mod, 1, 1, L, L, device=device)
+        flex = torch.compile(flex_attention, dynamic=False)
+        flex_tf = timed(lambda: flex(qt, kt, vt, block_mask=block_mask))
+    except Exception as e:  # the baseline only: report why it is missing
+        flex_note = f"FlexAttention unavailable: {type(e).__name__}: {str(e)[:160]}"
+    ref_tf = flex_tf if flex_tf is not None else sdpa_tf
     del mask, qt, kt, vt, q, k, v
 
     cf, P = 5, 1000
@@ -890,19 +911,24 @@ def segments_leg(device, iters=5):
     w_flops = 4.0 * cf * T * (P + 6 * cf * T) * H * 128
     del cache, hist, q, k, v, pk, pv
     torch.cuda.empty_cache()
-    return {
+    out = {
         "teacher_forcing_ms": round(ours_tf, 3),
         "teacher_forcing_tflops": round(tf_flops / (ours_tf / 1e3) / 1e12, 1),
         "teacher_forcing_reference_ms": round(ref_tf, 3),
+        "teacher_forcing_reference": "flex_attention + block mask" if flex_tf is not None else "SDPA + dense mask",
         "teacher_forcing_speedup": round(ref_tf / ours_tf, 2),
+        "teacher_forcing_sdpa_dense_mask_ms": round(sdpa_tf, 3),
         "h3_window_ms": round(ours_w, 3),
         "h3_window_tflops": round(w_flops / (ours_w / 1e3) / 1e12, 1),
         "h3_window_reference_ms": round(ref_w, 3),
         "h3_window_speedup": round(ref_w / ours_w, 2),
         "workload": (f"teacher forcing [clean|noisy] 2x{F} frames x {T} tok, H{H}, chunks of {nb}, "
-                     f"sink 1 chunk, 1 prior chunk (reference: SDPA + dense bool mask); H3 window "
+                     f"sink 1 chunk, 1 prior chunk (reference: FlexAttention with the block mask); H3 window "
                      f"{cf}-frame chunk over {P} prefix + 5 history chunks (reference: cat + flash SDPA)"),
     }
+    if flex_note:
+        out["teacher_forcing_note"] = flex_note
+    return out
 
 
 def c5_quality(device, hs=slice(4, 6), rows=slice(1500, 1756)):
