@@ -11,7 +11,9 @@
  *   - attention over an under-filled grid takes the balanced key split (skv_attention_plan:
  *     2 x n_cu x 256 rows x 130 floats, 68 MB on 256 CUs);
  *   - an fp8 append of a chunk with fewer than 4 (frame, batch, head, K|V) units per CU takes
- *     the tile-grid kernels (skv_append_workspace_size: one float per 64-token tile).
+ *     the one-pass slice kernel (bf16 sources, no K norm, 8-byte aligned workspace: a 128 B
+ *     header + 512 B per unit) or else the tile-grid kernels (one float per 64-token tile);
+ *     skv_append_workspace_size reports the larger of the two.
  * Without a workspace the same calls run the unsplit kernels (same results up to fp32
  * summation order for attention; bit-identical for the append).  A workspace is read and
  * written by the launch on `stream` only, so one workspace serves any number of calls on one
@@ -241,7 +243,7 @@ typedef struct skv_append_desc {
   int grid_h, grid_w;
   void* vx_pool;
   const float* kv_xform;
-  void* workspace;         /* device, optional, 4-byte aligned: fp8 tile-grid kernels */
+  void* workspace;         /* device, optional, 4-byte aligned (8 for the one-pass fp8 kernel) */
   int64_t workspace_bytes; /* its size; must cover skv_append_workspace_size */
 } skv_append_desc;
 

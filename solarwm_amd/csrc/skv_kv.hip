@@ -8,6 +8,8 @@
 // (frame, batch, head); K rows move as 16 B vectors, V is transposed in registers, 8 tokens x 8
 // channels per thread, so the pool keeps V channel-major (tokens contiguous), which is what the
 // attention kernel's PV product reads.
+#include <cstdlib>
+
 #include "skv_common.h"
 
 namespace skv {
@@ -610,6 +612,222 @@ __global__ __launch_bounds__(256) void append_fp8_tile_kernel(AppendArgs a, cons
   st_nt(dst + 16, u32x4{rd[4], rd[5], rd[6], rd[7]});
 }
 
+// fp8 append in one pass for chunks with few (frame, batch, head, K|V) units (fewer than 4 per
+// CU, e.g. C5: 288 units of 25 tiles on 256 CUs).  Each unit is cut into slices of at most
+// kSliceTiles 64-token tiles, one 256-thread workgroup per slice, and the grid is no larger
+// than the chip holds at once (occupancy x CUs), so every slice is resident: together the slices
+// hold the whole chunk on chip (C5: 115 MB of bf16 K/V in 2016 workgroups of 64 KB, against
+// 168 MB of registers and LDS) and HBM is read once.  A workgroup issues all of its slice's loads at once (12 vectors
+// per thread into registers, 4 into LDS by direct buffer loads), reduces the slice absmax,
+// publishes it in its own word of the unit's cell (one 64-bit device-scope atomic store of
+// (1 << 32) | absmax bits: the value and its presence travel together, so no other memory
+// ordering is needed), waits until every slice of the unit has published (one lane per slice
+// polls) and encodes with the unit's absmax: the frame absmax the per-unit kernels reduce, so
+// codes and scales are bit-identical to theirs.
+//   K: thread t owns the 16 B vectors at row (t >> 4) + 16 i of each tile, channels
+//      (t & 15) * 8 .. +8 (four rows of 256 B per wave instruction); codes are 8 B per vector.
+//   V: thread t owns two 8-token x 8-channel blocks, tokens 128 k + 8 (t & 15) .. +8 of the
+//      slice, channels 8 (t >> 4) .. +8.  Codes are packed channel-major (each e4m3 pack takes
+//      one channel of successive tokens), so a store writes one channel's 8 token codes and 16
+//      lanes fill a 128 B line of V^T: no transpose buffer, no partial lines.
+// Residency is what the grid size aims for, not what the launch guarantees (other work may hold
+// CUs), so no result depends on it: the wait is bounded in time (wait_ticks of the 100 MHz
+// real-time counter), and a workgroup whose unit has not completed by then reads the whole
+// unit again to form the same absmax itself (correct, slower; word 0 of the workspace then
+// records that a fallback ran).  fp8_slice_clear_kernel zeroes the cells just before, on the
+// same stream, so the workspace keeps no state between calls.
+constexpr int kSliceTiles = 4;
+constexpr int kSliceRegVecs = 12;  // of the 16 vectors a thread owns; the other 4 go to LDS
+constexpr int kSliceMax = 64;      // slices per unit (one polling lane each)
+constexpr int kSliceHead = 16;     // workspace words before the first cell (128 B)
+
+struct SliceSync {
+  unsigned long long* cells;  // word 0: fallback flag; unit u's cell at kSliceHead + u * cell_words
+  int slices;                 // slices per unit, <= kSliceMax
+  int tps;                    // tiles per slice, <= kSliceTiles
+  int cell_words;             // slices rounded up to 16 (whole 128 B lines per unit)
+  unsigned int wait_ticks;    // bound of the wait for the unit's other slices
+};
+
+__global__ __launch_bounds__(256) void fp8_slice_clear_kernel(unsigned long long* cells, int n_words) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n_words; i += gridDim.x * 256) cells[i] = 0ull;
+}
+
+__device__ inline float e4m3_in(uint32_t w, bool hi, float inv) {
+  const float x = __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
+  return fminf(fmaxf(x * inv, -448.0f), 448.0f);
+}
+
+// One slice (K when !V, V^T when V): load, reduce, publish, wait, encode.
+template <bool V>
+__device__ __forceinline__ void fp8_slice(const AppendArgs& a, const SliceSync& sy, int unit, int s,
+                                          int h, int b, int f, uint8_t (*stage)[256 * 16], float* red) {
+  const int t0 = s * sy.tps;
+  const int nt = min(sy.tps, a.ntiles - t0);
+  const int row0 = t0 * kTile;
+  const int live = min(a.T - row0, nt * kTile);  // >= 1: t0 < ntiles = ceil(T / 64)
+  const int tid = threadIdx.x;
+  // lane part and uniform part of vector j's row within the slice
+  const int lrow = V ? 8 * (tid & 15) : tid >> 4;
+  const int lcol = V ? 8 * (tid >> 4) : 8 * (tid & 15);
+  auto urow = [](int j) { return V ? 128 * (j >> 3) + (j & 7) : 64 * (j >> 2) + 16 * (j & 3); };
+  const bf16* src = static_cast<const bf16*>(V ? a.vsrc : a.ksrc) + (int64_t)b * a.s_sb +
+                    (int64_t)h * a.s_sh + ((int64_t)(a.src_frame0 + f) * a.T + row0) * a.s_st;
+  // the host guarantees a slice spans < 2^31 bytes: one 32-bit lane offset per thread, the
+  // row offsets of vector j are uniform (scalar offset of the buffer load)
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, 0x7fffffff, 0x00020000);
+  const uint32_t lane_off = (uint32_t)(lrow * a.s_st + lcol) * 2u;
+  const uint32_t rstep = (uint32_t)a.s_st * 2u;
+#pragma unroll
+  for (int c = 0; c < 16 - kSliceRegVecs; ++c) {
+    const int j = kSliceRegVecs + c;
+    if (lrow < live - urow(j))
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(&stage[c][0] + (tid >> 6) * 1024),
+                                               16, lane_off, urow(j) * rstep, 0, 0);
+  }
+  u32x4 r[kSliceRegVecs];
+#pragma unroll
+  for (int j = 0; j < kSliceRegVecs; ++j) {
+    r[j] = u32x4{0u, 0u, 0u, 0u};
+    if (lrow < live - urow(j))
+      r[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, urow(j) * rstep, 0));
+  }
+  // vector j wherever it lives, zero for rows >= T.  The LDS reads are volatile:
+  // each phase reads the staged vectors again rather than keep 16 more registers live.
+  auto vec = [&](int j) -> u32x4 {
+    if (j < kSliceRegVecs) return r[j];
+    if (lrow >= live - urow(j)) return u32x4{0u, 0u, 0u, 0u};
+    typedef __attribute__((address_space(3))) const volatile u32x4 lds_u32x4;
+    const u32x4 x = *(lds_u32x4*)(__attribute__((address_space(3))) const uint8_t*)
+                         &stage[j - kSliceRegVecs][tid * 16];
+    return x;
+  };
+  u16x2 mm = {0, 0};
+#pragma unroll
+  for (int j = 0; j < kSliceRegVecs; ++j) mm = absmax8(r[j], mm);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS vectors have landed
+#pragma unroll
+  for (int j = kSliceRegVecs; j < 16; ++j) {  // one staged vector at a time
+    mm = absmax8(vec(j), mm);
+    asm volatile("" : "+v"(mm) : : "memory");
+  }
+  float m = __uint_as_float((uint32_t)(mm[0] > mm[1] ? mm[0] : mm[1]) << 16);
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  if (tid < 64) {  // wave 0: publish, then lane l < slices polls slice l's word
+    unsigned long long* cell = sy.cells + kSliceHead + (int64_t)unit * sy.cell_words;
+    if (tid == 0) {
+      const float ms = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+      __hip_atomic_store(cell + s, (1ull << 32) | __float_as_uint(ms), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const uint64_t t_end = __builtin_amdgcn_s_memrealtime() + sy.wait_ticks;
+    unsigned long long w = 0;
+    bool have = tid >= sy.slices;
+    bool late = false;
+    for (;;) {
+      if (!have) {
+        w = __hip_atomic_load(cell + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        have = (w >> 32) != 0;
+      }
+      if (__all(have)) break;
+      if (__builtin_amdgcn_s_memrealtime() >= t_end) {
+        late = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    float um = __uint_as_float((uint32_t)w);  // 0 for lanes past the unit's slices
+    for (int off = 32; off > 0; off >>= 1) um = fmaxf(um, __shfl_xor(um, off));
+    if (tid == 0) red[4] = late ? -1.0f : um;
+  }
+  __syncthreads();
+  if (red[4] < 0.f) {  // the unit did not complete in time (uniform branch): read all of it
+    // (rows [0, T) of the frame), then load this slice's register vectors again, so they need
+    // no registers while the whole-unit loop runs; the LDS vectors are still in place
+    const bf16* fsrc = src - (int64_t)row0 * a.s_st;
+    u16x2 fm = {0, 0};
+    for (int c = tid; c < a.T * 16; c += 256)
+      fm = absmax8(ld_nt(fsrc + (int64_t)(c >> 4) * a.s_st + (c & 15) * 8), fm);
+    float x = __uint_as_float((uint32_t)(fm[0] > fm[1] ? fm[0] : fm[1]) << 16);
+    for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    __syncthreads();  // every read of red[0..4] above is done
+    if ((tid & 63) == 0) red[tid >> 6] = x;
+    __syncthreads();
+    if (tid == 0) {
+      red[4] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+      __hip_atomic_store(sy.cells, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int j = 0; j < kSliceRegVecs; ++j) {
+      r[j] = u32x4{0u, 0u, 0u, 0u};
+      if (lrow < live - urow(j))
+        r[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, urow(j) * rstep, 0));
+    }
+    __syncthreads();
+  }
+  const float amax = red[4];
+  const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+  const int64_t slot = a.slots[f];
+  if (s == 0 && tid == 0) {
+    float* sc = V ? a.vscale : a.kscale;
+    sc[(slot * a.B + b) * a.H + h] = amax / 448.0f;
+  }
+  // codes go out through a buffer resource over the (slot, b, h) block (Tp x 128 bytes):
+  // lane offset in one VGPR, the vector's uniform offset scalar, nontemporal (aux bit 1)
+  uint8_t* pool = static_cast<uint8_t*>(V ? a.vpool : a.kpool) + slot * a.slot_stride +
+                  (int64_t)(b * a.H + h) * a.Tp * kHeadDim;
+  const __amdgpu_buffer_rsrc_t ps =
+      __builtin_amdgcn_make_buffer_rsrc((void*)pool, (short)0, a.Tp * kHeadDim, 0x00020000);
+  const int rows = nt * kTile;  // the slice's pool rows, padding (code 0) included
+  if (!V) {
+    const uint32_t st_lane = (uint32_t)((row0 + lrow) * kHeadDim + lcol);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (lrow < rows - urow(j))
+        __builtin_amdgcn_raw_buffer_store_b64(quant8(vec(j), inv), ps, st_lane, urow(j) * kHeadDim, 2);
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int tok = 128 * k + lrow;
+    if (tok >= rows) continue;
+    u32x4 x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = vec(8 * k + i);
+    const uint32_t st_lane = (uint32_t)(lcol * a.Tp + row0 + tok);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int w = c >> 1;
+      const bool hi = c & 1;
+      const u32x2 q{e4m3x4(e4m3_in(x[0][w], hi, inv), e4m3_in(x[1][w], hi, inv),
+                           e4m3_in(x[2][w], hi, inv), e4m3_in(x[3][w], hi, inv)),
+                    e4m3x4(e4m3_in(x[4][w], hi, inv), e4m3_in(x[5][w], hi, inv),
+                           e4m3_in(x[6][w], hi, inv), e4m3_in(x[7][w], hi, inv))};
+      __builtin_amdgcn_raw_buffer_store_b64(q, ps, st_lane, c * a.Tp, 2);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void append_fp8_slice_kernel(AppendArgs a, SliceSync sy) {
+  __shared__ __attribute__((aligned(16))) uint8_t stage[16 - kSliceRegVecs][256 * 16];
+  __shared__ float red[5];
+  const int unit = blockIdx.x / sy.slices;
+  const int s = blockIdx.x - unit * sy.slices;
+  int wg = unit >> 1;
+  const int h = wg % a.H;
+  wg /= a.H;
+  const int b = wg % a.B;
+  const int f = wg / a.B;
+  if (unit & 1)
+    fp8_slice<true>(a, sy, unit, s, h, b, f, stage, red);
+  else
+    fp8_slice<false>(a, sy, unit, s, h, b, f, stage, red);
+}
+
 // Inverse RMS of each token's H x D row (WanRMSNorm's statistic, model.py:69-84):
 // out[b * rows + t] = 1 / sqrt(mean(x^2) + eps) in fp32.  One wave per token: lane l sums the
 // squares of 8-element chunks l, l+64, ... of the row (chunk c = head c / 16, channels
@@ -777,6 +995,42 @@ __global__ __launch_bounds__(256) void gather_u8_kernel(GatherArgs a) {
 
 using namespace skv;
 
+// Tiles per slice of the one-pass fp8 append for `units` units of `ntiles` tiles: the fewest
+// that let every slice be resident at once (workgroups of append_fp8_slice_kernel per CU, from
+// the occupancy query, times the CUs), or 0 when more than kSliceTiles would be needed.
+static int slice_tiles(int ntiles, int units) {
+  static int per_cu = -1;
+  if (per_cu < 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, (const void*)append_fp8_slice_kernel, 256, 0) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      nb = 0;
+    }
+    per_cu = nb;
+  }
+  const int64_t resident = (int64_t)per_cu * cu_count();
+  for (int tps = 1; tps <= kSliceTiles; ++tps) {
+    const int slices = (ntiles + tps - 1) / tps;
+    if (slices <= kSliceMax && (int64_t)units * slices <= resident) return tps;
+  }
+  return 0;
+}
+
+// Bound of the one-pass append's wait, in ticks of the 100 MHz real-time counter: 200 us (the
+// whole C5 chunk loads in ~20 us), or SOLARKV_SLICE_WAIT_US, read on every call, so that tests
+// can force the fallback from the host (0 = never wait).
+static unsigned int slice_wait_ticks() {
+  const char* e = getenv("SOLARKV_SLICE_WAIT_US");
+  long us = 200;
+  if (e && *e) {
+    char* end = nullptr;
+    const long v = strtol(e, &end, 10);
+    if (end && *end == 0 && v >= 0 && v <= 10000000) us = v;
+  }
+  return (unsigned int)(us * 100);
+}
+
 static bool aligned8(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)(8 * bytes)) == 0; }
 
 static int append_impl(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
@@ -896,21 +1150,24 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
     }
     a.slots[f] = dst_slots[f];
   }
-  // fp8 chunks with too few (frame, batch, head, K|V) units to fill the chip split them into
-  // 64-token tiles; the tile maxima live in the caller's workspace (one float per tile).
+  // fp8 chunks with too few (frame, batch, head, K|V) units to fill the chip split them: into
+  // resident slices (one pass, the units' cells in the caller's workspace) when the slices fit
+  // the chip at once, else into 64-token tiles (two passes, one float per tile).
   const int units = n_frames * batch * heads * 2;
-  const int64_t tile_bytes = fp8 && units < 4 * cu_count()
-                                 ? (int64_t)units * a.ntiles * (int64_t)sizeof(float) : 0;
+  const bool few_units = fp8 && units < 4 * cu_count();
+  const int64_t tile_bytes = few_units ? (int64_t)units * a.ntiles * (int64_t)sizeof(float) : 0;
+  const int64_t cell_bytes = few_units ? (kSliceHead + (int64_t)units * kSliceMax) * 8 : 0;
+  const int64_t ws_need = tile_bytes > cell_bytes ? tile_bytes : cell_bytes;
   if (ws_query) {
-    *ws_query = tile_bytes;
+    *ws_query = ws_need;
     return SKV_OK;
   }
   bool tile_split = false;
-  if (tile_bytes > 0 && workspace != nullptr) {
-    if (workspace_bytes < tile_bytes) {
+  if (ws_need > 0 && workspace != nullptr) {
+    if (workspace_bytes < ws_need) {
       set_error("skv_append_ex: workspace of %lld bytes is smaller than the %lld this fp8 append "
                 "needs (skv_append_workspace_size)", (long long)workspace_bytes,
-                (long long)tile_bytes);
+                (long long)ws_need);
       return SKV_E_ARG;
     }
     if (reinterpret_cast<uintptr_t>(workspace) % 4) {
@@ -921,6 +1178,25 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fp8) {
+    // the one-pass kernel: bf16 sources without the K norm, token rows at least a head apart,
+    // a slice spanning < 2^31 bytes, 8-byte aligned cells (else the tile grids below)
+    if (tile_split && src_dtype == SKV_BF16 && !k_inv_rms && src_st >= kHeadDim &&
+        (int64_t)kSliceTiles * kTile * src_st * 2 < ((int64_t)1 << 31) &&
+        reinterpret_cast<uintptr_t>(workspace) % 8 == 0) {
+      SliceSync sy;
+      sy.cells = static_cast<unsigned long long*>(workspace);
+      sy.tps = slice_tiles(a.ntiles, units);
+      sy.slices = sy.tps > 0 ? (a.ntiles + sy.tps - 1) / sy.tps : 0;
+      sy.cell_words = (sy.slices + 15) / 16 * 16;
+      sy.wait_ticks = slice_wait_ticks();
+      if (sy.tps > 0) {
+        const int n_words = kSliceHead + units * sy.cell_words;
+        hipLaunchKernelGGL(fp8_slice_clear_kernel, dim3((n_words + 255) / 256), dim3(256), 0, s,
+                           sy.cells, n_words);
+        hipLaunchKernelGGL(append_fp8_slice_kernel, dim3(units * sy.slices), dim3(256), 0, s, a, sy);
+        return SKV_OK;
+      }
+    }
     if (tile_split) {
       float* part = static_cast<float*>(workspace);
       dim3 tgrid(units * a.ntiles);

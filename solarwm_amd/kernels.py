@@ -253,7 +253,8 @@ def prepare_append(
     ``k_norm = (inv_rms, weight)`` stores RMS-normalised K (``rms_rows`` of ``k_new`` and the
     norm's float32 weight); every copy and fp8 code derives from the normalised value.
     ``use_workspace=False`` keeps an fp8 append of few units on the per-unit kernels (no
-    scratch); by default it takes the tile-grid kernels with this stream's workspace."""
+    scratch); by default it takes the one-pass slice kernel (bf16 sources without ``k_norm``)
+    or the tile-grid kernels, with this stream's workspace."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("k_new", k_new)
@@ -336,6 +337,7 @@ def append_frames(
     vr_pool: torch.Tensor | None = None,
     kv_xform: torch.Tensor | None = None,
     k_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
+    use_workspace: bool = True,
 ) -> None:
     """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``
     (and, with ``kr_pool``, K with its height/width RoPE pairs rotated into ``kr_pool``; with
@@ -343,7 +345,7 @@ def append_frames(
     prepare_append(k_new, v_new, kpool, vpool, dst_slots, frame_tokens=frame_tokens,
                    src_frame0=src_frame0, kscale=kscale, vscale=vscale, kr_pool=kr_pool,
                    rope_hw=rope_hw, grid_hw=grid_hw, vr_pool=vr_pool, kv_xform=kv_xform,
-                   k_norm=k_norm)()
+                   k_norm=k_norm, use_workspace=use_workspace)()
 
 
 def prepare_gather(

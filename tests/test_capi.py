@@ -274,8 +274,11 @@ def test_append_workspace_query():
         assert lib.skv_append_workspace_size(ctypes.byref(d), ctypes.byref(out)) == _lib.SKV_OK
         return out.value
 
-    # C5: 3 frames x 4 streams x 12 heads x (K, V) = 288 units of 25 tiles, one float per tile
-    assert need(4, 12, 1560, _lib.SKV_FP8_E4M3) == 288 * 25 * 4
+    # C5: 3 frames x 4 streams x 12 heads x (K, V) = 288 units: the larger of the one-pass
+    # kernel's cells (a 128 B header + up to 512 B per unit) and the tile grids' maxima (one
+    # float per 64-token tile, 25 per unit)
+    assert need(4, 12, 1560, _lib.SKV_FP8_E4M3) == max(128 + 288 * 512, 288 * 25 * 4)
+    assert need(1, 2, 8000, _lib.SKV_FP8_E4M3) == max(128 + 12 * 512, 12 * 125 * 4)
     assert need(4, 12, 1560, _lib.SKV_BF16) == 0
     assert need(16, 24, 1560, _lib.SKV_FP8_E4M3) == 0  # 2304 units fill the chip per unit
     assert lib.skv_append_workspace_size(None, None) == _lib.SKV_E_ARG

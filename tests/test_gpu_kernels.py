@@ -97,6 +97,60 @@ def test_fp8_append_matches_oracle(gpu, src_dtype, B, H, T, wide):
             assert int(pad.view(torch.uint8).count_nonzero()) == 0, (f, vt)  # rows T..Tp-1
 
 
+@pytest.mark.parametrize("B,T,forced", [(4, 1560, False), (3, 1560, False), (2, 1560, False),
+                                        (4, 1000, False), (1, 1560, False), (4, 1560, True),
+                                        (1, 1560, True)])
+def test_fp8_append_one_pass_slices(gpu, monkeypatch, B, T, forced):
+    """Config-5 chunks (3 frames x B streams x 12 heads) take the one-pass kernel, whose slices
+    are 4 / 3 / 2 / 3 / 1 tiles long here (T=1000: a 40-row last tile inside the last slice).
+    Codes and scales equal the oracle's and the per-unit kernels', stale slot bytes and padding
+    rows are overwritten.  Unforced, every unit completes within the wait (workspace flag word
+    0); ``forced`` sets the wait bound to 0 from the host, so workgroups that find their unit
+    incomplete take the fallback (re-read the whole unit) and the results must not change."""
+    H, nf = 12, 3
+    _say("fp8 append one pass", B, H, T, nf, "forced fallback" if forced else "")
+    if forced:
+        monkeypatch.setenv("SOLARKV_SLICE_WAIT_US", "0")
+    g = torch.Generator().manual_seed(40 + B)
+    x = torch.randn((B, nf * T, H, 128), generator=g)
+    x[..., torch.randperm(128, generator=g)[:3]] *= 25.0
+    x[0, T : 2 * T, 5] = 0.0  # an all-zero (frame, head) in the middle frame
+    x[B - 1, 2 * T - 1, 7, 3] = 900.0  # the absmax sits in the frame's last row
+    x = x.to(torch.bfloat16)
+    v = (x.float() * 0.75 - 0.1).to(torch.bfloat16)
+    xd, vd = x.to(gpu), v.to(gpu)
+    slots = [4, 0, 2]
+    outs = []
+    for use_ws in (True, False):
+        kpool, vpool, ks, vs = kernels.new_pools(6, B, H, T, torch.float8_e4m3fn, gpu)
+        kpool.view(torch.uint8).fill_(0x55), vpool.view(torch.uint8).fill_(0x55)
+        ks.fill_(7.0), vs.fill_(7.0)
+        kernels.append_frames(xd, vd, kpool, vpool, slots, frame_tokens=T, kscale=ks, vscale=vs,
+                              use_workspace=use_ws)
+        torch.cuda.synchronize()
+        if use_ws:  # word 0 of this stream's workspace: the one-pass kernel's fallback flag
+            ws = kernels._workspaces[(gpu.index or 0, kernels._stream(gpu))]
+            flag = int(ws[:8].view(torch.int64).item())
+            assert flag == (1 if forced else 0), \
+                f"fallback flag {flag:#x} (not 0/1: the one-pass kernel was not taken)"
+        outs.append([t.cpu() for t in (kpool, vpool, ks, vs)])
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.uint8) if a.dtype != torch.float32 else a,
+                           b.view(torch.uint8) if b.dtype != torch.float32 else b)
+    kpool, vpool, ks, vs = outs[0]
+    for f, s in enumerate(slots):
+        for src, pool, sc, vt in ((x, kpool, ks, False), (v, vpool, vs, True)):
+            frame = src[:, f * T : (f + 1) * T].permute(0, 2, 1, 3)
+            codes, scale = ref.fp8_quantize(frame)
+            got = pool[s]
+            got = got[..., :T].transpose(-1, -2) if vt else got[:, :, :T]
+            assert torch.equal(got.view(torch.uint8), codes.view(torch.uint8)), (f, vt)
+            assert torch.equal(sc[s], scale), (f, vt)
+            pad = pool[s][..., T:] if vt else pool[s][:, :, T:]
+            assert int(pad.view(torch.uint8).count_nonzero()) == 0, (f, vt)
+    assert torch.equal(kpool[1].view(torch.uint8), torch.full_like(kpool[1].view(torch.uint8), 0x55))
+
+
 def _pool_from(k, v, T, dtype, device, perm_seed=0):
     """Store dense K/V [B, n*T, H, D] frame by frame in shuffled slots; return pools + order."""
     B, L, H, _ = k.shape
