@@ -316,6 +316,10 @@ typedef struct skv_launch_plan {
   int n_workgroups;        /* workgroups of the attention kernel launches (both, for split 2) */
   int n_qtiles;            /* query tiles (over all batches and heads) */
   int64_t workspace_bytes; /* workspace the split needs; 0 when it does not pay */
+  int key_tiles;           /* 64-key tiles per query tile over the whole window: n_frames x
+                              ceil(T / 64), or ceil(n_frames x T / 64) when the bf16 / f16
+                              kernel packs tiles across frame boundaries (whole frames, T a
+                              multiple of 8 but not of 64, no RoPE): no padding keys computed */
 } skv_launch_plan;
 
 int skv_attention_plan(const skv_attention_desc* desc, skv_launch_plan* plan);

@@ -74,7 +74,7 @@ class LaunchPlan(ctypes.Structure):
 
     _fields_ = [
         ("waves_per_group", _i32), ("split", _i32), ("n_workgroups", _i32), ("n_qtiles", _i32),
-        ("workspace_bytes", _i64),
+        ("workspace_bytes", _i64), ("key_tiles", _i32),
     ]
 
 

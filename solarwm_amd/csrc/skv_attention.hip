@@ -36,6 +36,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 #include "skv_common.h"
 
 namespace skv {
@@ -51,6 +53,13 @@ struct AttnArgs {
   int64_t o_sb, o_st, o_sh;
   int64_t slot_stride;
   int B, H, Lq, T, Tp, n_frames, ntiles_f, n_qtiles, n_wg;
+  // key tiles per q-tile: n_frames * ntiles_f, or ceil(n_keys / 64) when the tiles are packed
+  // across frame boundaries (attn_kernel<..., PK = true>)
+  int nt;
+  int packed;  // 1: the bf16 / f16 kernels run their packed-tile instance
+  // bytes of each pool when packed (< 4 GB): the range of the packed kernel's buffer descriptors,
+  // so that no offset can reach past the pool
+  uint32_t pool_bytes;
   float scale_log2;  // softmax_scale * log2(e)
   int mask_mode;
   int64_t q_pos0, chunk, n_keys;
@@ -80,7 +89,7 @@ struct AttnArgs {
   // wave-uniform index reads it with a scalar load.
   int32_t flen[SKV_MAX_FRAMES];
   // Balanced key split (no mask, 8-wave groups): the n_wg workgroups share the
-  // units = B*H*n_qtiles*nt (q-tile, key tile) pairs equally, nt = n_frames*ntiles_f; workgroup i
+  // units = B*H*n_qtiles*nt (q-tile, key tile) pairs equally; workgroup i
   // takes units [i*units/n_wg, (i+1)*units/n_wg) in q-tile order.  A q-tile that one workgroup
   // covers whole is written directly; a part of a split q-tile goes to record 2i (the
   // workgroup's first segment) or 2i+1 (its last) of part_o / part_ml, and attn_combine_kernel
@@ -182,6 +191,38 @@ struct TileWalk {
   }
 };
 
+// Walks 64-key tiles packed across frame boundaries: tile g holds keys [64 g, 64 g + 64) of the
+// window (frames of T tokens end to end, no padding keys), so it may straddle frames j and j + 1:
+// its first T - t0 keys are tokens t0.. of frame j, the rest tokens 0.. of frame j + 1.  Offsets
+// are bytes from the pool's start (the host packs only pools under 4 GB), read when the walk
+// enters frame j; advancing by one tile costs a few scalar ops.  Past the last frame, off_n
+// repeats off (the keys there are masked and their rows are only read, in bounds, so that the
+// staged values stay finite).  Every member is wave-uniform.
+struct PackedWalk {
+  int j = 0, t0 = 0;
+  uint32_t off = 0, off_n = 0;  // byte offsets of frames j and j + 1's (b, h) blocks
+  __device__ void open(const AttnArgs& a, int64_t kbh) {
+    if (j < a.n_frames) {
+      off = (uint32_t)(((int64_t)a.slots[j] * a.slot_stride + kbh) * 2);
+      off_n = j + 1 < a.n_frames ? (uint32_t)(((int64_t)a.slots[j + 1] * a.slot_stride + kbh) * 2) : off;
+    }
+  }
+  __device__ void start(const AttnArgs& a, int64_t kbh, int g) {
+    const int key0 = g * kTile;
+    j = key0 / a.T;
+    t0 = key0 - j * a.T;
+    open(a, kbh);
+  }
+  __device__ void next(const AttnArgs& a, int64_t kbh) {
+    t0 += kTile;
+    if (t0 >= a.T) {
+      t0 -= a.T;
+      ++j;
+      open(a, kbh);
+    }
+  }
+};
+
 __device__ inline int64_t chunk_limit(int64_t pos, int64_t chunk, int64_t n_keys) {
   const int64_t lim = (pos / chunk + 1) * chunk;
   return lim < n_keys ? lim : n_keys;
@@ -221,6 +262,11 @@ struct TileLoader {
   uint32_t klane, vlane;  // byte offsets of this lane inside a block (buffer path)
   int wu, Tp;
   int lane16;
+  int kk_k;  // key (inside the tile) of this lane's K rows: the same in all of the wave's blocks
+  int hh8;   // first of the lane's 8 tokens inside a V^T block's 16-key step
+  // packed tiles: the lane's byte offset inside the tile for each of the wave's K / V^T blocks
+  // (lane part + block part), so that a load adds only the tile's offset
+  uint32_t kpk[kBpw], vpk[kBpw];
   __device__ void init(int w, int lane, int Tp_) {
     lane16 = lane * 16;
     Tp = Tp_;
@@ -231,6 +277,14 @@ struct TileLoader {
     voff = (int64_t)((b0 >> 2) * 32 + n) * Tp + (b0 & 3) * 16 + hh * 8;
     klane = (uint32_t)(key_perm(n) * kHeadDim + hh * 8) * 2u;
     vlane = (uint32_t)(n * Tp + hh * 8) * 2u;
+    kk_k = (b0 >> 3) * 32 + key_perm(n);
+    hh8 = hh * 8;
+#pragma unroll
+    for (int j = 0; j < kBpw; ++j) {  // after klane / vlane, which they extend
+      const int b = b0 + j;
+      kpk[j] = klane + (uint32_t)((b >> 3) * 32 * kHeadDim + (b & 7) * 16) * 2u;
+      vpk[j] = vlane + (uint32_t)((b >> 2) * 32 * Tp + (b & 3) * 16) * 2u;
+    }
   }
   // bf16 pools: one buffer descriptor per tile (base = the tile's first element), the lane's
   // byte offset in a VGPR that never changes, the block's offset in an SGPR.
@@ -266,6 +320,52 @@ struct TileLoader {
   }
   __device__ void stage(const KT* src, char* block) const {
     *reinterpret_cast<bf16x8*>(block + lane16) = Vec8<KT>::load(src).to_bf16();
+  }
+  // Packed tiles (2-byte pools), through one descriptor over the whole pool: the tile's keys
+  // kk < bnd come from frame j (byte offset oa of the tile's first key, token t0), the others
+  // from frame j + 1 (on: its first token's offset less bnd tokens, so that the same lane
+  // offsets apply).  A tile inside one frame (bnd >= 64) adds oa to each block's scalar offset;
+  // a straddling tile puts the lane's whole offset in its VGPR (formed modulo 2^32: a lane of
+  // frame j + 1 lies at least bnd tokens past `on`, so the sum is its true offset), the loads
+  // stay wave-uniform.  V^T's 8-token groups never straddle (T, t0 multiples of 8).
+  __device__ void issue_k_packed(const KT* pool, uint32_t nbytes, uint32_t oa, uint32_t on, int bnd,
+                                 char* dst) const {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the calling kernels' launch stubs
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)pool, (short)0, (int)nbytes, 0x00020000);
+    if (bnd >= kTile) {
+#pragma unroll
+      for (int j = 0; j < kBpw; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wu * kBpw + j) * kBlockBytes), 16,
+                                                 kpk[j], oa, 0, 0);
+    } else {
+      const uint32_t o = kk_k < bnd ? oa : on;
+#pragma unroll
+      for (int j = 0; j < kBpw; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wu * kBpw + j) * kBlockBytes), 16,
+                                                 kpk[j] + o, 0, 0, 0);
+    }
+#endif
+  }
+  __device__ void issue_v_packed(const KT* pool, uint32_t nbytes, uint32_t oa, uint32_t on, int bnd,
+                                 char* dst) const {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the calling kernels' launch stubs
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void*)pool, (short)0, (int)nbytes, 0x00020000);
+    if (bnd >= kTile) {
+#pragma unroll
+      for (int j = 0; j < kBpw; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wu * kBpw + j) * kBlockBytes), 16,
+                                                 vpk[j], oa, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kBpw; ++j) {
+        const int b = wu * kBpw + j;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + b * kBlockBytes), 16,
+                                                 vpk[j] + ((b & 3) * 16 + hh8 < bnd ? oa : on), 0, 0, 0);
+      }
+    }
+#endif
   }
 };
 
@@ -318,9 +418,12 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
     }
 }
 
-template <int NW, typename QT, typename KT, int RM, bool SPLIT = false>
+// PK: key tiles packed across frame boundaries (PackedWalk; whole frames of T = 8k tokens, 2-byte
+// pools, no RoPE): a window of n frames takes ceil(n T / 64) tiles instead of n ceil(T / 64).
+template <int NW, typename QT, typename KT, int RM, bool SPLIT = false, bool PK = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
+  static_assert(!PK || (RM == 0 && sizeof(KT) == 2), "packed tiles: 2-byte pools, no RoPE");
   constexpr int kBQ = NW * 32;
   using ET = typename OpOf<KT>::E;     // MFMA operand element
   using etx8 = typename OpOf<KT>::x8;
@@ -342,7 +445,7 @@ void attn_kernel(AttnArgs a) {
   // whole ones run first, then the last segment (key tiles from 0, in step with the other
   // workgroups, which all start at key tile 0), then the first (the tail of a q-tile, a fixed
   // number of tiles ahead of them): K/V tiles stay shared through L2 as in the unsplit grid.
-  const int nt = a.n_frames * a.ntiles_f;
+  const int nt = a.nt;
   int q_first = logical, nseg = 1;
   int64_t u0 = 0, u1 = 0;
   if constexpr (SPLIT) {
@@ -521,6 +624,7 @@ void attn_kernel(AttnArgs a) {
     const int jf = lim_hi / a.T;
     ntau = jf >= a.n_frames ? a.n_frames * a.ntiles_f
                             : jf * a.ntiles_f + (lim_hi - jf * a.T + kTile - 1) / kTile;
+    if constexpr (PK) ntau = (lim_hi + kTile - 1) / kTile;  // lim_hi <= n_keys
     if constexpr (SPLIT) ntau = te - tb;  // no mask: the segment's tiles
   }
 
@@ -576,8 +680,20 @@ void attn_kernel(AttnArgs a) {
     for (int y = 0; y < 2; ++y) pA[x][y] = OpOf<KT>::from(Vec8<float>::zero());
   f32x16 (&s_cur)[2] = sA;
   if (ntau > 0) {
-    loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
-    if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
+    if constexpr (PK) {
+      PackedWalk p;
+      p.start(a, kbh, tb);
+      loader.issue_k_packed(kpool, a.pool_bytes, p.off + p.t0 * (kHeadDim * 2), p.off_n - (a.T - p.t0) * (kHeadDim * 2),
+                            a.T - p.t0, kb_lds(0));
+      if (ntau > 1) {
+        p.next(a, kbh);
+        loader.issue_k_packed(kpool, a.pool_bytes, p.off + p.t0 * (kHeadDim * 2),
+                              p.off_n - (a.T - p.t0) * (kHeadDim * 2), a.T - p.t0, kb_lds(1));
+      }
+    } else {
+      loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
+      if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
+    }
     if constexpr (RM == 2) {
       issue_w(tb / a.ntiles_f);
       if (ntau > 1 && (tb + 1) % a.ntiles_f == 0) issue_w((tb + 1) / a.ntiles_f);
@@ -589,8 +705,13 @@ void attn_kernel(AttnArgs a) {
     __syncthreads();
     if constexpr (RM > 0) rot_q(tb / a.ntiles_f);
     qk_tile(kb_lds(0) + lane16, qf, s_cur);
-    int tok0, key0, tj;
-    if (tile_needs_mask(0, tok0, key0, tj)) mask_tile(s_cur, hh, tok0, tj, key0, lim_lane);
+    if constexpr (PK) {
+      const int key0 = tb * kTile;  // packed tiles hold no padding keys: only the limit masks
+      if (key0 + kTile > lim_lo) mask_tile(s_cur, hh, 0, 1 << 30, key0, lim_lane);
+    } else {
+      int tok0, key0, tj;
+      if (tile_needs_mask(0, tok0, key0, tj)) mask_tile(s_cur, hh, tok0, tj, key0, lim_lane);
+    }
     __syncthreads();  // K(0) read by every wave before its buffer takes K(2)
   }
 
@@ -605,9 +726,15 @@ void attn_kernel(AttnArgs a) {
   // Tiles addressed in step tau: K(tau+2) (kw), V(tau) (vw) and the mask / RoPE frame of
   // QK(tau+1) (mw); the walks advance one tile per step.
   TileWalk kw, vw, mw;
-  kw.start(a, kbh, tb + 2);
-  vw.start(a, kbh, tb);
-  mw.start(a, kbh, tb + 1);
+  [[maybe_unused]] PackedWalk kp, vp;
+  if constexpr (PK) {
+    kp.start(a, kbh, tb + 2);
+    vp.start(a, kbh, tb);
+  } else {
+    kw.start(a, kbh, tb + 2);
+    vw.start(a, kbh, tb);
+    mw.start(a, kbh, tb + 1);
+  }
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
                   etx8 (&pprev)[2][2], etx8 (&pb)[2][2]) __attribute__((always_inline)) {
     const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
@@ -636,8 +763,16 @@ void attn_kernel(AttnArgs a) {
     // (two each) at the step start (measured: C3 -2.4%, C2 unchanged or slower otherwise)
     constexpr int kLoadSlot = NW == 4 ? 1 : -1;
     auto issue_loads = [&]() {
-      if (tau + 2 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb), w);
-      loader.issue_v(vpool + vw.base + vw.t * kTile, vb_lds(cb), w);
+      if constexpr (PK) {
+        if (tau + 2 < ntau)
+          loader.issue_k_packed(kpool, a.pool_bytes, kp.off + kp.t0 * (kHeadDim * 2),
+                                kp.off_n - (a.T - kp.t0) * (kHeadDim * 2), a.T - kp.t0, kb_lds(cb));
+        loader.issue_v_packed(vpool, a.pool_bytes, vp.off + vp.t0 * 2, vp.off_n - (a.T - vp.t0) * 2, a.T - vp.t0,
+                              vb_lds(cb));
+      } else {
+        if (tau + 2 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb), w);
+        loader.issue_v(vpool + vw.base + vw.t * kTile, vb_lds(cb), w);
+      }
     };
     if (kLoadSlot < 0) issue_loads();
     if constexpr (RM == 2) {
@@ -766,12 +901,22 @@ void attn_kernel(AttnArgs a) {
     }
     l_run += lp;
     if (tau + 1 < ntau) {
-      int tok0, key0;
-      if (walk_needs_mask(mw, tok0, key0)) mask_tile(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
+      if constexpr (PK) {
+        const int key0 = (tb + tau + 1) * kTile;
+        if (key0 + kTile > lim_lo) mask_tile(s_nxt, hh, 0, 1 << 30, key0, lim_lane);
+      } else {
+        int tok0, key0;
+        if (walk_needs_mask(mw, tok0, key0)) mask_tile(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
+      }
     }
-    kw.next(a, kbh);
-    vw.next(a, kbh);
-    mw.next(a, kbh);
+    if constexpr (PK) {
+      kp.next(a, kbh);
+      vp.next(a, kbh);
+    } else {
+      kw.next(a, kbh);
+      vw.next(a, kbh);
+      mw.next(a, kbh);
+    }
     // K(tau+2) and V(tau) have landed; every wave is done with K(tau+1)'s and V(tau-1)'s
     // buffers (they take K(tau+3) and V(tau+1) next)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -967,7 +1112,7 @@ void attn_fp8_kernel(AttnArgs a) {
   }
   // Segments: key tiles [tb, te) of q-tile qg, as in attn_kernel (one whole q-tile unless split;
   // a split share runs its whole q-tiles, then its last segment, then its first).
-  const int nt = a.n_frames * a.ntiles_f;
+  const int nt = a.nt;
   int q_first = logical, nseg = 1;
   int64_t u0 = 0, u1 = 0;
   if constexpr (SPLIT) {
@@ -1323,7 +1468,7 @@ template <typename QT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   __shared__ int64_t recs[kMaxSplitWg];
   __shared__ int n_rec;
-  const int nt = a.n_frames * a.ntiles_f;
+  const int nt = a.nt;
   const int qg = blockIdx.x / (kSplitBQ / 8), rg = blockIdx.x % (kSplitBQ / 8);
   const int64_t x0 = (int64_t)qg * nt, x1 = x0 + nt - 1;
   auto lo = [&](int i) { return (int64_t)i * a.units / a.n_wg; };
@@ -1410,13 +1555,23 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     const bool qh = q_dtype == SKV_F16;
     if constexpr (NW == 8) {
       if (a.split) {
-        if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true>), grid, block, lds, s, a);
+        if (a.packed) {
+          if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true, true>), grid, block, lds, s, a);
+          else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true, true>), grid, block, lds, s, a);
+        } else {
+          if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true>), grid, block, lds, s, a);
+          else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true>), grid, block, lds, s, a);
+        }
         return;
       }
     }
-    if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0>), grid, block, lds, s, a);
-    else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0>), grid, block, lds, s, a);
+    if (a.packed) {
+      if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, false, true>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, false, true>), grid, block, lds, s, a);
+    } else {
+      if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0>), grid, block, lds, s, a);
+    }
     return;
   }
   if (pool_dtype == SKV_FP8_E4M3) {
@@ -1446,6 +1601,9 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
       } else if (rm == 1) {
         if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 1, true>), grid, block, lds, s, a);
         else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1, true>), grid, block, lds, s, a);
+      } else if (pool_dtype == SKV_BF16 && a.packed) {
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, true, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, true, true>), grid, block, lds, s, a);
       } else if (pool_dtype == SKV_BF16) {
         if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, true>), grid, block, lds, s, a);
         else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, true>), grid, block, lds, s, a);
@@ -1471,7 +1629,12 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
       hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1>), grid, block, lds_bytes, s, a);
     return;
   }
-  if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
+  if (pool_dtype == SKV_BF16 && a.packed) {
+    if (q_dtype == SKV_BF16)
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, false, true>), grid, block, lds_bytes, s, a);
+    else
+      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, false, true>), grid, block, lds_bytes, s, a);
+  } else if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
     hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0>), grid, block, lds_bytes, s, a);
   else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
     hipLaunchKernelGGL((attn_kernel<NW, bf16, float, 0>), grid, block, lds_bytes, s, a);
@@ -1597,7 +1760,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     return SKV_E_ARG;
   }
   if (q_len == 0) {
-    if (plan) *plan = skv_launch_plan{0, 0, 0, 0, 0};
+    if (plan) *plan = skv_launch_plan{0, 0, 0, 0, 0, 0};
     return SKV_OK;
   }
   AttnArgs a;
@@ -1631,6 +1794,24 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   a.Tp = padded_tokens(frame_tokens);
   a.n_frames = n_frames;
   a.ntiles_f = a.Tp / kTile;
+  // Packed key tiles: with whole frames whose token count is a multiple of 8 but not of 64, the
+  // bf16 / f16 kernel runs 64-key tiles across frame boundaries instead of padding each frame to
+  // a whole tile (C2: 512 tiles for 21 x 1560 keys instead of 525); V^T's 8-token groups stay
+  // inside one frame.  RoPE instances and fp8 / fp32 pools keep frame-aligned tiles (per-frame
+  // query rotations and scales; register staging).
+  // The packed kernel addresses each pool through one buffer descriptor with 32-bit offsets,
+  // so the pool must be smaller than 4 GB.
+  {
+    bool whole = true;
+    for (int j = 0; frame_lens && j < n_frames; ++j) whole &= frame_lens[j] == frame_tokens;
+    const int64_t pool_bytes = (int64_t)n_slots * batch * heads * a.Tp * kHeadDim * 2;
+    a.packed = (pool_dtype == SKV_BF16 || pool_dtype == SKV_F16) && !rope && whole &&
+               frame_tokens >= kTile && frame_tokens % 8 == 0 && frame_tokens % kTile != 0 &&
+               pool_bytes < ((int64_t)1 << 32) - 1;
+    a.pool_bytes = a.packed ? (uint32_t)pool_bytes : 0u;
+  }
+  a.nt = a.packed ? (int)(((int64_t)n_frames * frame_tokens + kTile - 1) / kTile)
+                  : n_frames * a.ntiles_f;
   // Workgroup shape: 8 waves (256 queries, 1 workgroup per CU) stages half the K/V bytes per
   // query of 4 waves (128 queries, 2 per CU) and measured ~4% faster per FLOP, but a grid that
   // barely spills into a second round of CUs leaves most of the chip idle; pick the shape with
@@ -1660,7 +1841,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   a.part_o = a.part_ml = nullptr;
   int64_t split_bytes = 0;
   int split_mode = 0;  // 1: every q-tile shares the CUs; 2: only the last round's q-tiles do
-  const int nt = n_frames * a.ntiles_f;
+  const int nt = a.nt;
   const int64_t qt8 = (int64_t)((q_len + kSplitBQ - 1) / kSplitBQ) * heads * batch;
   const int64_t units8 = qt8 * nt;
   if (mask_mode == SKV_MASK_NONE && nt >= 8 && units8 >= 4 * n_cu && n_cu <= kMaxSplitWg) {
@@ -1739,7 +1920,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   const int64_t full_wg = a.split == 2 ? (int64_t)(a.n_wg / n_cu) * n_cu : 0;
   if (plan) {
     *plan = skv_launch_plan{nw, a.split, a.split == 2 ? (int)full_wg + n_cu : a.n_wg,
-                            a.n_qtiles * heads * batch, split_bytes};
+                            a.n_qtiles * heads * batch, split_bytes, a.nt};
     return SKV_OK;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -507,7 +507,8 @@ def attention_plan(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
                    frame_slots: Sequence[int], *, use_workspace: bool = True,
                    **kw) -> dict[str, int]:
     """The launch :func:`attention_frames` makes for these arguments (``skv_attention_plan``):
-    ``waves_per_group``, ``split``, ``n_workgroups``, ``n_qtiles``, ``workspace_bytes``."""
+    ``waves_per_group``, ``split``, ``n_workgroups``, ``n_qtiles``, ``workspace_bytes``,
+    ``key_tiles``."""
     lib = _lib.load()
     d, _, keep = attention_desc(q, kpool, vpool, frame_slots, **kw)
     plan = _lib.LaunchPlan()

@@ -253,6 +253,37 @@ def test_launch_plans_of_benchmark_shapes(name, B, H, Lq, T, nf, pool, want):
         assert b"aligned" in lib.skv_last_error()
 
 
+@pytest.mark.parametrize("name,B,H,Lq,T,nf,pool,want", [
+    # 64-key tiles per query tile: packed across frame boundaries for whole bf16 / f16 frames of
+    # T = 8k tokens (T not a multiple of 64), frame-aligned otherwise
+    ("c2", 1, 12, 4680, 1560, 21, _lib.SKV_BF16, 512),        # 32760 keys, not 21 x 25 = 525
+    ("c3", 1, 24, 2640, 880, 21, _lib.SKV_BF16, 289),         # 18480 keys, not 21 x 14 = 294
+    ("f16", 1, 2, 300, 72, 7, _lib.SKV_F16, 8),               # 504 keys, not 7 x 2 = 14
+    ("c5_fp8", 4, 12, 4680, 1560, 21, _lib.SKV_FP8_E4M3, 525),  # per-frame scales: aligned
+    ("f32", 1, 2, 390, 1560, 3, _lib.SKV_F32, 75),            # register staging: aligned
+    ("t100", 1, 2, 300, 100, 5, _lib.SKV_BF16, 10),           # T % 8 != 0: aligned
+    ("t128", 1, 2, 300, 128, 5, _lib.SKV_BF16, 10),           # no padding to remove
+])
+def test_plans_report_packed_key_tiles(name, B, H, Lq, T, nf, pool, want):
+    d, _keep = _attn_desc(B, H, Lq, T, nf, pool)
+    if pool == _lib.SKV_F16:
+        d.q_dtype = _lib.SKV_F16  # f16 pools multiply f16 (or f32) queries
+    assert _plan(d).key_tiles == want, name
+
+
+def test_packing_needs_a_pool_under_4gb_and_whole_frames():
+    # H40 x 1600 rows x 256 B = 16.4 MB per slot: 263 slots make a pool over 4 GB, 262 do not
+    d, _keep = _attn_desc(1, 40, 4680, 1560, 3)
+    assert _plan(d).key_tiles == 74  # ceil(3 x 1560 / 64)
+    d.n_slots = 263
+    assert _plan(d).key_tiles == 75
+    d.n_slots = 262
+    assert _plan(d).key_tiles == 74
+    lens = _slots(1560, 1000, 1560)  # a ragged frame keeps frame-aligned tiles
+    d.frame_lens = lens
+    assert _plan(d).key_tiles == 75
+
+
 def test_masked_launches_never_split():
     d, _keep = _attn_desc(1, 12, 1560, 1560, 21, mask=_lib.SKV_MASK_CHUNK_CAUSAL)
     d.workspace, d.workspace_bytes = 0x2000, SPLIT_BYTES
