@@ -333,16 +333,20 @@ struct TileLoader {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the calling kernels' launch stubs
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc((void*)pool, (short)0, (int)nbytes, 0x00020000);
+    // an opaque copy of the wave index: the blocks' LDS addresses are formed here, by scalar
+    // adds, instead of hoisted out of the main loop as 4 long-lived SGPRs per operand
+    int wq = wu;
+    asm volatile("" : "+s"(wq));
     if (bnd >= kTile) {
 #pragma unroll
       for (int j = 0; j < kBpw; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wu * kBpw + j) * kBlockBytes), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wq * kBpw + j) * kBlockBytes), 16,
                                                  kpk[j], oa, 0, 0);
     } else {
       const uint32_t o = kk_k < bnd ? oa : on;
 #pragma unroll
       for (int j = 0; j < kBpw; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wu * kBpw + j) * kBlockBytes), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wq * kBpw + j) * kBlockBytes), 16,
                                                  kpk[j] + o, 0, 0, 0);
     }
 #endif
@@ -352,16 +356,18 @@ struct TileLoader {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the calling kernels' launch stubs
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc((void*)pool, (short)0, (int)nbytes, 0x00020000);
+    int wq = wu;
+    asm volatile("" : "+s"(wq));
     if (bnd >= kTile) {
 #pragma unroll
       for (int j = 0; j < kBpw; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wu * kBpw + j) * kBlockBytes), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wq * kBpw + j) * kBlockBytes), 16,
                                                  vpk[j], oa, 0, 0);
     } else {
 #pragma unroll
       for (int j = 0; j < kBpw; ++j) {
-        const int b = wu * kBpw + j;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + b * kBlockBytes), 16,
+        const int b = wu * kBpw + j;  // wu: the lane-offset choice, a constant per block
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (wq * kBpw + j) * kBlockBytes), 16,
                                                  vpk[j] + ((b & 3) * 16 + hh8 < bnd ? oa : on), 0, 0, 0);
       }
     }
