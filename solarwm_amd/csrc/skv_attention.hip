@@ -1238,8 +1238,13 @@ void attn_fp8_kernel(AttnArgs a) {
       stage.loff[j] = db * kOp8 + p * 1024;
     }
   }
-  auto kb_lds = [&](int i) { return lds + i * kBuf; };
-  auto vb_lds = [&](int i) { return lds + (2 + i) * kBuf; };
+  // K and V^T tiles each cycle through kRing LDS buffers (tile x in buffer x mod kRing): a step
+  // reads K(tau+1) and V(tau-1) and loads K(tau+3) and V(tau+1), so the buffers a step writes
+  // were last read two steps earlier, and the workgroup meets at a barrier after every second
+  // step (odd tau) only.
+  constexpr int kRing = 4;
+  auto kb_lds = [&](int i) { return lds + (i & (kRing - 1)) * kBuf; };
+  auto vb_lds = [&](int i) { return lds + (kRing + (i & (kRing - 1))) * kBuf; };
 
   constexpr float kMaxPart8 = 448.0f;  // bound on every partial sum of scaled probabilities
   float sv_max = 0.f;
@@ -1263,31 +1268,36 @@ void attn_fp8_kernel(AttnArgs a) {
   // loop is unrolled twice), so no loop-carried copy is needed
   f32x16 sA[2], sB[2];
   i32x8 pA = {0, 0, 0, 0, 0, 0, 0, 0}, pB;
+  // Prologue: K(0), K(1), K(2) and V(0) resident, V(-1)'s buffer zeroed so PV(-1) of step 0 adds
+  // nothing; then QK(0).
+  TileWalk w0;  // tile 0 of the segment: V(0) and the scales of its frame
+  w0.start(a, kbh, tb);
   if (ntau > 0) {
     if (kload) stage(ktile(0), kb_lds(0));
     if (ntau > 1) if (kload) stage(ktile(1), kb_lds(1));
+    if (ntau > 2) if (kload) stage(ktile(2), kb_lds(2));
+    if (!kload) stage(vpool + w0.base + w0.t * kTile, vb_lds(0));
 #pragma unroll
     for (int r = 0; r < 8 / NW; ++r)
-      *reinterpret_cast<u32x4*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(vb_lds(-1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     qk64(kb_lds(0) + lane16, q8, zero16, sA);
     int tok0, key0, tj;
     if (tile_needs_mask(0, tok0, key0, tj)) mask_tile64(sA, hh, tok0, tj, key0, lim_lane);
-    __syncthreads();
+    __syncthreads();  // K(0) read by every wave before its buffer takes K(4)
   }
-  // Tiles addressed in step tau: K(tau+2) (kw), V(tau) and its frame's scales (vw), the mask of
-  // QK(tau+1) (mw); the walks advance one tile per step.
+  // Tiles addressed in step tau: K(tau+3) (kw), V(tau+1) (vw), the mask and the scales of
+  // tile tau+1 (mw); the walks advance one tile per step.
   TileWalk kw, vw, mw;
-  kw.start(a, kbh, tb + 2);
-  vw.start(a, kbh, tb);
+  kw.start(a, kbh, tb + 3);
+  vw.start(a, kbh, tb + 1);
   mw.start(a, kbh, tb + 1);
   // Per key frame: the softmax multiplier (K scale folded in) and the log and reciprocal of the
-  // P scale.  Set for the frame of tile tau+1 at the end of step tau, after the wait for the
-  // step's loads, so a register reload here cannot drain loads still in flight.
+  // P scale, for the frame of tile tau+1, set at the end of step tau.
   float mult = 0.f, log_pv = 0.f, inv_pv = 1.0f;
-  auto open_scales = [&]() {
-    const int64_t sc = (int64_t)vw.slot * a.B * a.H + sc_bh;
+  auto open_scales = [&](const TileWalk& sw) {
+    const int64_t sc = (int64_t)sw.slot * a.B * a.H + sc_bh;
     // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
     // masked (-inf) logits stay -inf instead of becoming NaN.  The scales are read through the
     // constant address space (scalar loads).
@@ -1301,14 +1311,15 @@ void attn_fp8_kernel(AttnArgs a) {
     log_pv = __builtin_amdgcn_logf(pv);
     inv_pv = __builtin_amdgcn_rcpf(pv);
   };
-  if (ntau > 0) open_scales();
-  // cb = tau & 1, passed as a literal so buffer addresses fold into immediate offsets
+  if (ntau > 0) open_scales(w0);
+  // cb = tau & 1, passed as a literal: the register sets alternate with it, and odd steps end
+  // at the barrier
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], const i32x8& pprev,
                   i32x8& pb) __attribute__((always_inline)) {
-    if (tau + 2 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb));
-    if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(cb));
-    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1)
-    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
+    if (tau + 3 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(tau + 3));
+    if (tau + 1 < ntau) if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(tau + 1));
+    const char* kl = kb_lds(tau + 1) + lane16;  // K(tau+1) (stale data on the last step)
+    const char* vl = vb_lds(tau - 1) + lane16;  // V(tau-1) (zeros on the first step)
 
     // Eight MFMA slots, QK(tau+1) and PV(tau-1) alternating (QK steps in the order (kb, cs) =
     // (0,0), (1,0), (0,1), (1,1), so the two halves of one key block are four slots apart), each
@@ -1399,22 +1410,27 @@ void attn_fp8_kernel(AttnArgs a) {
       const int tok0 = mw.t * kTile, key0 = mw.j * a.T + tok0;
       if ((tok0 + kTile > mw.flen) || (key0 + kTile > lim_lo))
         mask_tile64(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
+      if (mw.t == 0) open_scales(mw);  // tile tau+1 opens a key frame
     }
     kw.next(a, kbh);
     vw.next(a, kbh);
     mw.next(a, kbh);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (tau + 1 < ntau && vw.t == 0) open_scales();  // tile tau+1 opens a key frame
-    __syncthreads();
+    if (cb) {
+      // K(tau+2), K(tau+3), V(tau), V(tau+1) have landed; every wave is done with the buffers
+      // the next two steps load into
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
   };
   int tau = 0;
   for (; tau + 1 < ntau; tau += 2) {
     step(tau, 0, sA, sB, pA, pB);
     step(tau + 1, 1, sB, sA, pB, pA);
   }
-  // PV(ntau-1)
+  // PV(ntau-1): V(ntau-1) was loaded by step ntau-2 (the prologue when ntau = 1), two steps or
+  // a barrier earlier
   auto epilogue = [&](const i32x8& pprev) __attribute__((always_inline)) {
-    const char* vl = vb_lds((ntau - 1) & 1) + lane16;
+    const char* vl = vb_lds(ntau - 1) + lane16;
 #pragma unroll
     for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
   };
@@ -1584,16 +1600,16 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     if constexpr (NW == 8) {
       if (a.split) {
         if (q_dtype == SKV_BF16)
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 16 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 32 * kOp8, s, a);
         else
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 16 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 32 * kOp8, s, a);
         return;
       }
     }
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 16 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 32 * kOp8, s, a);
     else
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 16 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 32 * kOp8, s, a);
     return;
   }
   const size_t lds_bytes = 2 * kTileBytes;
