@@ -424,6 +424,17 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
     }
 }
 
+// K and V^T tile buffers of attn_kernel's ring: 4 (a barrier every second step) for 8-wave groups
+// over 2-byte pools without RoPE, 2 otherwise: 4-wave groups run two workgroups per CU, whose
+// 2 x 128 KB would not fit the 160 KB of LDS; the RoPE instances stage per-frame data for the
+// step after next; fp32 pools and the frame-aligned split spill registers with the longer ring.
+constexpr int attn_ring(int nw, int rm, int kt_bytes, bool split, bool pk) {
+  return nw == 8 && rm == 0 && kt_bytes == 2 && (pk || !split) ? 4 : 2;
+}
+constexpr size_t attn_lds_bytes(int nw, int rm, int kt_bytes, bool split, bool pk) {
+  return (size_t)attn_ring(nw, rm, kt_bytes, split, pk) * kTileBytes + (rm == 2 ? 2 * kWBuf : 0);
+}
+
 // PK: key tiles packed across frame boundaries (PackedWalk; whole frames of T = 8k tokens, 2-byte
 // pools, no RoPE): a window of n frames takes ceil(n T / 64) tiles instead of n ceil(T / 64).
 template <int NW, typename QT, typename KT, int RM, bool SPLIT = false, bool PK = false>
@@ -643,6 +654,10 @@ void attn_kernel(AttnArgs a) {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
     return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
   };
+  [[maybe_unused]] auto tile_vbase = [&](int tau) -> int64_t {  // the same tile of V^T
+    const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
+    return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile;
+  };
   // mask decision for tile tau (uniform): returns true if any key of the tile may be hidden
   auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
@@ -671,11 +686,17 @@ void attn_kernel(AttnArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
   const float c2 = a.scale_log2;
   const int lane16 = lane * 16;
-  // LDS map: K buffers at [0, 32 KB), V^T buffers at [32 KB, 64 KB).
-  auto kb_lds = [&](int i) { return lds + i * kHalf; };
-  auto vb_lds = [&](int i) { return lds + (2 + i) * kHalf; };
+  // LDS map: kRing K buffers, then kRing V^T buffers (tile x in buffer x mod kRing).  A step
+  // reads K(tau+1) and V(tau-1) and loads K(tau+kL+1) and V(tau+kL-1); the workgroup meets at a
+  // barrier after every kL-th step.  kL = 1 (two buffers each) for 4-wave groups (two
+  // workgroups share a CU's LDS) and the RoPE instances; plain 8-wave groups take kL = 2.
+  constexpr int kRing = attn_ring(NW, RM, (int)sizeof(KT), SPLIT, PK);
+  constexpr int kL = kRing / 2;
+  auto kb_lds = [&](int i) { return lds + (i & (kRing - 1)) * kHalf; };
+  auto vb_lds = [&](int i) { return lds + (kRing + (i & (kRing - 1))) * kHalf; };
 
-  // Prologue: K(0), K(1) resident; V buffer 1 zeroed so PV(-1) of iteration 0 adds nothing.
+  // Prologue: K(0..kL) and V(0..kL-2) resident; V(-1)'s buffer zeroed so PV(-1) of step 0 adds
+  // nothing.
   // Score and probability registers ping-pong between two sets (A, B) across iterations, so no
   // loop-carried copy is needed.
   f32x16 sA[2], sB[2];
@@ -689,16 +710,28 @@ void attn_kernel(AttnArgs a) {
     if constexpr (PK) {
       PackedWalk p;
       p.start(a, kbh, tb);
-      loader.issue_k_packed(kpool, a.pool_bytes, p.off + p.t0 * (kHeadDim * 2), p.off_n - (a.T - p.t0) * (kHeadDim * 2),
-                            a.T - p.t0, kb_lds(0));
-      if (ntau > 1) {
+#pragma unroll
+      for (int x = 0; x <= kL; ++x) {
+        if (x < ntau)
+          loader.issue_k_packed(kpool, a.pool_bytes, p.off + p.t0 * (kHeadDim * 2),
+                                p.off_n - (a.T - p.t0) * (kHeadDim * 2), a.T - p.t0, kb_lds(x));
         p.next(a, kbh);
-        loader.issue_k_packed(kpool, a.pool_bytes, p.off + p.t0 * (kHeadDim * 2),
-                              p.off_n - (a.T - p.t0) * (kHeadDim * 2), a.T - p.t0, kb_lds(1));
+      }
+      p.start(a, kbh, tb);
+#pragma unroll
+      for (int x = 0; x < kL - 1; ++x) {
+        if (x < ntau)
+          loader.issue_v_packed(vpool, a.pool_bytes, p.off + p.t0 * 2, p.off_n - (a.T - p.t0) * 2,
+                                a.T - p.t0, vb_lds(x));
+        p.next(a, kbh);
       }
     } else {
-      loader.issue_k(kpool + tile_base(0), kb_lds(0), w);
-      if (ntau > 1) loader.issue_k(kpool + tile_base(1), kb_lds(1), w);
+#pragma unroll
+      for (int x = 0; x <= kL; ++x)
+        if (x < ntau) loader.issue_k(kpool + tile_base(x), kb_lds(x), w);
+#pragma unroll
+      for (int x = 0; x < kL - 1; ++x)
+        if (x < ntau) loader.issue_v(vpool + tile_vbase(x), vb_lds(x), w);
     }
     if constexpr (RM == 2) {
       issue_w(tb / a.ntiles_f);
@@ -706,7 +739,7 @@ void attn_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < 16 / NW; ++r)
-      *reinterpret_cast<bf16x8*>(vb_lds(1) + (tid + NW * 64 * r) * 16) = Vec8<bf16>::zero().to_bf16();
+      *reinterpret_cast<bf16x8*>(vb_lds(-1) + (tid + NW * 64 * r) * 16) = Vec8<bf16>::zero().to_bf16();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if constexpr (RM > 0) rot_q(tb / a.ntiles_f);
@@ -718,7 +751,7 @@ void attn_kernel(AttnArgs a) {
       int tok0, key0, tj;
       if (tile_needs_mask(0, tok0, key0, tj)) mask_tile(s_cur, hh, tok0, tj, key0, lim_lane);
     }
-    __syncthreads();  // K(0) read by every wave before its buffer takes K(2)
+    __syncthreads();  // K(0) read by every wave before its buffer takes K(kRing)
   }
 
   // Iteration tau: QK(tau+1), softmax(tau) and PV(tau-1) are independent; their 32 MFMAs and
@@ -734,17 +767,19 @@ void attn_kernel(AttnArgs a) {
   TileWalk kw, vw, mw;
   [[maybe_unused]] PackedWalk kp, vp;
   if constexpr (PK) {
-    kp.start(a, kbh, tb + 2);
-    vp.start(a, kbh, tb);
+    kp.start(a, kbh, tb + kL + 1);
+    vp.start(a, kbh, tb + kL - 1);
   } else {
-    kw.start(a, kbh, tb + 2);
-    vw.start(a, kbh, tb);
+    kw.start(a, kbh, tb + kL + 1);
+    vw.start(a, kbh, tb + kL - 1);
     mw.start(a, kbh, tb + 1);
   }
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
                   etx8 (&pprev)[2][2], etx8 (&pb)[2][2]) __attribute__((always_inline)) {
-    const char* kl = kb_lds(cb ^ 1) + lane16;  // K(tau+1) (stale data on the last iteration)
-    const char* vl = vb_lds(cb ^ 1) + lane16;  // V(tau-1) (zeros on the first iteration)
+    // K(tau+1) (stale data on the last step) and V(tau-1) (zeros on the first step); with two
+    // buffers the literal cb = tau & 1 names them, so their addresses fold into immediates
+    const char* kl = (kRing == 2 ? kb_lds(cb ^ 1) : kb_lds(tau + 1)) + lane16;
+    const char* vl = (kRing == 2 ? vb_lds(cb ^ 1) : vb_lds(tau - 1)) + lane16;
     // operand of MFMA slot i: even i -> QK step i/2 (k = i/4, kb = (i/2)&1), odd i -> PV step i/2
     auto operand = [&](int i) -> etx8 {
       const int st = i >> 1;
@@ -768,16 +803,20 @@ void attn_kernel(AttnArgs a) {
     // after the first MFMA slot, so that MFMA starts sooner after the barrier; 8-wave groups
     // (two each) at the step start (measured: C3 -2.4%, C2 unchanged or slower otherwise)
     constexpr int kLoadSlot = NW == 4 ? 1 : -1;
+    // K(tau+kL+1) and V(tau+kL-1) (with two buffers: buffer cb, the literal)
+    char* const kdst = kRing == 2 ? kb_lds(cb) : kb_lds(tau + kL + 1);
+    char* const vdst = kRing == 2 ? vb_lds(cb) : vb_lds(tau + kL - 1);
     auto issue_loads = [&]() {
       if constexpr (PK) {
-        if (tau + 2 < ntau)
+        if (tau + kL + 1 < ntau)
           loader.issue_k_packed(kpool, a.pool_bytes, kp.off + kp.t0 * (kHeadDim * 2),
-                                kp.off_n - (a.T - kp.t0) * (kHeadDim * 2), a.T - kp.t0, kb_lds(cb));
-        loader.issue_v_packed(vpool, a.pool_bytes, vp.off + vp.t0 * 2, vp.off_n - (a.T - vp.t0) * 2, a.T - vp.t0,
-                              vb_lds(cb));
+                                kp.off_n - (a.T - kp.t0) * (kHeadDim * 2), a.T - kp.t0, kdst);
+        if (tau + kL - 1 < ntau)
+          loader.issue_v_packed(vpool, a.pool_bytes, vp.off + vp.t0 * 2, vp.off_n - (a.T - vp.t0) * 2,
+                                a.T - vp.t0, vdst);
       } else {
-        if (tau + 2 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(cb), w);
-        loader.issue_v(vpool + vw.base + vw.t * kTile, vb_lds(cb), w);
+        if (tau + kL + 1 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kdst, w);
+        if (tau + kL - 1 < ntau) loader.issue_v(vpool + vw.base + vw.t * kTile, vdst, w);
       }
     };
     if (kLoadSlot < 0) issue_loads();
@@ -923,19 +962,23 @@ void attn_kernel(AttnArgs a) {
       vw.next(a, kbh);
       mw.next(a, kbh);
     }
-    // K(tau+2) and V(tau) have landed; every wave is done with K(tau+1)'s and V(tau-1)'s
-    // buffers (they take K(tau+3) and V(tau+1) next)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    if (kL == 1 || cb == 1) {
+      // the loads of the last kL steps have landed; every wave is done with the buffers the
+      // next kL steps load into (read kL steps before those loads)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
   };
+  static_assert(kL == 1 || kL == 2, "the barrier test above assumes kL <= 2 (cb = tau & 1)");
   int tau = 0;
   for (; tau + 1 < ntau; tau += 2) {
     step(tau, 0, sA, sB, pA, pB);
     step(tau + 1, 1, sB, sA, pB, pA);
   }
-  // Epilogue: PV(ntau-1).
+  // Epilogue: PV(ntau-1); V(ntau-1) was loaded kL steps earlier (or by the prologue), with a
+  // barrier in between.
   auto epilogue = [&](const etx8 (&pprev)[2][2]) __attribute__((always_inline)) {
-    const char* vl = vb_lds((ntau - 1) & 1) + lane16;
+    const char* vl = vb_lds(ntau - 1) + lane16;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -1023,6 +1066,9 @@ void attn_kernel(AttnArgs a) {
 //     lane-contiguous 32 B layout costs a 2-way conflict on every read).  Direct buffer->LDS
 //     loads fill them: DMA lane i of part q writes operand lane i, bytes 16 q .. +16.
 constexpr int kOp8 = 2048;
+// K and V^T tile buffers of the fp8 kernel's ring: a barrier every kFp8Ring / 2 steps (8 measured
+// slower than 4 at C5: the waves drift further apart between barriers)
+constexpr int kFp8Ring = 4;
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 __device__ inline int key_perm64(int kb, int r) {
@@ -1242,7 +1288,8 @@ void attn_fp8_kernel(AttnArgs a) {
   // reads K(tau+1) and V(tau-1) and loads K(tau+3) and V(tau+1), so the buffers a step writes
   // were last read two steps earlier, and the workgroup meets at a barrier after every second
   // step (odd tau) only.
-  constexpr int kRing = 4;
+  constexpr int kRing = kFp8Ring;
+  constexpr int kL = kRing / 2;  // steps between barriers
   auto kb_lds = [&](int i) { return lds + (i & (kRing - 1)) * kBuf; };
   auto vb_lds = [&](int i) { return lds + (kRing + (i & (kRing - 1))) * kBuf; };
 
@@ -1273,10 +1320,17 @@ void attn_fp8_kernel(AttnArgs a) {
   TileWalk w0;  // tile 0 of the segment: V(0) and the scales of its frame
   w0.start(a, kbh, tb);
   if (ntau > 0) {
-    if (kload) stage(ktile(0), kb_lds(0));
-    if (ntau > 1) if (kload) stage(ktile(1), kb_lds(1));
-    if (ntau > 2) if (kload) stage(ktile(2), kb_lds(2));
-    if (!kload) stage(vpool + w0.base + w0.t * kTile, vb_lds(0));
+#pragma unroll
+    for (int x = 0; x <= kL; ++x)
+      if (x < ntau) if (kload) stage(ktile(x), kb_lds(x));
+    if (!kload) {
+      TileWalk wv = w0;
+#pragma unroll
+      for (int x = 0; x < kL - 1; ++x) {
+        if (x < ntau) stage(vpool + wv.base + wv.t * kTile, vb_lds(x));
+        wv.next(a, kbh);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 8 / NW; ++r)
       *reinterpret_cast<u32x4*>(vb_lds(-1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
@@ -1290,8 +1344,8 @@ void attn_fp8_kernel(AttnArgs a) {
   // Tiles addressed in step tau: K(tau+3) (kw), V(tau+1) (vw), the mask and the scales of
   // tile tau+1 (mw); the walks advance one tile per step.
   TileWalk kw, vw, mw;
-  kw.start(a, kbh, tb + 3);
-  vw.start(a, kbh, tb + 1);
+  kw.start(a, kbh, tb + kL + 1);
+  vw.start(a, kbh, tb + kL - 1);
   mw.start(a, kbh, tb + 1);
   // Per key frame: the softmax multiplier (K scale folded in) and the log and reciprocal of the
   // P scale, for the frame of tile tau+1, set at the end of step tau.
@@ -1316,8 +1370,8 @@ void attn_fp8_kernel(AttnArgs a) {
   // at the barrier
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], const i32x8& pprev,
                   i32x8& pb) __attribute__((always_inline)) {
-    if (tau + 3 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(tau + 3));
-    if (tau + 1 < ntau) if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(tau + 1));
+    if (tau + kL + 1 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(tau + kL + 1));
+    if (tau + kL - 1 < ntau) if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(tau + kL - 1));
     const char* kl = kb_lds(tau + 1) + lane16;  // K(tau+1) (stale data on the last step)
     const char* vl = vb_lds(tau - 1) + lane16;  // V(tau-1) (zeros on the first step)
 
@@ -1415,7 +1469,7 @@ void attn_fp8_kernel(AttnArgs a) {
     kw.next(a, kbh);
     vw.next(a, kbh);
     mw.next(a, kbh);
-    if (cb) {
+    if (kL == 2 ? cb == 1 : (tau & (kL - 1)) == kL - 1) {
       // K(tau+2), K(tau+3), V(tau), V(tau+1) have landed; every wave is done with the buffers
       // the next two steps load into
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1573,26 +1627,25 @@ template <int NW>
 static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipStream_t s) {
   dim3 grid(a.n_wg), block(NW * 64);
   if (pool_dtype == SKV_F16) {  // plain attention, f16 MFMAs; q f16 or f32 (checked by the caller)
-    const size_t lds = 2 * kTileBytes;
     const bool qh = q_dtype == SKV_F16;
     if constexpr (NW == 8) {
       if (a.split) {
         if (a.packed) {
-          if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true, true>), grid, block, lds, s, a);
-          else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true, true>), grid, block, lds, s, a);
+          if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, true), s, a);
+          else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, true), s, a);
         } else {
-          if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true>), grid, block, lds, s, a);
-          else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true>), grid, block, lds, s, a);
+          if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, false), s, a);
+          else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, false), s, a);
         }
         return;
       }
     }
     if (a.packed) {
-      if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, false, true>), grid, block, lds, s, a);
-      else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, false, true>), grid, block, lds, s, a);
+      if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0, false, true>), grid, block, attn_lds_bytes(NW, 0, 2, false, true), s, a);
+      else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0, false, true>), grid, block, attn_lds_bytes(NW, 0, 2, false, true), s, a);
     } else {
-      if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0>), grid, block, lds, s, a);
-      else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0>), grid, block, lds, s, a);
+      if (qh) hipLaunchKernelGGL((attn_kernel<NW, f16, f16, 0>), grid, block, attn_lds_bytes(NW, 0, 2, false, false), s, a);
+      else hipLaunchKernelGGL((attn_kernel<NW, float, f16, 0>), grid, block, attn_lds_bytes(NW, 0, 2, false, false), s, a);
     }
     return;
   }
@@ -1600,70 +1653,67 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     if constexpr (NW == 8) {
       if (a.split) {
         if (q_dtype == SKV_BF16)
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 32 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
         else
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 32 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
         return;
       }
     }
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 32 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
     else
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 32 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
     return;
   }
-  const size_t lds_bytes = 2 * kTileBytes;
   if constexpr (NW == 8) {
     if (a.split) {  // bf16 or fp32 pools, no mask (checked by the caller)
-      const size_t lds = lds_bytes + (rm == 2 ? 2 * kWBuf : 0);
       const bool qb = q_dtype == SKV_BF16;
       if (rm == 2) {
-        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 2, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 2, true>), grid, block, lds, s, a);
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 2, true>), grid, block, attn_lds_bytes(NW, 2, 2, true, false), s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 2, true>), grid, block, attn_lds_bytes(NW, 2, 2, true, false), s, a);
       } else if (rm == 1) {
-        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 1, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1, true>), grid, block, lds, s, a);
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 1, true>), grid, block, attn_lds_bytes(NW, 1, 2, true, false), s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1, true>), grid, block, attn_lds_bytes(NW, 1, 2, true, false), s, a);
       } else if (pool_dtype == SKV_BF16 && a.packed) {
-        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, true, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, true, true>), grid, block, lds, s, a);
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, true, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, true), s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, true, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, true), s, a);
       } else if (pool_dtype == SKV_BF16) {
-        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, true>), grid, block, lds, s, a);
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, false), s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, true>), grid, block, attn_lds_bytes(NW, 0, 2, true, false), s, a);
       } else {
-        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, float, 0, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((attn_kernel<NW, float, float, 0, true>), grid, block, lds, s, a);
+        if (qb) hipLaunchKernelGGL((attn_kernel<NW, bf16, float, 0, true>), grid, block, attn_lds_bytes(NW, 0, 4, true, false), s, a);
+        else hipLaunchKernelGGL((attn_kernel<NW, float, float, 0, true>), grid, block, attn_lds_bytes(NW, 0, 4, true, false), s, a);
       }
       return;
     }
   }
   if (rm == 2) {  // bf16 pools, frame_tokens >= 64 (checked by the caller)
-    const size_t lds_w = lds_bytes + 2 * kWBuf;
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 2>), grid, block, lds_w, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 2>), grid, block, attn_lds_bytes(NW, 2, 2, false, false), s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 2>), grid, block, lds_w, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 2>), grid, block, attn_lds_bytes(NW, 2, 2, false, false), s, a);
     return;
   }
   if (rm == 1) {  // bf16 pools only (checked by the caller)
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 1>), grid, block, lds_bytes, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 1>), grid, block, attn_lds_bytes(NW, 1, 2, false, false), s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1>), grid, block, lds_bytes, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 1>), grid, block, attn_lds_bytes(NW, 1, 2, false, false), s, a);
     return;
   }
   if (pool_dtype == SKV_BF16 && a.packed) {
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, false, true>), grid, block, lds_bytes, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0, false, true>), grid, block, attn_lds_bytes(NW, 0, 2, false, true), s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, false, true>), grid, block, lds_bytes, s, a);
+      hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0, false, true>), grid, block, attn_lds_bytes(NW, 0, 2, false, true), s, a);
   } else if (q_dtype == SKV_BF16 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, bf16, 0>), grid, block, attn_lds_bytes(NW, 0, 2, false, false), s, a);
   else if (q_dtype == SKV_BF16 && pool_dtype == SKV_F32)
-    hipLaunchKernelGGL((attn_kernel<NW, bf16, float, 0>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, float, 0>), grid, block, attn_lds_bytes(NW, 0, 4, false, false), s, a);
   else if (q_dtype == SKV_F32 && pool_dtype == SKV_BF16)
-    hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, float, bf16, 0>), grid, block, attn_lds_bytes(NW, 0, 2, false, false), s, a);
   else
-    hipLaunchKernelGGL((attn_kernel<NW, float, float, 0>), grid, block, lds_bytes, s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, float, float, 0>), grid, block, attn_lds_bytes(NW, 0, 4, false, false), s, a);
 }
 
 static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st,
