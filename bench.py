@@ -45,10 +45,10 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 HBM_PEAK_GBPS = 8000.0
 # HBM bytes per steady-state attention launch (Lq 4680 x Lk 32760, H12) measured with rocprofv3
-# on `bench.py --probe`: FETCH_SIZE x2.0 (341.52 MB) + WRITE_SIZE x1.0 (14.38 MB); the scale
+# on `bench.py --probe`: FETCH_SIZE x2.0 (337.45 MB) + WRITE_SIZE x1.0 (14.38 MB); the scale
 # factors are what the same counters read for a 1 GiB device copy.  Counters cannot be read
 # from inside the process, so the figure is recorded here for the config it was measured on.
-ATTN_TRAFFIC_BYTES = {"c2": 355.89e6}
+ATTN_TRAFFIC_BYTES = {"c2": 351.83e6}
 # Launch timing inside the timed rollout: HIP events around every 7th launch of each kind
 # (7 is coprime with the 150 launches of a chunk, so the samples rotate over layers and
 # passes).  A timing event waits for the work before it; events around every launch cost
@@ -1165,7 +1165,8 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "skv::attn_kernel<NW, bf16, bf16> (NW = 8 at config 2)" if cfg["cache"] == "bf16" else "skv::attn_fp8_kernel<NW, bf16>",
+            "kernel": ("skv::attn_kernel<8, bf16, bf16, 0, false, true> (8-wave groups, key tiles "
+                       "packed across frames)") if cfg["cache"] == "bf16" else "skv::attn_fp8_kernel<8, bf16>",
             "achieved": round(achieved, 2),
             "peak": peak,
             "unit": "TFLOP/s",
