@@ -425,11 +425,12 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
 }
 
 // K and V^T tile buffers of attn_kernel's ring: 4 (a barrier every second step) for 8-wave groups
-// over 2-byte pools without RoPE, 2 otherwise: 4-wave groups run two workgroups per CU, whose
-// 2 x 128 KB would not fit the 160 KB of LDS; the RoPE instances stage per-frame data for the
-// step after next; fp32 pools and the frame-aligned split spill registers with the longer ring.
+// over 2-byte pools without PRoPE, 2 otherwise: 4-wave groups run two workgroups per CU, whose
+// 2 x 128 KB would not fit the 160 KB of LDS; the PRoPE instance stages each key frame's matrices
+// for the step after next; fp32 pools and the frame-aligned split spill registers with the
+// longer ring.
 constexpr int attn_ring(int nw, int rm, int kt_bytes, bool split, bool pk) {
-  return nw == 8 && rm == 0 && kt_bytes == 2 && (pk || !split) ? 4 : 2;
+  return nw == 8 && rm <= 1 && kt_bytes == 2 && (pk || !split) ? 4 : 2;
 }
 constexpr size_t attn_lds_bytes(int nw, int rm, int kt_bytes, bool split, bool pk) {
   return (size_t)attn_ring(nw, rm, kt_bytes, split, pk) * kTileBytes + (rm == 2 ? 2 * kWBuf : 0);
