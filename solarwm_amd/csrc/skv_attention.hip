@@ -425,15 +425,18 @@ __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int ke
 }
 
 // K and V^T tile buffers of attn_kernel's ring: 4 (a barrier every second step) for 8-wave groups
-// over 2-byte pools without PRoPE, 2 otherwise: 4-wave groups run two workgroups per CU, whose
-// 2 x 128 KB would not fit the 160 KB of LDS; the PRoPE instance stages each key frame's matrices
-// for the step after next; fp32 pools and the frame-aligned split spill registers with the
+// over 2-byte pools, 2 otherwise: 4-wave groups run two workgroups per CU, whose 2 x 128 KB would
+// not fit the 160 KB of LDS; fp32 pools and the frame-aligned split spill registers with the
 // longer ring.
 constexpr int attn_ring(int nw, int rm, int kt_bytes, bool split, bool pk) {
-  return nw == 8 && rm <= 1 && kt_bytes == 2 && (pk || !split) ? 4 : 2;
+  return nw == 8 && kt_bytes == 2 && (pk || !split) ? 4 : 2;
 }
+// PRoPE matrix buffers: one per key frame in flight (frame j in buffer j mod n); with the longer
+// ring a frame's matrices are staged three steps before use, so frames of a single tile need four
+constexpr int attn_wbufs(int ring) { return ring == 4 ? 4 : 2; }
 constexpr size_t attn_lds_bytes(int nw, int rm, int kt_bytes, bool split, bool pk) {
-  return (size_t)attn_ring(nw, rm, kt_bytes, split, pk) * kTileBytes + (rm == 2 ? 2 * kWBuf : 0);
+  return (size_t)attn_ring(nw, rm, kt_bytes, split, pk) * kTileBytes +
+         (rm == 2 ? (size_t)attn_wbufs(attn_ring(nw, rm, kt_bytes, split, pk)) * kWBuf : 0);
 }
 
 // PK: key tiles packed across frame boundaries (PackedWalk; whole frames of T = 8k tokens, 2-byte
@@ -443,6 +446,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   static_assert(!PK || (RM == 0 && sizeof(KT) == 2), "packed tiles: 2-byte pools, no RoPE");
   constexpr int kBQ = NW * 32;
+  // LDS map: kRing K buffers, then kRing V^T buffers (tile x in buffer x mod kRing), then (PRoPE)
+  // kWN matrix buffers.  A step reads K(tau+1) and V(tau-1) and loads K(tau+kL+1) and V(tau+kL-1);
+  // the workgroup meets at a barrier after every kL-th step.  kL = 1 (two buffers each) for
+  // 4-wave groups (two workgroups share a CU's LDS), fp32 pools and the frame-aligned split;
+  // the others take kL = 2.
+  constexpr int kRing = attn_ring(NW, RM, (int)sizeof(KT), SPLIT, PK);
+  constexpr int kL = kRing / 2;
+  constexpr int kWN = attn_wbufs(kRing);
   using ET = typename OpOf<KT>::E;     // MFMA operand element
   using etx8 = typename OpOf<KT>::x8;
   // LDS: K tiles in [0, 32 KB) (two buffers), V^T tiles in [32 KB, 64 KB) (two buffers).
@@ -572,7 +583,7 @@ void attn_kernel(AttnArgs a) {
             __builtin_amdgcn_make_buffer_rsrc((void*)a.pq_t, (short)0, 0x7fffffff, 0x00020000);
         const uint32_t so = (uint32_t)((((int64_t)b * a.n_frames + j) * a.n_qframes + qf_lo) * kWPair);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r, (lds_void_t*)(lds + 2 * kTileBytes + (j & 1) * kWBuf + w * 1024), 16, off, so, 0, 0);
+            r, (lds_void_t*)(lds + kRing * kTileBytes + (j % kWN) * kWBuf + w * 1024), 16, off, so, 0, 0);
       }
     }
   };
@@ -582,7 +593,7 @@ void attn_kernel(AttnArgs a) {
     if constexpr (RM == 2) {
       // W of (this lane's query frame, key frame j), staged in LDS by issue_w; one group's
       // rows are live at a time (this runs inside the main loop, where registers are scarce)
-      const float* wt = reinterpret_cast<const float*>(lds + 2 * kTileBytes + (j & 1) * kWBuf) +
+      const float* wt = reinterpret_cast<const float*>(lds + kRing * kTileBytes + (j % kWN) * kWBuf) +
                         (qfi - qf_lo) * (kGroupsT * 16);
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
@@ -687,12 +698,6 @@ void attn_kernel(AttnArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
   const float c2 = a.scale_log2;
   const int lane16 = lane * 16;
-  // LDS map: kRing K buffers, then kRing V^T buffers (tile x in buffer x mod kRing).  A step
-  // reads K(tau+1) and V(tau-1) and loads K(tau+kL+1) and V(tau+kL-1); the workgroup meets at a
-  // barrier after every kL-th step.  kL = 1 (two buffers each) for 4-wave groups (two
-  // workgroups share a CU's LDS) and the RoPE instances; plain 8-wave groups take kL = 2.
-  constexpr int kRing = attn_ring(NW, RM, (int)sizeof(KT), SPLIT, PK);
-  constexpr int kL = kRing / 2;
   auto kb_lds = [&](int i) { return lds + (i & (kRing - 1)) * kHalf; };
   auto vb_lds = [&](int i) { return lds + (kRing + (i & (kRing - 1))) * kHalf; };
 
@@ -735,8 +740,11 @@ void attn_kernel(AttnArgs a) {
         if (x < ntau) loader.issue_v(vpool + tile_vbase(x), vb_lds(x), w);
     }
     if constexpr (RM == 2) {
+      // matrices of the frames of tiles 0 .. kL (the steps stage those of later frames)
       issue_w(tb / a.ntiles_f);
-      if (ntau > 1 && (tb + 1) % a.ntiles_f == 0) issue_w((tb + 1) / a.ntiles_f);
+#pragma unroll
+      for (int x = 1; x <= kL; ++x)
+        if (ntau > x && (tb + x) % a.ntiles_f == 0) issue_w((tb + x) / a.ntiles_f);
     }
 #pragma unroll
     for (int r = 0; r < 16 / NW; ++r)
@@ -822,8 +830,8 @@ void attn_kernel(AttnArgs a) {
     };
     if (kLoadSlot < 0) issue_loads();
     if constexpr (RM == 2) {
-      // W for the frame tile tau+2 opens (rot_q reads it at the start of step tau+1)
-      if (tau + 2 < ntau && kw.t == 0) issue_w(kw.j);
+      // W for the frame tile tau+kL+1 opens (rot_q reads it at the start of step tau+kL)
+      if (tau + kL + 1 < ntau && kw.t == 0) issue_w(kw.j);
     }
     if constexpr (RM > 0) {
       // QK(tau+1) below opens a new key frame: turn Q's temporal pairs for it
