@@ -116,7 +116,7 @@ def camera_trajectory(cfg, frames, device, seed=11):
     return v.float().to(device), k.float().to(device)
 
 
-def timed_rollout(cfg, inputs, caches, chunk_ids, cams=None):
+def timed_rollout(cfg, inputs, caches, chunk_ids, cams=None, n_none=len(PASSES) - 1):
     """Run chunks with HIP events around every EVENT_EVERY-th launch of each kind; returns the
     measured figures."""
     import torch
@@ -135,7 +135,7 @@ def timed_rollout(cfg, inputs, caches, chunk_ids, cams=None):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         mark()
-        run_ours(cfg, inputs, caches, chunk_ids, cams, on_chunk=mark)
+        run_ours(cfg, inputs, caches, chunk_ids, cams, on_chunk=mark, n_none=n_none)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     chunk_ms = [a.elapsed_time(b) for a, b in zip(marks[:-1], marks[1:])]
@@ -167,9 +167,9 @@ def timed_rollout(cfg, inputs, caches, chunk_ids, cams=None):
     }
 
 
-def run_ours(cfg, inputs, caches, chunk_ids, cams=None, on_chunk=None):
-    """Our path over chunks, in the sampler's pass order (``driver.rollout_passes``: 4 ``none``
-    passes then the commit pass per chunk) with ``driver.cached_forward``'s block loop and
+def run_ours(cfg, inputs, caches, chunk_ids, cams=None, on_chunk=None, n_none=len(PASSES) - 1):
+    """Our path over chunks, in the sampler's pass order (``driver.rollout_passes``: ``n_none``
+    ``none`` passes, 4 by default, then the commit pass per chunk) with ``driver.cached_forward``'s block loop and
     deferred commit; ``cams`` (per-frame viewmats, K) stages one fused-PRoPE camera pass per
     forward for all layers.  ``on_chunk(c)`` runs after each chunk's commit pass is enqueued."""
     from solarwm_amd import attend_cached, driver, stage_camera_cache
@@ -180,7 +180,7 @@ def run_ours(cfg, inputs, caches, chunk_ids, cams=None, on_chunk=None):
     if not chunk_ids:
         return
     n_frames = (max(chunk_ids) + 1) * cfg["chunk_f"]
-    plan = [p for p in driver.rollout_passes(n_frames, cfg["chunk_f"], T, len(PASSES) - 1)
+    plan = [p for p in driver.rollout_passes(n_frames, cfg["chunk_f"], T, n_none)
             if p.chunk in set(chunk_ids)]
     for p in plan:
         cp = None
@@ -613,6 +613,32 @@ def probe(cfg, device, iters=20):
         torch.cuda.synchronize()
         msg += f", gather x{iters} ({C4['mem_frames']} of {n_bank} frames, H{Hb}, fresh indices)"
     log(msg)
+
+
+def four_pass_leg(device):
+    """The config-2 rollout with 4 passes per chunk, the 4th committing (3 ``none`` + 1 commit:
+    the NFE-4 count of BASELINE's configs with the cache written on the last denoising step),
+    beside the headline's reference-faithful 4 ``none`` + 1 commit (stage2.py:683-760)."""
+    import torch
+
+    cfg = CONFIGS["c2"]
+    inputs = make_inputs(cfg, device)
+    caches = make_caches(cfg, device)
+    run_ours(cfg, inputs, caches, range(2), n_none=3)  # warmup, then back to an empty cache
+    torch.cuda.synchronize()
+    for c in caches:
+        c.reset()
+    torch.cuda.synchronize()
+    st = timed_rollout(cfg, inputs, caches, range(cfg["chunks"]), n_none=3)
+    del inputs, caches
+    torch.cuda.empty_cache()
+    return {
+        "frames_per_s": round(st["frames_per_s"], 4),
+        "steady_frames_per_s": round(st["steady_frames_per_s"], 4) if st["steady_frames_per_s"] else None,
+        "attn_tflops": round(st["attn_tflops"], 1),
+        "workload": f"{cfg['workload']}: {cfg['chunks']} chunks x (3 none + 1 commit) passes, "
+                    f"{cfg['layers']} layers",
+    }
 
 
 def steady_state(name, device, fill=7, timed=3, rope=False, prope=False):
@@ -1258,6 +1284,8 @@ def main():
             r = steady_state(name, dev)
             aux[name] = {k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in r.items()}
             log(f"[bench] aux {name}: {aux[name]}")
+        aux["c2_four_passes"] = four_pass_leg(dev)
+        log(f"[bench] aux c2_four_passes: {aux['c2_four_passes']}")
         log("[bench] aux c2 with RoPE on load")
         aux["c2_rope"] = c2_rope(dev)
         log(f"[bench] aux c2_rope: {aux['c2_rope']}")
