@@ -1075,9 +1075,10 @@ void attn_kernel(AttnArgs a) {
 //     lane-contiguous 32 B layout costs a 2-way conflict on every read).  Direct buffer->LDS
 //     loads fill them: DMA lane i of part q writes operand lane i, bytes 16 q .. +16.
 constexpr int kOp8 = 2048;
-// K and V^T tile buffers of the fp8 kernel's ring: a barrier every kFp8Ring / 2 steps (8 measured
-// slower than 4 at C5: the waves drift further apart between barriers)
-constexpr int kFp8Ring = 4;
+// K and V^T tile buffers of the fp8 kernel's ring: a barrier every ring / 2 steps (8 measured
+// slower than 4 at C5: the waves drift further apart between barriers).  4-wave groups keep two
+// buffers (with four they spill a register).
+constexpr int fp8_ring(int nw) { return nw == 8 ? 4 : 2; }
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 __device__ inline int key_perm64(int kb, int r) {
@@ -1297,7 +1298,7 @@ void attn_fp8_kernel(AttnArgs a) {
   // reads K(tau+1) and V(tau-1) and loads K(tau+3) and V(tau+1), so the buffers a step writes
   // were last read two steps earlier, and the workgroup meets at a barrier after every second
   // step (odd tau) only.
-  constexpr int kRing = kFp8Ring;
+  constexpr int kRing = fp8_ring(NW);
   constexpr int kL = kRing / 2;  // steps between barriers
   auto kb_lds = [&](int i) { return lds + (i & (kRing - 1)) * kBuf; };
   auto vb_lds = [&](int i) { return lds + (kRing + (i & (kRing - 1))) * kBuf; };
@@ -1662,16 +1663,16 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     if constexpr (NW == 8) {
       if (a.split) {
         if (q_dtype == SKV_BF16)
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
         else
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
         return;
       }
     }
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
     else
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 2 * kFp8Ring * 4 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
     return;
   }
   if constexpr (NW == 8) {

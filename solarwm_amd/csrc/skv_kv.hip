@@ -376,7 +376,9 @@ __global__ __launch_bounds__(1024) void append_fp8_reg_kernel(AppendArgs a) {
   const int d = tid >> 3, tc = (tid & 7) * 8;
 #pragma unroll
   for (int j = 0; j < kFp8OnChip; ++j) {
-    if (j >= nt) break;
+    // `continue`, not `break`: a break keeps the loop from unrolling fully, and r[] then lives
+    // in scratch memory (304 bytes per lane) instead of registers
+    if (j >= nt) continue;
     uint8_t* buf = vt8[j & 1];
     const u32x2 q = quant8(chunk(j), inv);
 #pragma unroll
