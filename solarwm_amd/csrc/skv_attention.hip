@@ -1058,10 +1058,13 @@ void attn_kernel(AttnArgs a) {
 //   * P is quantised as P * sv * G (sv = the tile's V frame scale, G = 28 / max_window(sv), so
 //     P <= 16 maps below 448) and O is divided by G * sum(P) at the end;
 //   * the running max is speculative, as in attn_kernel: probabilities are formed against the
-//     max of the earlier tiles, and a lane whose four partial sums of 8 scaled probabilities
-//     P * sv * G are not all <= 448 (so one of them might not fit e4m3), or whose max is still
-//     -inf, sends the wave to a rare path that raises the max to the tile's true max and
-//     recomputes the tile (P up to 16 x the row max's fits without it);
+//     max of the earlier tiles.  The row sums of the stored P come from the matrix core (one
+//     16x16x128 product per tile, mfma_rowsum) instead of 32 VALU adds per lane; a stored
+//     probability that does not fit e4m3 (>= 480) converts to NaN, so a NaN row sum, or a max
+//     still -inf, sends the wave to a rare path that raises the max to the tile's true max and
+//     recomputes the tile.  The test runs at the start of the next step, before that tile's
+//     PV product and before its scores' registers take the next QK product (P up to 16 x the
+//     row max's fits without it);
 //   * per 64-key tile and wave: 4 QK MFMAs (2 key blocks kb x 2 channel halves cs; A = K rows,
 //     B = the lane's 32 quantised Q channels cs*64 + 32 hh ..) and 4 PV MFMAs (one per
 //     32-channel block db; A = V^T row 32 db + n, keys 32 hh .. +31; B = P^T, the lane's
@@ -1079,6 +1082,8 @@ constexpr int kOp8 = 2048;
 // slower than 4 at C5: the waves drift further apart between barriers).  4-wave groups keep two
 // buffers (with four they spill a register).
 constexpr int fp8_ring(int nw) { return nw == 8 ? 4 : 2; }
+// dynamic LDS of attn_fp8_kernel: the K and V^T rings (4 operand blocks of kOp8 bytes per tile)
+constexpr int fp8_lds_bytes(int nw) { return 2 * fp8_ring(nw) * 4 * kOp8; }
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 __device__ inline int key_perm64(int kb, int r) {
@@ -1130,6 +1135,14 @@ __device__ inline float pair_max_raw(float x) {
 
 __device__ inline f32x16 mfma64(const i32x8& a, const i32x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// Row sums of P on the matrix core: the 32x32x64 B operand P^T (lane (n, hh) = query n, keys
+// 32 hh ..) read as the B operand of the 16x16x128 product is column n & 15 with K group
+// (n >> 4) + 2 hh; A row r is 1.0 (e4m3 0x38) on the K groups of parity (r >> 2) & 1 and 0
+// elsewhere, so output rows 4g .. 4g+3 (held by lanes 16g ..) sum query (n & 15) + 16 (g & 1)
+// over both key halves: every lane receives its own query's sum.
+__device__ inline f32x4 mfma_rowsum(const i32x8& ones, const i32x8& p, const f32x4& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, p, c, 0, 0, 0, 0, 0, 0);
 }
 
 // direct buffer->LDS copy of this lane's N 16-byte pieces of one tile: goff = the piece's byte
@@ -1303,7 +1316,6 @@ void attn_fp8_kernel(AttnArgs a) {
   auto kb_lds = [&](int i) { return lds + (i & (kRing - 1)) * kBuf; };
   auto vb_lds = [&](int i) { return lds + (kRing + (i & (kRing - 1))) * kBuf; };
 
-  constexpr float kMaxPart8 = 448.0f;  // bound on every partial sum of scaled probabilities
   float sv_max = 0.f;
   for (int j = 0; j < a.n_frames; ++j)
     sv_max = fmaxf(sv_max, a.vscale[(int64_t)a.slots[j] * a.B * a.H + sc_bh]);
@@ -1317,6 +1329,15 @@ void attn_fp8_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  // A operand of the row-sum product (mfma_rowsum)
+  i32x8 ones;
+  {
+    const int v = (((lane >> 4) ^ (lane >> 2)) & 1) ? 0 : 0x38383838;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ones[i] = v;
+  }
+  f32x4 tsum;  // row sums of the last tile's stored P, from the matrix core
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
   f32x16 zero16;
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero16[i] = 0.f;
@@ -1358,10 +1379,10 @@ void attn_fp8_kernel(AttnArgs a) {
   vw.start(a, kbh, tb + kL - 1);
   mw.start(a, kbh, tb + 1);
   // Per key frame: the softmax multiplier (K scale folded in) and the log and reciprocal of the
-  // P scale, for the frame of tile tau+1, set at the end of step tau.
+  // P scale, for the frame of the tile whose softmax runs next.
   float mult = 0.f, log_pv = 0.f, inv_pv = 1.0f;
-  auto open_scales = [&](const TileWalk& sw) {
-    const int64_t sc = (int64_t)sw.slot * a.B * a.H + sc_bh;
+  auto open_scales = [&](int slot) {
+    const int64_t sc = (int64_t)slot * a.B * a.H + sc_bh;
     // an all-zero query row or K frame makes every logit 0; keep the multiplier positive so
     // masked (-inf) logits stay -inf instead of becoming NaN.  The scales are read through the
     // constant address space (scalar loads).
@@ -1375,23 +1396,74 @@ void attn_fp8_kernel(AttnArgs a) {
     log_pv = __builtin_amdgcn_logf(pv);
     inv_pv = __builtin_amdgcn_rcpf(pv);
   };
-  if (ntau > 0) open_scales(w0);
+  if (ntau > 0) open_scales(w0.slot);
+  int open_slot = -1;  // the slot of the frame the next tile opens (wave-uniform), else -1
+  // Settles P of the previous tile (scores s) before its PV product.  Probabilities use the
+  // running max m, not the tile's own max: an e4m3 probability at or above 480 converts to NaN,
+  // so its query's row sum from the matrix core is NaN, and that (or m still -inf) sends the
+  // wave to the rare path, which raises m of such queries to the tile's true max, recomputes
+  // their probabilities and rescales O and l.  The scales are still those of that tile's frame.
+  auto settle = [&](const f32x16 (&s)[2], i32x8& p) __attribute__((always_inline)) {
+    const bool need = !(tsum[0] <= 3.0e38f) || m_run == -INFINITY;
+    if (__any(need)) {
+      // both key halves of a query take the same decision
+      const bool needq = pair_max(need ? 1.f : 0.f) > 0.f;
+      float mq[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const f32x16& sc = s[c];
+        mq[c] = max3_raw(sc[0], sc[1], sc[2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) mq[c] = max3_raw(mq[c], sc[r], sc[r + 1]);
+        mq[c] = max3_raw(mq[c], sc[15], sc[15]);
+      }
+      const float mx = pair_max_raw(max3_raw(mq[0], mq[1], mq[1])) * mult;
+      const float m_new = needq ? fmaxf(m_run, mx) : m_run;
+      const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float bias2 = log_pv - (m_new == -INFINITY ? 0.f : m_new);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        float q4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e = 4 * d + j;
+          q4[j] = __builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], mult, bias2));
+        }
+        p[d] = pack_fp8x4_into(p[d], q4[0], q4[1], q4[2], q4[3]);
+      }
+      tsum = mfma_rowsum(ones, p, zero4);
+      l_run *= alpha;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+      }
+      m_run = m_new;
+    }
+    l_run = fmaf(tsum[0], inv_pv, l_run);
+  };
   // cb = tau & 1, passed as a literal: the register sets alternate with it, and odd steps end
   // at the barrier
-  auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], const i32x8& pprev,
+  auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], i32x8& pprev,
                   i32x8& pb) __attribute__((always_inline)) {
     if (tau + kL + 1 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(tau + kL + 1));
     if (tau + kL - 1 < ntau) if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(tau + kL - 1));
+    if (tau > 0) settle(s_nxt, pprev);  // s_nxt still holds the scores of tile tau-1
+    if (open_slot >= 0) {  // tile tau opens a key frame
+      open_scales(open_slot);
+      open_slot = -1;
+    }
     const char* kl = kb_lds(tau + 1) + lane16;  // K(tau+1) (stale data on the last step)
     const char* vl = vb_lds(tau - 1) + lane16;  // V(tau-1) (zeros on the first step)
 
     // Eight MFMA slots, QK(tau+1) and PV(tau-1) alternating (QK steps in the order (kb, cs) =
     // (0,0), (1,0), (0,1), (1,1), so the two halves of one key block are four slots apart), each
     // followed by a quarter of softmax(tau): the 4 probabilities of P^T dword i.  The operands
-    // come from LDS three slots ahead; the sum and the fp8 pack of a quarter run one slot later,
-    // when its exps have finished.
+    // come from LDS three slots ahead; the fp8 pack of a quarter runs one slot later, when its
+    // exps have finished.
     i32x8 op[4];
-    float pf[32], ls[4];
+    float pf[32];
     const float bias = log_pv - (m_run == -INFINITY ? 0.f : m_run);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -1416,65 +1488,18 @@ void attn_fp8_kernel(AttnArgs a) {
       }
       if (i > 0) {
         const int d = i - 1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ls[j] = d == 0 ? pf[4 * d + j] : ls[j] + pf[4 * d + j];
         pb[d] = pack_fp8x4_into(pb[d], pf[4 * d], pf[4 * d + 1], pf[4 * d + 2], pf[4 * d + 3]);
         asm volatile("" ::"v"(pb[d]));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ls[j] += pf[28 + j];
     pb[7] = pack_fp8x4_into(pb[7], pf[28], pf[29], pf[30], pf[31]);
-    {
-      const float lmax = max3_raw(max3_raw(ls[0], ls[1], ls[2]), ls[3], ls[3]);
-      const bool need = !(lmax <= kMaxPart8) || m_run == -INFINITY;
-      if (__any(need)) {
-        // rare path: both key halves of a query take the same decision; raise the max of each
-        // such query to the tile's true max and recompute its probabilities, sums and packs
-        const bool needq = pair_max(need ? 1.f : 0.f) > 0.f;
-        float mq[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const f32x16& sc = s_cur[c];
-          mq[c] = max3_raw(sc[0], sc[1], sc[2]);
-#pragma unroll
-          for (int r = 3; r < 15; r += 2) mq[c] = max3_raw(mq[c], sc[r], sc[r + 1]);
-          mq[c] = max3_raw(mq[c], sc[15], sc[15]);
-        }
-        const float mx = pair_max_raw(max3_raw(mq[0], mq[1], mq[1])) * mult;
-        const float m_new = needq ? fmaxf(m_run, mx) : m_run;
-        const float alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        const float bias2 = log_pv - (m_new == -INFINITY ? 0.f : m_new);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ls[j] = 0.f;
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-          float q4[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int e = 4 * d + j;
-            q4[j] = __builtin_amdgcn_exp2f(fmaf(s_cur[e >> 4][e & 15], mult, bias2));
-            ls[j] += q4[j];
-          }
-          pb[d] = pack_fp8x4_into(pb[d], q4[0], q4[1], q4[2], q4[3]);
-        }
-        l_run *= alpha;
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-          for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-        }
-        m_run = m_new;
-      }
-    }
-    l_run = fmaf(((ls[0] + ls[1]) + (ls[2] + ls[3])), inv_pv, l_run);
+    tsum = mfma_rowsum(ones, pb, zero4);  // read by the next step's settle
     if (tau + 1 < ntau) {
       const int tok0 = mw.t * kTile, key0 = mw.j * a.T + tok0;
       if ((tok0 + kTile > mw.flen) || (key0 + kTile > lim_lo))
         mask_tile64(s_nxt, hh, tok0, mw.flen, key0, lim_lane);
-      if (mw.t == 0) open_scales(mw);  // tile tau+1 opens a key frame
+      if (mw.t == 0) open_slot = mw.slot;
     }
     kw.next(a, kbh);
     vw.next(a, kbh);
@@ -1493,18 +1518,20 @@ void attn_fp8_kernel(AttnArgs a) {
   }
   // PV(ntau-1): V(ntau-1) was loaded by step ntau-2 (the prologue when ntau = 1), two steps or
   // a barrier earlier
-  auto epilogue = [&](const i32x8& pprev) __attribute__((always_inline)) {
+  auto epilogue = [&](const f32x16 (&s_last)[2], i32x8& pprev) __attribute__((always_inline)) {
+    settle(s_last, pprev);
     const char* vl = vb_lds(ntau - 1) + lane16;
 #pragma unroll
     for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
   };
   if (tau < ntau) {
     step(tau, 0, sA, sB, pA, pB);
-    epilogue(pB);
+    epilogue(sA, pB);
   } else if (ntau > 0) {
-    epilogue(pA);
+    epilogue(sB, pA);
   }
-  const float l_tot = pair_sum(l_run);
+  // the matrix core sums both key halves of a query: every lane holds its query's full sum
+  const float l_tot = l_run;
   if (SPLIT && (tb > 0 || te < nt)) {
     // part of a split q-tile: O / G (the P scale's G divided out), the running max in log2
     // units and the row sum, the record attn_combine_kernel merges
@@ -1663,16 +1690,16 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     if constexpr (NW == 8) {
       if (a.split) {
         if (q_dtype == SKV_BF16)
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true>), grid, block, fp8_lds_bytes(NW), s, a);
         else
-          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
+          hipLaunchKernelGGL((attn_fp8_kernel<NW, float, true>), grid, block, fp8_lds_bytes(NW), s, a);
         return;
       }
     }
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16>), grid, block, fp8_lds_bytes(NW), s, a);
     else
-      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, 2 * fp8_ring(NW) * 4 * kOp8, s, a);
+      hipLaunchKernelGGL((attn_fp8_kernel<NW, float>), grid, block, fp8_lds_bytes(NW), s, a);
     return;
   }
   if constexpr (NW == 8) {
