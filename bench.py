@@ -562,6 +562,45 @@ def gather_bandwidth(device, iters=24):
     return moved / (ms / 1e3) / 1e9, ms
 
 
+def eviction_latency(cfg, iters=2000):
+    """Eviction is slot-table arithmetic on the host (causal_model.py:1054-1067 memmove and
+    2863-2921 commit replaced by a permutation of frame slots): time one layer's plan + stage +
+    commit in steady state (full window, rolling eviction of chunk_f frames), and report the
+    reference's clone + memmove bytes per layer and pass that it replaces."""
+    from solarwm_amd.cache import CacheGeometry, SlotTable
+
+    T, H, cap, sink, chunk = cfg["T"], cfg["heads"], cfg["cap_f"], cfg["sink_f"], cfg["chunk_f"]
+    geom = CacheGeometry(batch=cfg["batch"], heads=H, head_dim=128, frame_tokens=T,
+                         capacity_frames=cap, sink_frames=sink, staging_frames=chunk)
+    tab = SlotTable(geom)
+    Lq = chunk * T
+    start = 0
+    for _ in range(-(-cap // chunk) + 2):  # fill the window, then roll twice
+        p, temp, _, _ = tab.plan(start, Lq)
+        tab.commit(tab.stage(p, temp), p.current_end, p.local_end_index)
+        start += Lq
+    rolled = None
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        p, temp, _, _ = tab.plan(start, Lq)
+        tab.commit(tab.stage(p, temp), p.current_end, p.local_end_index)
+        rolled = p.num_rolled_tokens
+        start += Lq
+    us = (time.perf_counter() - t0) / iters * 1e6
+    elem = cfg["batch"] * H * 128 * 2  # bytes per token of K (or V), bf16
+    clone = 2 * 2 * cap * T * elem     # read + write of K and V
+    memmove = 2 * 2 * rolled * elem    # read + write of the rolled tokens of K and V
+    return {
+        "host_us_per_layer_pass": round(us, 2),
+        "device_bytes": 0,
+        "reference_bytes_avoided_per_layer_pass": clone + memmove,
+        "reference_clone_bytes": clone,
+        "reference_memmove_bytes": memmove,
+        "note": "plan + stage + commit of one layer's slot table in steady state (rolling "
+                f"eviction of {chunk} frames); no bytes move on the GPU",
+    }
+
+
 def probe(cfg, device, iters=20):
     """Short fixed sequence for hardware-counter runs (rocprofv3 --pmc): a plain device copy of
     exactly 1 GiB (the FETCH_SIZE / WRITE_SIZE calibration), then steady-state launches of the
@@ -1236,6 +1275,10 @@ def main():
     result["gather_avg_launch_us"] = round(g_ms * 1e3, 2)
     log(f"[bench] gather (C4 bank, 8 of 256 frames, fresh indices per launch): {gbps:.0f} GB/s, "
         f"{g_ms * 1e3:.1f} us")
+    result["eviction"] = eviction_latency(cfg)
+    log(f"[bench] eviction: {result['eviction']['host_us_per_layer_pass']} us host per layer pass, "
+        f"{result['eviction']['reference_bytes_avoided_per_layer_pass'] / 1e6:.1f} MB of reference "
+        "clone + memmove avoided")
 
     if not args.no_baselines:
         del caches

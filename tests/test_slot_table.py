@@ -145,3 +145,15 @@ def test_plan_unbounded_window_is_direct_insert():
                          local_attn_size=-1, staging_frames=3)
     p = plan_cached_forward(geom, 0, 0, 0, 30)
     assert p.action == "direct_insert" and geom.max_attention_size == 39600
+
+
+def test_bench_eviction_leg_counts_the_reference_bytes():
+    """bench.py's eviction leg: the reference's clone + memmove per layer and pass at C2
+    (causal_model.py:1054-1067) is 402.6 MB + 325.9 MB, and the slot table moves none."""
+    import bench
+
+    r = bench.eviction_latency(bench.CONFIGS["c2"], iters=50)
+    # clone: K and V of the 21-frame cache, read + write; memmove: the 17 rolled frames
+    assert r["reference_clone_bytes"] == 2 * 2 * 21 * 1560 * 12 * 128 * 2 == 402554880
+    assert r["reference_memmove_bytes"] == 2 * 2 * 17 * 1560 * 12 * 128 * 2 == 325877760
+    assert r["device_bytes"] == 0 and r["host_us_per_layer_pass"] > 0
