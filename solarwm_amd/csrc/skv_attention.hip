@@ -37,6 +37,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "skv_common.h"
 
@@ -414,14 +416,31 @@ __device__ inline void qk_tile(const char* kl, const X8 (&qf)[8], f32x16 (&s)[2]
 }
 
 // Padding keys (token >= T inside the frame) and keys past the lane's chunk-causal limit.
+// x = -inf unless C < t: one compare into vcc and one select per register, written as one asm
+// statement so the compares are not hoisted ahead of the selects (32 live SGPR pairs spill)
+template <int C>
+__device__ inline float mask_below(float x, int t, float ninf) {
+  asm("v_cmp_lt_i32 vcc, %2, %1\n\tv_cndmask_b32 %0, %3, %0, vcc"
+      : "+v"(x) : "v"(t), "n"(C), "v"(ninf) : "vcc");
+  return x;
+}
+// register I of a tile's two accumulators (s[I >> 4][I & 15]) holds key offset KeyOf(I)
+template <template <int> class KeyOf, int... I>
+__device__ inline void mask_regs(f32x16 (&s)[2], int t, std::integer_sequence<int, I...>) {
+  const float ninf = -INFINITY;
+  ((s[I >> 4][I & 15] = mask_below<KeyOf<I>::value>(s[I >> 4][I & 15], t, ninf)), ...);
+}
+template <int I>
+struct KeyBf16 : std::integral_constant<int, (I >> 4) * 32 + ((I & 15) >> 3) * 16 + (I & 7)> {};
+template <int I>
+struct KeyFp8 : std::integral_constant<int, I> {};
+
 __device__ inline void mask_tile(f32x16 (&s)[2], int hh, int tok0, int T, int key0, int lim) {
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kk = kb * 32 + (i >> 3) * 16 + hh * 8 + (i & 7);
-      if (tok0 + kk >= T || key0 + kk >= lim) s[kb][i] = -INFINITY;
-    }
+  // key kk of the tile is masked when tok0 + kk >= T or key0 + kk >= lim, i.e. when
+  // kk >= min(T - tok0, lim - key0); kk = 8 hh + c with c fixed per register, so each register
+  // takes one compare against a constant
+  const int t = min(T - tok0, lim - key0) - 8 * hh;
+  mask_regs<KeyBf16>(s, t, std::make_integer_sequence<int, 32>{});
 }
 
 // K and V^T tile buffers of attn_kernel's ring: 4 (a barrier every second step) for 8-wave groups
@@ -1105,13 +1124,9 @@ __device__ inline int pack_fp8x4_into(int old, float x0, float x1, float x2, flo
 }
 
 __device__ inline void mask_tile64(f32x16 (&s)[2], int hh, int tok0, int T, int key0, int lim) {
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kk = 32 * hh + 16 * kb + i;
-      if (tok0 + kk >= T || key0 + kk >= lim) s[kb][i] = -INFINITY;
-    }
+  // as mask_tile: key kk = 32 hh + 16 kb + i is masked when kk >= min(T - tok0, lim - key0)
+  const int t = min(T - tok0, lim - key0) - 32 * hh;
+  mask_regs<KeyFp8>(s, t, std::make_integer_sequence<int, 32>{});
 }
 
 // the lane's 32-byte operand: p = block + 16 * lane (first half), second half 1 KB further
