@@ -1344,14 +1344,9 @@ void attn_fp8_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
-  // Row sums: on the matrix core (kMS), or, in the split instances, whose segment bookkeeping
-  // leaves no room for the product's operands (their hot loop then reloads spilled registers),
-  // as 32 VALU adds per lane into four partial sums of 8 probabilities.
-  constexpr bool kMS = !SPLIT;
-  constexpr float kMaxPart8 = 448.0f;  // VALU sums: bound on every partial sum of stored P
   // A operand of the row-sum product (mfma_rowsum)
   i32x8 ones;
-  if constexpr (kMS) {
+  {
     const int v = (((lane >> 4) ^ (lane >> 2)) & 1) ? 0 : 0x38383838;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ones[i] = v;
@@ -1423,10 +1418,8 @@ void attn_fp8_kernel(AttnArgs a) {
   // so its query's row sum from the matrix core is NaN, and that (or m still -inf) sends the
   // wave to the rare path, which raises m of such queries to the tile's true max, recomputes
   // their probabilities and rescales O and l.  The scales are still those of that tile's frame.
-  // rare path for P of one tile (scores s, packs p, lane decision `need`); with VALU sums it
-  // returns the recomputed probabilities' sum (a lane's half of the keys)
-  auto rare = [&](const f32x16 (&s)[2], i32x8& p, bool need) __attribute__((always_inline)) -> float {
-    float lsum = 0.f;
+  // rare path for P of one tile (scores s, packs p, lane decision `need`)
+  auto rare = [&](const f32x16 (&s)[2], i32x8& p, bool need) __attribute__((always_inline)) {
     {
       // both key halves of a query take the same decision
       const bool needq = pair_max(need ? 1.f : 0.f) > 0.f;
@@ -1450,11 +1443,10 @@ void attn_fp8_kernel(AttnArgs a) {
         for (int j = 0; j < 4; ++j) {
           const int e = 4 * d + j;
           q4[j] = __builtin_amdgcn_exp2f(fmaf(s[e >> 4][e & 15], mult, bias2));
-          if constexpr (!kMS) lsum += q4[j];
         }
         p[d] = pack_fp8x4_into(p[d], q4[0], q4[1], q4[2], q4[3]);
       }
-      if constexpr (kMS) tsum = mfma_rowsum(ones, p, zero4);
+      tsum = mfma_rowsum(ones, p, zero4);
       l_run *= alpha;
       if (__any(alpha != 1.0f)) {
 #pragma unroll
@@ -1464,7 +1456,6 @@ void attn_fp8_kernel(AttnArgs a) {
       }
       m_run = m_new;
     }
-    return lsum;
   };
   auto settle = [&](const f32x16 (&s)[2], i32x8& p) __attribute__((always_inline)) {
     const bool need = !(tsum[0] <= 3.0e38f) || m_run == -INFINITY;
@@ -1477,9 +1468,7 @@ void attn_fp8_kernel(AttnArgs a) {
                   i32x8& pb) __attribute__((always_inline)) {
     if (tau + kL + 1 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(tau + kL + 1));
     if (tau + kL - 1 < ntau) if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(tau + kL - 1));
-    if constexpr (kMS) {
-      if (tau > 0) settle(s_nxt, pprev);  // s_nxt still holds the scores of tile tau-1
-    }
+    if (tau > 0) settle(s_nxt, pprev);  // s_nxt still holds the scores of tile tau-1
     if (open_slot >= 0) {  // tile tau opens a key frame
       open_scales(open_slot);
       open_slot = -1;
@@ -1493,7 +1482,7 @@ void attn_fp8_kernel(AttnArgs a) {
     // come from LDS three slots ahead; the fp8 pack of a quarter runs one slot later, when its
     // exps have finished.
     i32x8 op[4];
-    float pf[32], ls[4];
+    float pf[32];
     const float bias = log_pv - (m_run == -INFINITY ? 0.f : m_run);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -1518,27 +1507,13 @@ void attn_fp8_kernel(AttnArgs a) {
       }
       if (i > 0) {
         const int d = i - 1;
-        if constexpr (!kMS) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) ls[j] = d == 0 ? pf[4 * d + j] : ls[j] + pf[4 * d + j];
-        }
         pb[d] = pack_fp8x4_into(pb[d], pf[4 * d], pf[4 * d + 1], pf[4 * d + 2], pf[4 * d + 3]);
         asm volatile("" ::"v"(pb[d]));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     pb[7] = pack_fp8x4_into(pb[7], pf[28], pf[29], pf[30], pf[31]);
-    if constexpr (kMS) {
-      tsum = mfma_rowsum(ones, pb, zero4);  // read by the next step's settle
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ls[j] += pf[28 + j];
-      const float lmax = max3_raw(max3_raw(ls[0], ls[1], ls[2]), ls[3], ls[3]);
-      const bool need = !(lmax <= kMaxPart8) || m_run == -INFINITY;
-      float lsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
-      if (__any(need)) lsum = rare(s_cur, pb, need);
-      l_run = fmaf(lsum, inv_pv, l_run);  // the scales are still tile tau's
-    }
+    tsum = mfma_rowsum(ones, pb, zero4);  // read by the next step's settle
     if (tau + 1 < ntau) {
       const int tok0 = mw.t * kTile, key0 = mw.j * a.T + tok0;
       if ((tok0 + kTile > mw.flen) || (key0 + kTile > lim_lo))
@@ -1563,7 +1538,7 @@ void attn_fp8_kernel(AttnArgs a) {
   // PV(ntau-1): V(ntau-1) was loaded by step ntau-2 (the prologue when ntau = 1), two steps or
   // a barrier earlier
   auto epilogue = [&](const f32x16 (&s_last)[2], i32x8& pprev) __attribute__((always_inline)) {
-    if constexpr (kMS) settle(s_last, pprev);
+    settle(s_last, pprev);
     const char* vl = vb_lds(ntau - 1) + lane16;
 #pragma unroll
     for (int db = 0; db < 4; ++db) oacc[db] = mfma64(lds_op32(vl + db * kOp8), pprev, oacc[db]);
@@ -1574,9 +1549,8 @@ void attn_fp8_kernel(AttnArgs a) {
   } else if (ntau > 0) {
     epilogue(sB, pA);
   }
-  // the matrix core sums both key halves of a query (every lane holds its query's full sum);
-  // VALU sums cover the lane's half
-  const float l_tot = kMS ? l_run : pair_sum(l_run);
+  // the matrix core sums both key halves of a query: every lane holds its query's full sum
+  const float l_tot = l_run;
   if (SPLIT && (tb > 0 || te < nt)) {
     // part of a split q-tile: O / G (the P scale's G divided out), the running max in log2
     // units and the row sum, the record attn_combine_kernel merges
