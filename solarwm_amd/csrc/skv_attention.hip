@@ -20,7 +20,8 @@
 //   * 64-key K and V^T tiles are staged in LDS and shared by the waves, in MFMA operand order
 //     (see kBlockBytes), by buffer loads straight into LDS: one descriptor per tile, the
 //     lane's byte offset in a VGPR that never changes, the block offset in an SGPR.  K is
-//     staged two tiles ahead and V one tile ahead of their use;
+//     staged two tiles ahead and V one tile ahead of their use (three and one on the
+//     four-buffer ring of 8-wave groups over 2-byte pools, with a barrier every second tile);
 //   * the K rows of each 32-key block are loaded in the permuted order key_perm(), which makes
 //     the fp32 S^T accumulator of a lane hold, per 8 registers, 8 consecutive keys — exactly
 //     the bf16x8 B operand (P^T) of the PV product; V is stored transposed in the pool so
@@ -30,9 +31,11 @@
 //     VALU work at the same time; the softmax is front-loaded so its row sum is ready when the
 //     last MFMA issues; the loop is unrolled twice so score and probability registers
 //     alternate between two sets instead of being copied;
-//   * tiles never straddle frames (frames are padded to 64 tokens); padding keys and keys
-//     beyond a query's chunk-causal limit get -inf, decided per tile: full tiles skip the
-//     mask, tiles past every query's limit are not visited.
+//   * tiles either follow frames (each frame padded to whole 64-token tiles) or, for whole
+//     bf16 / f16 frames of 8k tokens without RoPE, run across frame boundaries (PK: a tile's
+//     keys end one frame's slot and start the next one's); padding keys and keys beyond a
+//     query's chunk-causal limit get -inf, decided per tile: full tiles skip the mask, tiles
+//     past every query's limit are not visited.
 
 #include <math.h>
 
