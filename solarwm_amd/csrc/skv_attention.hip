@@ -527,10 +527,6 @@ void attn_kernel(AttnArgs a) {
   const int q0 = qt * kBQ;
   const int qrow = q0 + w * 32 + n;
   const bool qlive = qrow < a.Lq;
-  // 8-wave packed unsplit groups: a wave whose 32 queries all lie past Lq (in the last q-tile)
-  // skips the products and the softmax; it still stages its share of every tile
-  constexpr bool kDW = PK && !SPLIT && NW == 8;
-  const bool wave_live = !kDW || __builtin_amdgcn_readfirstlane((int)(q0 + w * 32 < a.Lq)) != 0;
 
   // Q^T operand: lane (n, hh) holds q[qrow][k*16 + hh*8 .. +7] for k = 0..7.
   etx8 qf[8];
@@ -868,7 +864,6 @@ void attn_kernel(AttnArgs a) {
       for (int i = 0; i < 3; ++i) opq[i] = operand(i);
     }
 
-    if (wave_live) {
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ls[4];
     float pf[32];
@@ -981,7 +976,6 @@ void attn_kernel(AttnArgs a) {
       m_run = m_new;
     }
     l_run += lp;
-    }
     if (tau + 1 < ntau) {
       if constexpr (PK) {
         const int key0 = (tb + tau + 1) * kTile;
