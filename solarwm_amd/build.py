@@ -49,16 +49,23 @@ def build(verbose: bool = False) -> Path:
     """Compile every source under csrc/ and link libsolarkv.so; returns its path."""
     hipcc = _hipcc()
     with tempfile.TemporaryDirectory(prefix="skv_build_") as tmp:
-        objs = []
+        # the translation units compile side by side (one hipcc process each)
+        jobs = []
         for src in sources():
             obj = Path(tmp) / (src.stem + ".o")
             cmd = [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
             if verbose:
                 print(" ".join(cmd), flush=True)
-            res = subprocess.run(cmd, capture_output=True, text=True)
-            if res.returncode != 0:
-                raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+            jobs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                    stderr=subprocess.PIPE, text=True)))
+        objs, failed = [], []
+        for src, obj, proc in jobs:
+            out, err = proc.communicate()
+            if proc.returncode != 0:
+                failed.append(f"hipcc failed on {src.name}:\n{out}\n{err}")
             objs.append(str(obj))
+        if failed:
+            raise RuntimeError("\n".join(failed))
         tmp_lib = Path(tmp) / LIB_PATH.name
         cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp_lib)]
         res = subprocess.run(cmd, capture_output=True, text=True)

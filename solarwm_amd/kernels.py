@@ -208,19 +208,23 @@ def _norm_args(name: str, norm, batch: int, rows: int, heads: int, device):
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> tuple[int, int]:
-    """(pointer, bytes) of this device and current stream's scratch tensor, grown to at least
-    ``nbytes``.  The kernels' split paths keep their partial results there; launches on one
-    stream run in order, so every call on that stream shares it."""
+def workspace(device: torch.device, nbytes: int) -> tuple[int, int, torch.Tensor | None]:
+    """(pointer, bytes, tensor) of this device and current stream's scratch tensor, grown to at
+    least ``nbytes``.  The kernels' split paths keep their partial results there; launches on one
+    stream run in order, so every call on that stream shares it.
+
+    Growing replaces the shared tensor: a launcher that keeps the pointer for later launches must
+    also keep the returned tensor alive, or its launches would write into memory the caching
+    allocator has handed to another tensor."""
     if nbytes <= 0:
-        return 0, 0
+        return 0, 0, None
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            _stream(device))
     t = _workspaces.get(key)
     if t is None or t.numel() < nbytes:
         t = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
         _workspaces[key] = t
-    return t.data_ptr(), t.numel()
+    return t.data_ptr(), t.numel(), t
 
 
 def prepare_append(
@@ -301,11 +305,12 @@ def prepare_append(
         rms_p, rms_sb, w_p = _norm_args("k_norm", k_norm, b, (src_frame0 + n) * frame_tokens, h,
                                         kpool.device)
         desc.k_inv_rms, desc.k_rms_stride_b, desc.k_norm_weight = rms_p, rms_sb, w_p
+    ws_tensor = None
     if use_workspace and kpool.dtype == torch.float8_e4m3fn:
         need = ctypes.c_int64(0)
         _lib.check("skv_append_workspace_size",
                    lib.skv_append_workspace_size(ctypes.byref(desc), ctypes.byref(need)))
-        desc.workspace, desc.workspace_bytes = workspace(kpool.device, need.value)
+        desc.workspace, desc.workspace_bytes, ws_tensor = workspace(kpool.device, need.value)
     args = (ctypes.byref(desc), _stream(kpool.device))
     fn = lib.skv_append_ex
 
@@ -315,8 +320,10 @@ def prepare_append(
         _toc("append", t0, moved)
 
     launch.bytes_moved = moved
+    # the workspace tensor is kept too: a later call that grows this stream's workspace drops
+    # the shared reference, and this launcher's descriptor still points at the old block
     launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots, kr_pool, rope_hw, vr_pool,
-                   kv_xform, k_norm, desc, args)
+                   kv_xform, k_norm, desc, args, ws_tensor)
     return launch
 
 
@@ -514,7 +521,7 @@ def attention_plan(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
     plan = _lib.LaunchPlan()
     _lib.check("skv_attention_plan", lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)))
     if use_workspace and plan.workspace_bytes > 0:
-        d.workspace, d.workspace_bytes = workspace(q.device, plan.workspace_bytes)
+        d.workspace, d.workspace_bytes, _ = workspace(q.device, plan.workspace_bytes)
         _lib.check("skv_attention_plan", lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)))
     return {name: int(getattr(plan, name)) for name, _ in _lib.LaunchPlan._fields_}
 
@@ -568,7 +575,8 @@ def attention_frames(
         plan = _lib.LaunchPlan()
         _lib.check("skv_attention_plan", lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)))
         if plan.workspace_bytes > 0:
-            d.workspace, d.workspace_bytes = workspace(q.device, plan.workspace_bytes)
+            d.workspace, d.workspace_bytes, ws = workspace(q.device, plan.workspace_bytes)
+            keep = keep + (ws,)
     t0 = _tic("attention")
     _lib.check("skv_attention_ex", lib.skv_attention_ex(ctypes.byref(d), _stream(q.device)))
     # algorithmic FLOPs: QKᵀ and PV over every key (masking is not discounted)
@@ -596,3 +604,36 @@ def new_pools(
     else:
         kscale = vscale = None
     return kpool, vpool, kscale, vscale
+
+
+_staging: dict[tuple[int, int, torch.dtype], torch.Tensor] = {}
+
+
+def staging_pools(
+    n_slots: int,
+    batch: int,
+    heads: int,
+    frame_tokens: int,
+    dtype: torch.dtype,
+    device: torch.device,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """K/V pools of ``n_slots`` frames over this device and current stream's staging buffer, for
+    dense K/V that a call stages and attends at once (the drop-in ``attention``, teacher
+    forcing).  The buffer grows on demand and is reused by every such call on the stream; its
+    contents are left as they are (not zero-filled): an append writes every row of the slots it
+    fills, rows past ``frame_tokens`` as zeros.  Calls on one stream run in order, so a call's
+    append waits for the previous call's attention; the buffer stays allocated at its largest
+    size (bf16 K+V of a 32768-key window at 12 heads: 201 MB)."""
+    if dtype == torch.float8_e4m3fn:
+        raise ValueError("staging pools hold bf16, f16 or float32 frames")
+    tp = padded_tokens(frame_tokens)
+    n = n_slots * batch * heads * tp * HEAD_DIM
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           _stream(device), dtype)
+    buf = _staging.get(key)
+    if buf is None or buf.numel() < 2 * n:
+        buf = torch.empty(2 * n, dtype=dtype, device=device)
+        _staging[key] = buf
+    kpool = buf[:n].view(n_slots, batch, heads, tp, HEAD_DIM)
+    vpool = buf[n : 2 * n].view(n_slots, batch, heads, HEAD_DIM, tp)
+    return kpool, vpool
