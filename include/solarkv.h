@@ -339,6 +339,17 @@ int skv_attention_plan(const skv_attention_desc* desc, skv_launch_plan* plan);
 #define SKV_NOALLOC_SCRATCH_BYTES 68157440
 int skv_attention_ex_noalloc(const skv_attention_desc* desc, skv_stream_t stream);
 
+/*
+ * skv_noalloc_init — set-up of skv_attention_ex_noalloc on the current device: looks up the
+ * device address of that device's scratch array (loading the code object that holds it).  Call
+ * it once per device, with the device current, before the first skv_attention_ex_noalloc made
+ * under HIP graph capture: a captured call whose device is not set up returns SKV_E_UNSUPPORTED
+ * instead of loading a module mid-capture.  Outside capture the entry point sets itself up on
+ * first use.  Idempotent and thread-safe; allocates nothing beyond the static array.  No
+ * counterpart in the reference (see skv_attention_ex_noalloc).
+ */
+int skv_noalloc_init(void);
+
 #ifdef __cplusplus
 }
 #endif

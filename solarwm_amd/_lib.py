@@ -125,6 +125,7 @@ SIGNATURES: dict[str, tuple] = {
     "skv_attention_ex": (_i32, [ctypes.POINTER(AttentionDesc), _vp]),
     "skv_attention_plan": (_i32, [ctypes.POINTER(AttentionDesc), ctypes.POINTER(LaunchPlan)]),
     "skv_attention_ex_noalloc": (_i32, [ctypes.POINTER(AttentionDesc), _vp]),
+    "skv_noalloc_init": (_i32, []),
     "skv_append_workspace_size": (_i32, [ctypes.POINTER(AppendDesc), ctypes.POINTER(_i64)]),
 }
 

@@ -22,16 +22,29 @@ std::mutex g_mu;
 void* g_scratch[kMaxDevices] = {};  // device address of `scratch` on each device
 
 // The device address of this device's copy of `scratch`, looked up once per device with that
-// device current (host code never uses the array's name as an address).
-int scratch_ptr(void** out) {
+// device current (host code never uses the array's name as an address).  The first lookup on a
+// device loads this file's code object there (deferred loading) and places the array, which a
+// stream under graph capture must not do: with `stream` capturing and no address known yet the
+// call fails and names skv_noalloc_init, which callers make once per device before capturing.
+int scratch_ptr(void** out, skv_stream_t stream, bool from_init) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    skv::set_error("skv_attention_ex_noalloc: no usable current device (%s)",
+    skv::set_error("%s: no usable current device (%s)",
+                   from_init ? "skv_noalloc_init" : "skv_attention_ex_noalloc",
                    e != hipSuccess ? hipGetErrorString(e) : "device index out of range");
     return SKV_E_LAUNCH;
   }
   std::lock_guard<std::mutex> g(g_mu);
+  if (!g_scratch[dev] && !from_init) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs) == hipSuccess &&
+        cs != hipStreamCaptureStatusNone) {
+      skv::set_error("skv_attention_ex_noalloc: the scratch array of device %d is not set up; "
+                     "call skv_noalloc_init() with that device current before capturing", dev);
+      return SKV_E_UNSUPPORTED;
+    }
+  }
   if (!g_scratch[dev]) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -70,8 +83,14 @@ extern "C" int skv_attention_ex_noalloc(const skv_attention_desc* d, skv_stream_
   }
   void* ws = nullptr;
   if (plan.workspace_bytes > 0) {
-    st = scratch_ptr(&ws);
+    st = scratch_ptr(&ws, stream, false);
     if (st != SKV_OK) return st;
   }
   return skv::attention_with_workspace(d, ws, ws ? kScratchBytes : 0, stream, nullptr);
+}
+
+extern "C" int skv_noalloc_init(void) {
+  skv::clear_error();
+  void* p = nullptr;
+  return scratch_ptr(&p, nullptr, true);
 }

@@ -313,3 +313,21 @@ def test_append_workspace_query():
     assert need(4, 12, 1560, _lib.SKV_BF16) == 0
     assert need(16, 24, 1560, _lib.SKV_FP8_E4M3) == 0  # 2304 units fill the chip per unit
     assert lib.skv_append_workspace_size(None, None) == _lib.SKV_E_ARG
+
+
+def test_library_launches_nothing_cooperatively():
+    """No entry point launches a kernel cooperatively: the one-pass fp8 append sizes its grid
+    from the occupancy query and launches it plainly (its waits are bounded).  A cooperative
+    launch of that kernel, in a build that was never part of the library, was running when a
+    rocprofv3-traced process crashed in the runtime's exit handlers."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    res = subprocess.run([nm, "-D", "--undefined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True)
+    imports = {w.split("@")[0] for w in res.stdout.split() if w != "U"}
+    assert "hipLaunchKernel" in imports or "__hipPushCallConfiguration" in imports
+    assert not {s for s in imports if "Cooperative" in s}, imports
