@@ -9,9 +9,12 @@ cache_update_policy "none" and 1 commit pass, each pass running the cached self-
 30 layers (append of the chunk into staging slots + attention over sink | window | chunk) and
 the commit pass advancing every layer's slot table.  Projections/FFN are outside the path.
 
-Printed JSON (one line): value = latent frames/s of the timed chunks (3 frames per chunk);
-roofline = the attention kernel's algorithmic TFLOP/s (4*Lq*Lk*H*D per launch, from HIP events
-around every launch in the timed region) against dense bf16 MFMA peak; cpu_baseline = the
+Printed JSON (one line): value = latent frames/s of K timed steady-state chunks (3 frames per
+chunk), each attending over the full 21-frame window: the chunks that fill the window run first,
+untimed, so the figure does not depend on K; configured_run = the 27 chunks of BASELINE's run
+from an empty cache, ramp-up included, beside it.  roofline = the attention kernel's algorithmic
+TFLOP/s (4*Lq*Lk*H*D per launch, from HIP events around every 7th launch in the timed region)
+against dense bf16 MFMA peak; cpu_baseline = the
 reference op sequence (clone, memmove, slice-assign, cat, bf16 SDPA) restated on the host CPU
 for one steady-state layer pass, extrapolated; reference_gpu = the same op sequence with
 PyTorch-ROCm on the GPU (SDPA flash backend) over the same chunks.
@@ -49,6 +52,8 @@ HBM_PEAK_GBPS = 8000.0
 # factors are what the same counters read for a 1 GiB device copy.  Counters cannot be read
 # from inside the process, so the figure is recorded here for the config it was measured on.
 ATTN_TRAFFIC_BYTES = {"c2": 351.83e6}
+ATTN_TRAFFIC_SOURCE = ("recorded constant, not measured in this run: rocprofv3 --pmc FETCH_SIZE "
+                       "and WRITE_SIZE runs of `bench.py --probe` (profiles/attn_kernel_c2_traffic.txt)")
 # Launch timing inside the timed rollout: HIP events around every 7th launch of each kind
 # (7 is coprime with the 150 launches of a chunk, so the samples rotate over layers and
 # passes).  A timing event waits for the work before it; events around every launch cost
@@ -1043,12 +1048,25 @@ def c5_quality(device, hs=slice(4, 6), rows=slice(1500, 1756)):
                 "normalised_max": float((e / rms_v).max()),
                 "normalised_mean": float((e / rms_v).mean())}
 
+    alone = err("decoded", "bf16")
+    whole = err("fp8", "bf16")
     res = {
+        "north_star_fp8_bar": {
+            "max_abs": 3e-2,
+            "met": whole["max_abs"] <= 3e-2,
+            "fp8_cache_max_abs": whole["max_abs"],
+            "e4m3_cache_alone_max_abs": alone["max_abs"],
+            "note": "unmet by the quantisation recipe itself: one absmax/448 scale per (head, "
+                    "frame) leaves the x20 outlier channels' e4m3 steps far above 3e-2, and the "
+                    "bf16 kernel over the decoded fp8 cache (no fp8 arithmetic) already misses "
+                    "the bar by the e4m3_cache_alone figure; the tests bound the kernel's own "
+                    "error against the quantisation-aware oracle instead",
+        },
         "cache_bytes_per_layer_bf16": mem["bf16"],
         "cache_bytes_per_layer_fp8": mem["fp8"],
         "memory_saved_pct": round(100 * (1 - mem["fp8"] / mem["bf16"]), 2),
-        "fp8_vs_bf16_cache": err("fp8", "bf16"),
-        "e4m3_cache_alone": err("decoded", "bf16"),
+        "fp8_vs_bf16_cache": whole,
+        "e4m3_cache_alone": alone,
         "fp8_kernel_arithmetic": err("fp8", "decoded"),
         "note": "fp8_vs_bf16_cache = e4m3_cache_alone (bf16 kernel over decoded fp8 frames vs the "
                 "bf16 cache) + fp8_kernel_arithmetic (fp8 kernel vs that decoded run); the "
@@ -1193,11 +1211,29 @@ def main():
     torch.cuda.synchronize()
     log("[bench] warmup done")
 
-    st = timed_rollout(cfg, inputs, caches, range(K))
+    # steady state: fill the window untimed (chunks 0..full_from-1, whose windows are still
+    # growing), then time K chunks whose attention sees the whole cache window; the result no
+    # longer depends on how many ramp-up chunks a short --steps run includes
+    full_from = max(0, -(-cfg["cap_f"] // cfg["chunk_f"]) - 1)
+    run_ours(cfg, inputs, caches, range(full_from))
+    torch.cuda.synchronize()
+    timed_ids = range(full_from, full_from + K)
+    st = timed_rollout(cfg, inputs, caches, timed_ids)
     wall, fps = st["wall_s"], st["frames_per_s"]
     achieved = st["attn_tflops"]
     log(f"[bench] chunk ms: {[round(x, 2) for x in st['chunk_ms']]}")
-    log(f"[bench] ours: {wall:.3f} s for {K} chunks -> {fps:.3f} latent frames/s; attention "
+    # the configured run beside it: chunks 0..chunks-1 from an empty cache, ramp-up included
+    for c in caches:
+        c.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_ours(cfg, inputs, caches, range(cfg["chunks"]))
+    torch.cuda.synchronize()
+    full_wall = time.perf_counter() - t0
+    full_fps = cfg["chunk_f"] * cfg["batch"] * cfg["chunks"] / full_wall
+    log(f"[bench] configured run: {cfg['chunks']} chunks from an empty cache in {full_wall:.3f} s "
+        f"-> {full_fps:.3f} latent frames/s")
+    log(f"[bench] ours: {wall:.3f} s for {K} steady chunks -> {fps:.3f} latent frames/s; attention "
         f"{st['attn_launches']} timed launches avg {st['attn_avg_ms']:.3f} ms, {achieved:.1f} TFLOP/s "
         f"(steady {st['attn_steady_ms']:.3f} ms, {st['attn_steady_tflops']:.1f} TFLOP/s); "
         f"append {st['append_gbps']:.0f} GB/s")
@@ -1221,8 +1257,9 @@ def main():
             "workload": (
                 f"{cfg['workload']} kv-cache rollout: {cfg['layers']} layers, H{cfg['heads']}xD128, "
                 f"{T} tok/frame, chunk {cfg['chunk_f']} frames (Lq {Lq}), cache {cfg['cap_f']} "
-                f"frames ({cfg['cap_f'] * T} tokens), sink {cfg['sink_f']} frame, chunks 0..{K - 1} "
-                "x (4 none + 1 commit) passes"
+                f"frames ({cfg['cap_f'] * T} tokens), sink {cfg['sink_f']} frame, steady state: "
+                f"chunks {full_from}..{full_from + K - 1} (full window; chunks 0..{full_from - 1} "
+                "fill it untimed) x (4 none + 1 commit) passes"
             ),
             "batch": cfg["batch"],
             "layers": cfg["layers"],
@@ -1238,6 +1275,7 @@ def main():
             "frac": round(achieved / peak, 4),
             "traffic": ATTN_TRAFFIC_BYTES.get(args.config),
             "traffic_per": "steady-state launch (Lk = cache window), rocprofv3 FETCH_SIZE + WRITE_SIZE",
+            "traffic_source": ATTN_TRAFFIC_SOURCE,
             "launches_timed": st["attn_launches"],
             "timed_every": EVENT_EVERY,
             "avg_launch_ms": round(st["attn_avg_ms"], 4),
@@ -1245,11 +1283,12 @@ def main():
                              "achieved": round(st["attn_steady_tflops"], 2)},
         },
         "attn_mfma_util_pct": round(100 * achieved / peak, 2),
-        "steady_state": {
-            "frames_per_s": round(st["steady_frames_per_s"], 4) if st["steady_frames_per_s"] else None,
-            "chunks": st["steady_chunks"],
-            "note": "chunks whose attention window is full (21 frames), timed by HIP events at chunk "
-                    "boundaries inside the same rollout",
+        "configured_run": {
+            "frames_per_s": round(full_fps, 4),
+            "chunks": cfg["chunks"],
+            "wall_s": round(full_wall, 4),
+            "note": f"BASELINE's run length: chunks 0..{cfg['chunks'] - 1} from an empty cache "
+                    f"(the first {full_from} see growing windows), wall clock, no launch events",
         },
         "append_in_rollout": {
             "gbps": round(st["append_gbps"], 1),
@@ -1295,9 +1334,11 @@ def main():
             d["v"].zero_()
             d["g"] = d["l"] = 0
         torch.cuda.synchronize()
+        reference_gpu_step(cfg, inputs, dense, range(full_from))  # fill, untimed
+        torch.cuda.synchronize()
         log("[bench] reference GPU path: timing")
         t0 = time.perf_counter()
-        reference_gpu_step(cfg, inputs, dense, range(K))
+        reference_gpu_step(cfg, inputs, dense, timed_ids)
         torch.cuda.synchronize()
         rwall = time.perf_counter() - t0
         rfps = cfg["chunk_f"] * K / rwall
@@ -1305,6 +1346,7 @@ def main():
             "value": round(rfps, 4),
             "unit": "latent frames/s",
             "kind": "reference op sequence on PyTorch-ROCm (clone, memmove, cat, SDPA flash)",
+            "chunks": f"{full_from}..{full_from + K - 1} (the same steady-state chunks)",
             "speedup": round(fps / rfps, 3),
         }
         log(f"[bench] reference GPU: {rwall:.3f} s -> {rfps:.3f} frames/s; speedup {fps / rfps:.2f}x")
