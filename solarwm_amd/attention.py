@@ -28,9 +28,10 @@ from .rope import positions as rope_positions
 
 
 def _pack_dense(k: torch.Tensor, v: torch.Tensor, pool_dtype: torch.dtype):
-    """Stage dense K/V [B, L, H, D] as a one-frame pool (V transposed) for the kernel."""
+    """Stage dense K/V [B, L, H, D] as a one-frame pool (V transposed) for the kernel, in this
+    stream's reused staging buffer (no allocation or zero-fill per call)."""
     b, lk, h, _ = k.shape
-    kpool, vpool, _, _ = kernels.new_pools(1, b, h, lk, pool_dtype, k.device)
+    kpool, vpool = kernels.staging_pools(1, b, h, lk, pool_dtype, k.device)
     kernels.append_frames(k, v, kpool, vpool, [0], frame_tokens=lk)
     return kpool, vpool
 

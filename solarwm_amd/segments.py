@@ -70,7 +70,7 @@ def teacher_forcing_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     lists = teacher_forcing_frame_lists(num_frames=num_frames, num_frame_per_block=num_frame_per_block,
                                         max_prior_clean_chunks=max_prior_clean_chunks, sink_size=sink_size)
     kv_dtype = k.dtype if k.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
-    kp, vp, _, _ = kernels.new_pools(2 * num_frames, b, h, T, kv_dtype, q.device)
+    kp, vp = kernels.staging_pools(2 * num_frames, b, h, T, kv_dtype, q.device)
     kernels.append_frames(k.to(kv_dtype), v.to(kv_dtype), kp, vp, list(range(2 * num_frames)),
                           frame_tokens=T)
     qq = q if q.dtype in (torch.bfloat16, torch.float32) else q.to(kv_dtype)

@@ -151,6 +151,54 @@ def test_fp8_append_one_pass_slices(gpu, monkeypatch, B, T, forced):
     assert torch.equal(kpool[1].view(torch.uint8), torch.full_like(kpool[1].view(torch.uint8), 0x55))
 
 
+def test_kept_fp8_append_outlives_workspace_growth(gpu):
+    """A kept fp8 append launcher (few units: the one-pass kernel with this stream's workspace)
+    must hold its workspace block.  An attention launch that takes the split grows the stream's
+    workspace in between; a sentinel of the old block's size is then allocated, and the kept
+    launcher runs again: the sentinel is untouched and the codes still match the oracle."""
+    B, H, T, nf = 4, 12, 1560, 3
+    _say("kept fp8 append across workspace growth", B, H, T, nf)
+    g = torch.Generator().manual_seed(90)
+    x = torch.randn((B, nf * T, H, 128), generator=g)
+    x[..., torch.randperm(128, generator=g)[:2]] *= 20.0
+    x = x.to(torch.bfloat16)
+    v = (x.float() * 0.5).to(torch.bfloat16)
+    kpool, vpool, ks, vs = kernels.new_pools(5, B, H, T, torch.float8_e4m3fn, gpu)
+    slots = [3, 0, 4]
+    key = (gpu.index or 0, kernels._stream(gpu))
+    torch.cuda.synchronize()
+    kernels._workspaces.pop(key, None)  # start from no workspace (earlier tests grew it)
+    launch = kernels.prepare_append(x.to(gpu), v.to(gpu), kpool, vpool, slots, frame_tokens=T,
+                                    kscale=ks, vscale=vs)
+    desc = next(o for o in launch.keep if isinstance(o, _lib.AppendDesc))
+    ws_small = launch.keep[-1]
+    assert ws_small is not None and desc.workspace == ws_small.data_ptr()
+    small_bytes = ws_small.numel()
+    del ws_small  # from here on only the launcher holds the block
+    launch()
+    # grow the workspace: one frame of queries over 6 frames splits over every CU
+    qa = _rand((1, T, 12, 128), 91, torch.bfloat16).to(gpu)
+    ka = _rand((1, 6 * T, 12, 128), 92, torch.bfloat16)
+    apool, bpool, aslots = _pool_from(ka, ka, T, torch.bfloat16, gpu)
+    plan = kernels.attention_plan(qa, apool, bpool, aslots, frame_tokens=T)
+    assert plan["split"] >= 1 and plan["workspace_bytes"] > desc.workspace_bytes, plan
+    kernels.attention_frames(qa, apool, bpool, aslots, frame_tokens=T)
+    torch.cuda.synchronize()
+    assert kernels._workspaces[key].data_ptr() != desc.workspace  # the stream's was replaced
+    sentinel = torch.full((small_bytes,), 0xA5, dtype=torch.uint8, device=gpu)
+    kpool.view(torch.uint8).fill_(0x55), vpool.view(torch.uint8).fill_(0x55)
+    launch()
+    torch.cuda.synchronize()
+    assert int((sentinel != 0xA5).sum()) == 0, "the kept launcher wrote into a freed workspace"
+    for f, s in enumerate(slots):
+        for src, pool, sc, vt in ((x, kpool, ks, False), (v, vpool, vs, True)):
+            codes, scale = ref.fp8_quantize(src[:, f * T : (f + 1) * T].permute(0, 2, 1, 3))
+            got = pool[s].cpu()
+            got = got[..., :T].transpose(-1, -2) if vt else got[:, :, :T]
+            assert torch.equal(got.view(torch.uint8), codes.view(torch.uint8)), (f, vt)
+            assert torch.equal(sc[s].cpu(), scale), (f, vt)
+
+
 def _pool_from(k, v, T, dtype, device, perm_seed=0):
     """Store dense K/V [B, n*T, H, D] frame by frame in shuffled slots; return pools + order."""
     B, L, H, _ = k.shape
@@ -256,6 +304,25 @@ def test_dropin_attention_signature(gpu):
     assert_attn_close(out[0], ref.attention(q[:1], k[:1, :77], v[:1, :77])[0])
     assert_attn_close(out[1, :120], ref.attention(q[1:, :120], k[1:], v[1:])[0])
     assert out[1, 120:].abs().sum() == 0
+
+
+def test_dropin_attention_reuses_staging_without_zero_fill(gpu):
+    """attention() stages dense K/V in this stream's reused buffer, which it never zero-fills: a
+    first call grows the buffer, the buffer is then filled with NaN, and a smaller call whose
+    390-key window leaves 58 padding rows in its slot must still match the oracle (the append
+    writes every row of the slot) without reallocating the buffer."""
+    q1, k1, v1 = (_rand((1, L, 3, 128), 80 + i, torch.bfloat16) for i, L in enumerate((300, 1000, 1000)))
+    out1 = attention(q1.to(gpu), k1.to(gpu), v1.to(gpu))
+    torch.cuda.synchronize()
+    assert_attn_close(out1, ref.attention(q1, k1, v1))
+    key = (gpu.index or 0, kernels._stream(gpu), torch.bfloat16)
+    buf = kernels._staging[key]
+    buf.fill_(float("nan"))
+    q2, k2, v2 = (_rand((2, L, 2, 128), 90 + i, torch.bfloat16) for i, L in enumerate((100, 390, 390)))
+    out2 = attention(q2.to(gpu), k2.to(gpu), v2.to(gpu))
+    torch.cuda.synchronize()
+    assert kernels._staging[key] is buf
+    assert_attn_close(out2, ref.attention(q2, k2, v2))
 
 
 def test_full_size_closed_form_identical_keys(gpu):

@@ -2,8 +2,9 @@
 (oracle/wan_cache_ref.py attention, attention.py:141-188 of the reference).
 
 Each case draws a frame size (multiples of 8 that pack key tiles across frames, and sizes that do
-not), a window of frames stored in shuffled slots of a larger pool, a query count (one row,
-ragged q-tiles, under-filled grids that take the balanced key split), heads, streams, the pool
+not, odd ones included: 135 and the release geometry's 405), a window of frames stored in
+shuffled slots of a larger pool, a query count (one row, ragged q-tiles, under-filled grids that
+take the balanced key split), heads, streams, the pool
 dtype and the mask (none, or chunk-causal with the chunk limit anywhere in the window).  The
 launch plan's key-tile count is checked against the packing rule, so the cases cover both tile
 walks.  Bars: tests/helpers.py."""
@@ -20,7 +21,7 @@ from .helpers import assert_attn_close
 
 pytestmark = pytest.mark.gpu
 
-FRAME_SIZES = [64, 72, 96, 100, 136, 200, 256, 390, 520, 880, 1000, 1560]
+FRAME_SIZES = [64, 72, 96, 100, 135, 136, 200, 256, 390, 405, 520, 880, 1000, 1560]
 Q_LENS = [1, 37, 130, 256, 600, 1170]
 
 
@@ -41,7 +42,7 @@ def _case(seed):
     return T, n, H, B, Lq, pool, qdt, causal, r.randrange(1 << 30)
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(32))
 def test_random_shape_vs_oracle(gpu, seed):
     T, n, H, B, Lq, pool, qdt, causal, s = _case(seed)
     print("case", seed, dict(T=T, n=n, H=H, B=B, Lq=Lq, pool=pool, q=qdt, causal=causal), flush=True)
