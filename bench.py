@@ -1376,6 +1376,18 @@ def main():
         log(f"[bench] aux c2_rope: {aux['c2_rope']}")
         aux["c2_prope"] = c2_rope(dev, prope=True)
         log(f"[bench] aux c2_prope: {aux['c2_prope']}")
+        for name, kw in (("c5_rope", dict(rope=True)), ("c5_prope", dict(prope=True))):
+            log(f"[bench] aux {name}: fp8 cache with RoPE on load")
+            r = steady_state("c5", dev, timed=2, **kw)
+            aux[name] = {"frames_per_s": round(r["frames_per_s"], 4),
+                         "attn_tflops": round(r["attn_tflops"], 1),
+                         "attn_avg_ms": round(r["attn_avg_ms"], 4),
+                         "attn_frac_bf16_peak": round(r["attn_tflops"] / BF16_PEAK_TFLOPS, 4),
+                         "append_avg_us": round(r["append_avg_us"], 2),
+                         "workload": r["workload"],
+                         "note": "fp8 raw frames plus fp8 RoPE (PRoPE) copies; the attention "
+                                 "decodes each staged tile to bf16 and multiplies in bf16"}
+            log(f"[bench] aux {name}: {aux[name]}")
         aux["commit_path"] = commit_path(dev)
         log(f"[bench] aux commit_path: {aux['commit_path']}")
         aux["segments"] = segments_leg(dev)

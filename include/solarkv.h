@@ -220,6 +220,10 @@ int skv_rms_rows(const void* x, int dtype, int64_t sb, int64_t st, int64_t sh, i
  *   kr_pool, rope_hw, grid_h, grid_w: the RoPE copy of K (skv_append_rope).
  *   vx_pool, kv_xform: the PRoPE copies (skv_append_prope; kr_pool then receives K with RoPE and
  *     P⁻¹ on its spatial groups).
+ *   kr_scale, vx_scale: fp8 pools only, the copies' own scales ([n_slots][batch][heads] float32,
+ *     absmax / 448 of each written (slot, stream, head) of kr_pool / vx_pool).  A copy's codes
+ *     are the e4m3 encoding of exactly the value a bf16 (f32 for f32 sources) copy would hold;
+ *     fp8 copies need the workspace skv_append_workspace_size reports.
  */
 typedef struct skv_append_desc {
   const void* k_new;
@@ -245,6 +249,8 @@ typedef struct skv_append_desc {
   const float* kv_xform;
   void* workspace;         /* device, optional, 4-byte aligned (8 for the one-pass fp8 kernel) */
   int64_t workspace_bytes; /* its size; must cover skv_append_workspace_size */
+  float* kr_scale;         /* fp8 pools with kr_pool */
+  float* vx_scale;         /* fp8 pools with vx_pool */
 } skv_append_desc;
 
 int skv_append_ex(const skv_append_desc* desc, skv_stream_t stream);

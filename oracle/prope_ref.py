@@ -123,6 +123,41 @@ def apply_tiled(feats: torch.Tensor, matrix: torch.Tensor) -> torch.Tensor:
     return out.reshape(b, l, h, d)
 
 
+SPATIAL0 = 44  # first channel of the height/width RoPE pairs (22 temporal pairs before them)
+
+
+def fp8_prope_copies_effective(k: torch.Tensor, v: torch.Tensor, p_inv: torch.Tensor,
+                               grid_hw: tuple[int, int], freqs: torch.Tensor,
+                               frame_seqlen: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Raw (K, V) [B, n*T, H, D] -> the raw K and V a camera-aware fp8 cache effectively attends
+    with (float64), for the per-token P⁻¹ ``p_inv`` [B, n*T, 4, 4] of ``projection_matrices``.
+
+    The cache keeps K's copy as [temporal groups raw | P⁻¹ on the spatial groups of its
+    height/width-roped values] and V's copy as P⁻¹ v, each the value a bf16 copy holds,
+    quantised per (frame, stream, head) with its own absmax/448.  Undoing the copies' transforms
+    on the decoded values (the exact inverse of ``p_inv`` on K's spatial groups and the conjugate
+    height/width table; the same inverse on V) gives the inputs whose RoPE-then-PRoPE in
+    ``cached_self_attention(prope=...)`` reproduce the decoded copies.  (``p_inv`` inverts the
+    rotation by its transpose, so it is P's inverse only to float32 accuracy; its own inverse is
+    used.)  Not a reference function (the reference has no fp8 cache).
+    """
+    p = torch.linalg.inv(p_inv.double())
+    from .wan_cache_ref import fp8_fake_quant_frames, rope_frames
+
+    nf = k.shape[1] // frame_seqlen
+    zero = [0] * nf
+    kr = rope_frames(k.double(), grid_hw, zero, freqs)
+    kx = kr.clone()
+    kx[..., SPATIAL0:] = apply_tiled(kr[..., SPATIAL0:], p_inv.double())
+    kq = fp8_fake_quant_frames(kx.to(torch.bfloat16).float(), frame_seqlen).double()
+    kr_eff = kq.clone()
+    kr_eff[..., SPATIAL0:] = apply_tiled(kq[..., SPATIAL0:], p.double())
+    k_eff = rope_frames(kr_eff, grid_hw, zero, freqs.conj())
+    vx = apply_tiled(v.double(), p_inv.double()).to(torch.bfloat16)
+    v_eff = apply_tiled(fp8_fake_quant_frames(vx.float(), frame_seqlen).double(), p.double())
+    return k_eff, v_eff
+
+
 def prope_qkv_separate(q, k, v, *, q_viewmats, q_ks, kv_viewmats, kv_ks,
                        transform: str = "linear", emulate_bf16: bool = False):
     """PRoPE with separate query and key/value cameras (camera_prope.py:93-180), in the

@@ -439,6 +439,24 @@ def fp8_fake_quant_rows(q: torch.Tensor) -> torch.Tensor:
     return fp8_dequantize(codes, scale).squeeze(-2)
 
 
+def fp8_rope_copy_effective(k: torch.Tensor, grid_hw: tuple[int, int], freqs: torch.Tensor,
+                            frame_seqlen: int) -> torch.Tensor:
+    """Raw K [B, n*T, H, D] -> the raw K a pre-RoPE fp8 cache effectively attends with (float64).
+
+    The cache keeps a copy of K with its height/width pairs rotated (temporal pairs raw), the
+    value a bf16 copy holds, quantised per (frame, stream, head) with its own absmax/448; the
+    attention reads that copy.  Rotating the decoded copy back (the conjugate table at temporal
+    position 0) gives the K whose window RoPE (``cached_self_attention(rope=...)``) reproduces
+    the decoded copy exactly, so the oracle's own RoPE path runs on the quantised values.  Not
+    a reference function: the reference has no fp8 cache (BASELINE config 5 defines the scales).
+    """
+    nf = k.shape[1] // frame_seqlen
+    zero = [0] * nf
+    copy = rope_frames(k.double(), grid_hw, zero, freqs).to(torch.bfloat16)
+    deq = fp8_fake_quant_frames(copy.float(), frame_seqlen).double()
+    return rope_frames(deq, grid_hw, zero, freqs.conj())
+
+
 def e4m3_decode(code: int) -> float:
     """Value of an e4m3fn byte from its fields (bias 7; e=0 subnormal; 0x7f/0xff NaN)."""
     s = -1.0 if code & 0x80 else 1.0

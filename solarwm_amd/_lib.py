@@ -48,6 +48,7 @@ class AppendDesc(ctypes.Structure):
         ("k_inv_rms", _vp), ("k_rms_stride_b", _i64), ("k_norm_weight", _vp),
         ("kr_pool", _vp), ("rope_hw", _vp), ("grid_h", _i32), ("grid_w", _i32),
         ("vx_pool", _vp), ("kv_xform", _vp), ("workspace", _vp), ("workspace_bytes", _i64),
+        ("kr_scale", _vp), ("vx_scale", _vp),
     ]
 
 

@@ -241,6 +241,8 @@ def attend_cached(
             vr_pool=kv_cache.vrpool if camera is not None else None,
             kv_xform=camera.kv_xform if camera is not None else None,
             k_norm=_row_norm(k, norm_k, g.heads) if norm_k is not None else None,
+            kr_scale=kv_cache.krscale,
+            vr_scale=kv_cache.vrscale if camera is not None else None,
         )
     frames = list(kv_cache.bank_slots(memory_frames)) if memory_frames else []
     frames.extend(window)
@@ -248,23 +250,31 @@ def attend_cached(
         raise RuntimeError("KV-cache attention window is empty")  # causal_model.py:785-787
     rope_args = prope_args = None
     kpool, vpool = kv_cache.kpool, kv_cache.vpool
+    kscale, vscale = kv_cache.kscale, kv_cache.vscale
+    q_in, out_in = q, out
     if rope is not None:
         nb = q.shape[1] // T
         if nb * T != q.shape[1]:
             raise ValueError("EchoRoPE expects the query chunk to contain whole frames")
-        kpool = kv_cache.krpool
+        kpool, kscale = kv_cache.krpool, kv_cache.krscale
         if camera is not None:
             prope_args = (rope.hw, rope.cfg.grid_hw, camera.q_xform_t, camera.q_xform_s,
                           camera.out_xform)
-            vpool = kv_cache.vrpool
+            vpool, vscale = kv_cache.vrpool, kv_cache.vrscale
         else:
             qpos, kpos = window_positions(kv_cache, plan, window, nb, int(current_start))
             rope_args = (rope.hw, rope.cfg.grid_hw, rope.temporal(qpos, kpos))
+        if kv_cache.dtype == torch.float8_e4m3fn and q.dtype != torch.bfloat16:
+            # the fp8 RoPE kernels take bf16 queries (the bf16-pool kernels round to bf16 on load)
+            q_in = q.to(torch.bfloat16)
+            out_in = None
     x = kernels.attention_frames(
-        q, kpool, vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
-        kscale=kv_cache.kscale, vscale=kv_cache.vscale, out=out, rope=rope_args,
-        prope=prope_args, q_norm=_row_norm(q, norm_q, g.heads) if norm_q is not None else None,
+        q_in, kpool, vpool, frames, frame_tokens=T, softmax_scale=softmax_scale,
+        kscale=kscale, vscale=vscale, out=out_in, rope=rope_args, prope=prope_args,
+        q_norm=_row_norm(q, norm_q, g.heads) if norm_q is not None else None,
     )
+    if x.dtype != q.dtype:
+        x = x.to(q.dtype) if out is None else out.copy_(x)
     update = kv_cache.stage(plan, temp)
     return x, (plan.current_end, plan.local_end_index, update)
 

@@ -340,7 +340,9 @@ class SlotKVCache(Mapping):
 
     With ``rope`` (tables shared by every layer of a model) the cache is pre-RoPE like the
     reference's: ``k``/``v`` hold the raw frames, and ``krpool`` holds each frame's K with its
-    height/width RoPE pairs rotated, which the attention kernel reads (bf16 caches only).
+    height/width RoPE pairs rotated, which the attention kernel reads.  An fp8 cache keeps the
+    copies in fp8 too, each with its own per-(slot, stream, head) scales (``krscale``,
+    ``vrscale``); the attention kernel decodes each staged tile to bf16 and multiplies in bf16.
 
     With ``camera`` (one ``CameraCache`` shared by every layer of a model, fused PRoPE) ``krpool``
     also carries each frame's P⁻¹ on its spatial channel groups once a camera pass wrote it, and
@@ -371,13 +373,17 @@ class SlotKVCache(Mapping):
         )
         self.rope = rope
         self.krpool = None
+        self.krscale = self.vrscale = None  # fp8 caches: the copies' own scales
+        fp8 = dtype == torch.float8_e4m3fn
         if rope is not None:
-            if dtype != torch.bfloat16:
-                raise ValueError(f"RoPE on load needs a bf16 cache, got {dtype}")
+            if dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+                raise ValueError(f"RoPE on load needs a bf16 or fp8 cache, got {dtype}")
             gh, gw = rope.cfg.grid_hw
             if gh * gw != geom.frame_tokens:
                 raise ValueError(f"RoPE grid {gh}x{gw} does not tile {geom.frame_tokens}-token frames")
             self.krpool = torch.zeros_like(self.kpool)
+            if fp8:
+                self.krscale = torch.zeros_like(self.kscale)
         self.camera = camera
         self.first_layer = first_layer
         self.camera_owner = first_layer and camera is not None
@@ -389,6 +395,8 @@ class SlotKVCache(Mapping):
             if gh * gw < kernels.TILE:
                 raise ValueError(f"fused PRoPE needs frames of at least {kernels.TILE} tokens")
             self.vrpool = torch.zeros_like(self.vpool)
+            if fp8:
+                self.vrscale = torch.zeros_like(self.vscale)
         self.slots = SlotTable(geom)
         # the PRoPE self-attention branch's cache of this layer (make_kv_cache_allocator's
         # prope_branch=): the reference's prope_k / prope_v / prope_*_end_index keys
@@ -406,9 +414,9 @@ class SlotKVCache(Mapping):
         if self.camera is not None and self.camera_owner:
             self.camera.reset()
         self.metadata_present = self.first_layer
-        if self.kscale is not None:
-            self.kscale.zero_()
-            self.vscale.zero_()
+        for t in (self.kscale, self.vscale, self.krscale, self.vrscale):
+            if t is not None:
+                t.zero_()
         if self.branch is not None:
             self.branch.reset()
 

@@ -260,6 +260,27 @@ __device__ inline void store4<f16>(f16* p, float x0, float x1, float x2, float x
 // [w*kBpw, (w+1)*kBpw) of the 16.  K block b = (kb = b/8, k-step s = b%8); V^T block
 // b = (db = b/4, kb*2+s2 = b%4).  bf16 pools use direct 16 B global->LDS loads (no registers);
 // fp32 pools (the C1 path, not performance critical) go through registers and are rounded.
+// fp8-e4m3 pool element (one code byte) for attn_kernel's RoPE / PRoPE instances, which decode
+// each staged tile to bf16 with its frame's scale and multiply in bf16.
+struct fp8e4 {
+  uint8_t v;
+};
+
+// 8 e4m3 codes -> 8 bf16 of code x scale (fp32 product, one rounding to bf16)
+__device__ inline bf16x8 decode_e4m3x8(const u32x2& w, float sc) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+    r[4 * i] = (bf16)(lo[0] * sc);
+    r[4 * i + 1] = (bf16)(lo[1] * sc);
+    r[4 * i + 2] = (bf16)(hi[0] * sc);
+    r[4 * i + 3] = (bf16)(hi[1] * sc);
+  }
+  return r;
+}
+
 template <int NW, typename KT>
 struct TileLoader {
   static constexpr int kBpw = 16 / NW;
@@ -302,7 +323,7 @@ struct TileLoader {
         const uint32_t so = (uint32_t)((b >> 3) * 32 * kHeadDim + (b & 7) * 16) * 2u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + b * kBlockBytes), 16, klane, so, 0, 0);
       }
-    } else {
+    } else if constexpr (sizeof(KT) == 4) {
       dst += w * kBpw * kBlockBytes;
 #pragma unroll
       for (int j = 0; j < kBpw; ++j) stage(kt + koff + j * 16, dst + j * kBlockBytes);
@@ -317,7 +338,7 @@ struct TileLoader {
         const uint32_t so = (uint32_t)((b >> 2) * 32 * Tp + (b & 3) * 16) * 2u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + b * kBlockBytes), 16, vlane, so, 0, 0);
       }
-    } else {
+    } else if constexpr (sizeof(KT) == 4) {
       dst += w * kBpw * kBlockBytes;
 #pragma unroll
       for (int j = 0; j < kBpw; ++j) stage(vt + voff + j * 16, dst + j * kBlockBytes);
@@ -325,6 +346,36 @@ struct TileLoader {
   }
   __device__ void stage(const KT* src, char* block) const {
     *reinterpret_cast<bf16x8*>(block + lane16) = Vec8<KT>::load(src).to_bf16();
+  }
+  // fp8 pools: the lane's 8 codes of each of the wave's K / V^T blocks, fetched into registers
+  // at a step's start and decoded into the LDS blocks at its end, so the loads' latency is
+  // covered by the step's products
+  // (buffer loads: one descriptor per tile in SGPRs, the lane's byte offset in a VGPR that never
+  // changes, so no 64-bit address per lane and block)
+  u32x2 kraw[kBpw], vraw[kBpw];
+  __device__ void fetch_k(const KT* kt) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)kt, (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < kBpw; ++j)
+      kraw[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)koff, j * 16, 0));
+  }
+  __device__ void fetch_v(const KT* vt) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)vt, (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < kBpw; ++j)
+      vraw[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, j * 16, 0));
+  }
+  __device__ void commit_k(char* dst, int w, float sc) const {
+    dst += w * kBpw * kBlockBytes + lane16;
+#pragma unroll
+    for (int j = 0; j < kBpw; ++j)
+      *reinterpret_cast<bf16x8*>(dst + j * kBlockBytes) = decode_e4m3x8(kraw[j], sc);
+  }
+  __device__ void commit_v(char* dst, int w, float sc) const {
+    dst += w * kBpw * kBlockBytes + lane16;
+#pragma unroll
+    for (int j = 0; j < kBpw; ++j)
+      *reinterpret_cast<bf16x8*>(dst + j * kBlockBytes) = decode_e4m3x8(vraw[j], sc);
   }
   // Packed tiles (2-byte pools), through one descriptor over the whole pool: the tile's keys
   // kk < bnd come from frame j (byte offset oa of the tile's first key, token t0), the others
@@ -692,6 +743,13 @@ void attn_kernel(AttnArgs a) {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
     return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile;
   };
+  // fp8 pools: scales are [n_slots][B][H]; (b, h) of this workgroup is bh
+  constexpr bool kFp8Pool = sizeof(KT) == 1;
+  const int64_t n_bh = (int64_t)a.B * a.H;
+  [[maybe_unused]] auto tile_scale = [&](const float* sc, int tau) -> float {
+    const int j = (tb + tau) / a.ntiles_f;
+    return sc[(int64_t)a.slots[j] * n_bh + bh];
+  };
   // mask decision for tile tau (uniform): returns true if any key of the tile may be hidden
   auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
@@ -753,6 +811,19 @@ void attn_kernel(AttnArgs a) {
                                 a.T - p.t0, vb_lds(x));
         p.next(a, kbh);
       }
+    } else if constexpr (kFp8Pool) {
+#pragma unroll
+      for (int x = 0; x <= kL; ++x)
+        if (x < ntau) {
+          loader.fetch_k(kpool + tile_base(x));
+          loader.commit_k(kb_lds(x), w, tile_scale(a.kscale, x));
+        }
+#pragma unroll
+      for (int x = 0; x < kL - 1; ++x)
+        if (x < ntau) {
+          loader.fetch_v(vpool + tile_vbase(x));
+          loader.commit_v(vb_lds(x), w, tile_scale(a.vscale, x));
+        }
     } else {
 #pragma unroll
       for (int x = 0; x <= kL; ++x)
@@ -837,6 +908,7 @@ void attn_kernel(AttnArgs a) {
     // K(tau+kL+1) and V(tau+kL-1) (with two buffers: buffer cb, the literal)
     char* const kdst = kRing == 2 ? kb_lds(cb) : kb_lds(tau + kL + 1);
     char* const vdst = kRing == 2 ? vb_lds(cb) : vb_lds(tau + kL - 1);
+    [[maybe_unused]] float ksc_n = 0.f, vsc_n = 0.f;  // fp8 pools: scales of the fetched tiles
     auto issue_loads = [&]() {
       if constexpr (PK) {
         if (tau + kL + 1 < ntau)
@@ -845,6 +917,17 @@ void attn_kernel(AttnArgs a) {
         if (tau + kL - 1 < ntau)
           loader.issue_v_packed(vpool, a.pool_bytes, vp.off + vp.t0 * 2, vp.off_n - (a.T - vp.t0) * 2,
                                 a.T - vp.t0, vdst);
+      } else if constexpr (kFp8Pool) {
+        // codes and scales of K(tau+kL+1) and V(tau+kL-1) into registers now, decoded at the
+        // step's end (the step's products cover the loads' latency)
+        if (tau + kL + 1 < ntau) {
+          loader.fetch_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim);
+          ksc_n = a.kscale[(int64_t)kw.slot * n_bh + bh];
+        }
+        if (tau + kL - 1 < ntau) {
+          loader.fetch_v(vpool + vw.base + vw.t * kTile);
+          vsc_n = a.vscale[(int64_t)vw.slot * n_bh + bh];
+        }
       } else {
         if (tau + kL + 1 < ntau) loader.issue_k(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kdst, w);
         if (tau + kL - 1 < ntau) loader.issue_v(vpool + vw.base + vw.t * kTile, vdst, w);
@@ -992,6 +1075,11 @@ void attn_kernel(AttnArgs a) {
       kw.next(a, kbh);
       vw.next(a, kbh);
       mw.next(a, kbh);
+    }
+    if constexpr (kFp8Pool) {
+      // the codes fetched with the step's loads, decoded into buffers no wave reads this step
+      if (tau + kL + 1 < ntau) loader.commit_k(kdst, w, ksc_n);
+      if (tau + kL - 1 < ntau) loader.commit_v(vdst, w, vsc_n);
     }
     if (kL == 1 || cb == 1) {
       // the loads of the last kL steps have landed; every wave is done with the buffers the
@@ -1708,6 +1796,22 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     }
     return;
   }
+  if (pool_dtype == SKV_FP8_E4M3 && rm > 0) {  // bf16 queries (checked by the caller)
+    if constexpr (NW == 8) {
+      if (a.split) {
+        if (rm == 2)
+          hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 2, true>), grid, block, attn_lds_bytes(NW, 2, 1, true, false), s, a);
+        else
+          hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 1, true>), grid, block, attn_lds_bytes(NW, 1, 1, true, false), s, a);
+        return;
+      }
+    }
+    if (rm == 2)
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 2>), grid, block, attn_lds_bytes(NW, 2, 1, false, false), s, a);
+    else
+      hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 1>), grid, block, attn_lds_bytes(NW, 1, 1, false, false), s, a);
+    return;
+  }
   if (pool_dtype == SKV_FP8_E4M3) {
     if constexpr (NW == 8) {
       if (a.split) {
@@ -1873,8 +1977,9 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     return SKV_E_UNSUPPORTED;
   }
   if (rope) {
-    if (pool_dtype != SKV_BF16) {
-      set_error("skv_attention_rope: only bf16 pools are supported");
+    // fp8 pools: the bf16 kernel decodes each staged tile with its frame's scale
+    if (!(pool_dtype == SKV_BF16 || (pool_dtype == SKV_FP8_E4M3 && q_dtype == SKV_BF16))) {
+      set_error("skv_attention_rope: bf16 pools, or fp8 pools with bf16 queries, are supported");
       return SKV_E_UNSUPPORTED;
     }
     if (!rope_hw || grid_h <= 0 || grid_w <= 0 || (int64_t)grid_h * grid_w != frame_tokens ||
@@ -2168,10 +2273,6 @@ static int attention_desc(const skv_attention_desc* d, skv_stream_t stream,
   if (d->rope_t && d->q_xform_t) {
     set_error("skv_attention_ex: give rope_t (RoPE) or q_xform_t (RoPE + PRoPE), not both");
     return SKV_E_ARG;
-  }
-  if (d->pool_dtype == SKV_FP8_E4M3 && (d->rope_t || d->q_xform_t)) {
-    set_error("skv_attention_ex: RoPE / PRoPE need bf16 pools");
-    return SKV_E_UNSUPPORTED;
   }
   return attention_impl(d->q, d->q_dtype, d->q_sb, d->q_st, d->q_sh, d->k_pool, d->v_pool,
                         d->k_scale, d->v_scale, d->pool_dtype, d->n_slots, d->frame_slots,

@@ -40,6 +40,9 @@ struct AppendArgs {
   const float* krms;
   int64_t krms_sb;
   const float* kw;
+  // fp8 pools: the copies' scales ([n_slots][B][H], absmax / 448 of each written copy)
+  float* krscale;
+  float* vrscale;
   int32_t slots[SKV_MAX_APPEND_FRAMES];
 };
 
@@ -488,14 +491,15 @@ __global__ __launch_bounds__(1024) void append_fp8_kernel(AppendArgs a) {
 //          as the per-unit kernels reduce it), tile 0 stores the scale amax / 448, every tile
 //          re-reads its rows (L2/MALL resident after pass 1) and stores their codes; rows T..Tp-1
 //          get code 0.  V^T goes through an LDS tile.
+// k_only: the grid holds K units only (u = (f * B + b) * H + h), for the RoPE copy of K.
 struct TileUnit {
   int t, is_v, h, b, f;
-  __device__ explicit TileUnit(const AppendArgs& a) {
+  __device__ TileUnit(const AppendArgs& a, bool k_only) {
     int wg = blockIdx.x;
     t = wg % a.ntiles;
     wg /= a.ntiles;
-    is_v = wg & 1;
-    wg >>= 1;
+    is_v = k_only ? 0 : wg & 1;
+    if (!k_only) wg >>= 1;
     h = wg % a.H;
     wg /= a.H;
     b = wg % a.B;
@@ -503,16 +507,41 @@ struct TileUnit {
   }
 };
 
+// XM = 0: the raw frames (kpool / vpool).  XM = 1: the RoPE copy of K (krpool), K units only.
+// XM = 2: the PRoPE copies, K (krpool: RoPE, then P^-1 on the spatial groups) and V (vrpool:
+// P^-1 on every group).  A copy's value is what append_kernel writes into a bf16 / f32 copy
+// pool (fp32 arithmetic, one rounding to E); the fp8 codes encode that value with the copy's
+// own absmax.
+template <typename E, int XM>
+__device__ inline void copy_xform(Vec8<E>& x, const AppendArgs& a, const TileUnit& u, int row, int col) {
+  if constexpr (XM > 0) {
+    Vec8<float> y = to_f32(x);
+    const float* m = XM == 2 ? a.kv_xf + ((int64_t)u.f * a.B + u.b) * 16 : nullptr;
+    if (!u.is_v) {
+      rope_spatial8(y, col, u.t * kTile + row, a.gh, a.gw, a.rope_hw);
+      if constexpr (XM == 2) {
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg)
+          if (col + 4 * gg >= 2 * kRopeT) xform4(y, gg, m);
+      }
+    } else if constexpr (XM == 2) {
+      xform4(y, 0, m);
+      xform4(y, 1, m);
+    }
+    x = from_f32<E>(y);
+  }
+}
+
 template <typename E>
 __device__ inline const E* tile_src(const AppendArgs& a, const TileUnit& u) {
   return static_cast<const E*>(u.is_v ? a.vsrc : a.ksrc) + (int64_t)u.b * a.s_sb +
          (int64_t)u.h * a.s_sh + ((int64_t)(a.src_frame0 + u.f) * a.T + u.t * kTile) * a.s_st;
 }
 
-template <typename E>
+template <typename E, int XM = 0>
 __global__ __launch_bounds__(256) void fp8_tile_absmax_kernel(AppendArgs a, float* part) {
   __shared__ float red[4];
-  const TileUnit u(a);
+  const TileUnit u(a, XM == 1);
   const E* src = tile_src<E>(a, u);
   const int tid = threadIdx.x, rows = min(kTile, a.T - u.t * kTile);
   const bool knorm = !u.is_v && a.krms;
@@ -530,6 +559,7 @@ __global__ __launch_bounds__(256) void fp8_tile_absmax_kernel(AppendArgs a, floa
     const int row = (tid >> 4) + 16 * i;
     if (row < rows) {
       if (knorm) norm8(x[i], a, u.b, u.h, tok0 + row, col);
+      copy_xform<E, XM>(x[i], a, u, row, col);
       m = absval8(x[i], m);
     }
   }
@@ -556,11 +586,11 @@ __device__ inline u32x2 quant_vec8<float>(const Vec8<float>& v, float inv) {
   return u32x2{lo, hi};
 }
 
-template <typename E>
+template <typename E, int XM = 0>
 __global__ __launch_bounds__(256) void append_fp8_tile_kernel(AppendArgs a, const float* part) {
   constexpr int kRowT = kTile + 4;  // V^T tile row: 64 codes + 4 bytes of skew
   __shared__ __attribute__((aligned(16))) uint8_t vt8[kHeadDim * kRowT];
-  const TileUnit u(a);
+  const TileUnit u(a, XM == 1);
   const E* src = tile_src<E>(a, u);
   const int tid = threadIdx.x, rows = min(kTile, a.T - u.t * kTile);
   const float* pm = part + (int64_t)(blockIdx.x - u.t);
@@ -569,12 +599,13 @@ __global__ __launch_bounds__(256) void append_fp8_tile_kernel(AppendArgs a, cons
   const float inv = amax > 0.f ? 448.0f / amax : 0.f;
   const int64_t slot = a.slots[u.f];
   if (u.t == 0 && tid == 0) {
-    float* sc = u.is_v ? a.vscale : a.kscale;
+    float* sc = XM ? (u.is_v ? a.vrscale : a.krscale) : (u.is_v ? a.vscale : a.kscale);
     sc[(slot * a.B + u.b) * a.H + u.h] = amax / 448.0f;
   }
   const bool knorm = !u.is_v && a.krms;
   const int64_t tok0 = (int64_t)(a.src_frame0 + u.f) * a.T + u.t * kTile;
-  uint8_t* pool = static_cast<uint8_t*>(u.is_v ? a.vpool : a.kpool) + slot * a.slot_stride +
+  void* dst_pool = XM ? (u.is_v ? a.vrpool : a.krpool) : (u.is_v ? a.vpool : a.kpool);
+  uint8_t* pool = static_cast<uint8_t*>(dst_pool) + slot * a.slot_stride +
                   (int64_t)(u.b * a.H + u.h) * a.Tp * kHeadDim;
   u32x2 q[4];
   Vec8<E> x[4];
@@ -586,8 +617,12 @@ __global__ __launch_bounds__(256) void append_fp8_tile_kernel(AppendArgs a, cons
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = (tid >> 4) + 16 * i;
-      if (row >= rows) x[i] = Vec8<E>::zero();
-      else if (knorm) norm8(x[i], a, u.b, u.h, tok0 + row, col);
+      if (row >= rows) {
+        x[i] = Vec8<E>::zero();
+      } else {
+        if (knorm) norm8(x[i], a, u.b, u.h, tok0 + row, col);
+        copy_xform<E, XM>(x[i], a, u, row, col);
+      }
       q[i] = quant_vec8<E>(x[i], inv);
     }
   }
@@ -1035,6 +1070,42 @@ static unsigned int slice_wait_ticks() {
 
 static bool aligned8(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)(8 * bytes)) == 0; }
 
+static int launch_status() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("skv_append: launch failed: %s", hipGetErrorString(e));
+    return SKV_E_LAUNCH;
+  }
+  return SKV_OK;
+}
+
+// The fp8 copies of a pre-RoPE cache (after the raw frames): the tile grids' two passes over
+// the K units (RoPE copy) or the K and V units (PRoPE copies), tile maxima in `part`.
+static int append_fp8_copies(const AppendArgs& a, int src_dtype, int copy_units, void* part_ws,
+                             hipStream_t s) {
+  float* part = static_cast<float*>(part_ws);
+  const dim3 grid(copy_units * a.ntiles), block(256);
+  const bool prope = a.vrpool != nullptr;
+  if (src_dtype == SKV_BF16) {
+    if (prope) {
+      hipLaunchKernelGGL((fp8_tile_absmax_kernel<bf16, 2>), grid, block, 0, s, a, part);
+      hipLaunchKernelGGL((append_fp8_tile_kernel<bf16, 2>), grid, block, 0, s, a, part);
+    } else {
+      hipLaunchKernelGGL((fp8_tile_absmax_kernel<bf16, 1>), grid, block, 0, s, a, part);
+      hipLaunchKernelGGL((append_fp8_tile_kernel<bf16, 1>), grid, block, 0, s, a, part);
+    }
+  } else {
+    if (prope) {
+      hipLaunchKernelGGL((fp8_tile_absmax_kernel<float, 2>), grid, block, 0, s, a, part);
+      hipLaunchKernelGGL((append_fp8_tile_kernel<float, 2>), grid, block, 0, s, a, part);
+    } else {
+      hipLaunchKernelGGL((fp8_tile_absmax_kernel<float, 1>), grid, block, 0, s, a, part);
+      hipLaunchKernelGGL((append_fp8_tile_kernel<float, 1>), grid, block, 0, s, a, part);
+    }
+  }
+  return launch_status();
+}
+
 static int append_impl(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
                        int64_t src_st, int64_t src_sh, int src_frame0, void* k_pool,
                        void* v_pool, float* k_scale, float* v_scale, int pool_dtype,
@@ -1044,7 +1115,8 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
                        const float* kv_xform, skv_stream_t stream,
                        const float* k_inv_rms = nullptr, int64_t rms_sb = 0,
                        const float* k_norm_weight = nullptr, void* workspace = nullptr,
-                       int64_t workspace_bytes = 0, int64_t* ws_query = nullptr) {
+                       int64_t workspace_bytes = 0, int64_t* ws_query = nullptr,
+                       float* kr_scale = nullptr, float* vr_scale = nullptr) {
   if (ws_query) *ws_query = 0;
   if (!k_new || !v_new || !k_pool || !v_pool || !dst_slots) {
     set_error("skv_append: null pointer argument");
@@ -1080,9 +1152,9 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
     return SKV_E_UNSUPPORTED;
   }
   if (kr_pool) {
-    if (fp8) {
-      set_error("skv_append_rope: fp8 pools are not supported");
-      return SKV_E_UNSUPPORTED;
+    if (fp8 && (!kr_scale || (vr_pool && !vr_scale))) {
+      set_error("skv_append_ex: fp8 RoPE / PRoPE copies need kr_scale (and vx_scale with vx_pool)");
+      return SKV_E_ARG;
     }
     if (!rope_hw || grid_h <= 0 || grid_w <= 0 || (int64_t)grid_h * grid_w != frame_tokens) {
       set_error("skv_append_rope: need rope_hw and grid_h * grid_w == frame_tokens (%d x %d vs %d)",
@@ -1095,8 +1167,8 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
       set_error("skv_append_prope: need kx_pool, vx_pool and kv_xform");
       return SKV_E_ARG;
     }
-    if (pool_dtype != SKV_BF16) {
-      set_error("skv_append_prope: only bf16 pools are supported");
+    if (pool_dtype != SKV_BF16 && !fp8) {
+      set_error("skv_append_prope: only bf16 and fp8 pools are supported");
       return SKV_E_UNSUPPORTED;
     }
   }
@@ -1145,6 +1217,8 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   a.krms = k_inv_rms;
   a.krms_sb = rms_sb;
   a.kw = k_norm_weight;
+  a.krscale = kr_scale;
+  a.vrscale = vr_scale;
   for (int f = 0; f < n_frames; ++f) {
     if (dst_slots[f] < 0 || dst_slots[f] >= n_slots) {
       set_error("skv_append: dst_slots[%d]=%d outside [0, %d)", f, dst_slots[f], n_slots);
@@ -1160,9 +1234,25 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
   const int64_t tile_bytes = few_units ? (int64_t)units * a.ntiles * (int64_t)sizeof(float) : 0;
   const int64_t cell_bytes = few_units ? (kSliceHead + (int64_t)units * kSliceMax) * 8 : 0;
   const int64_t ws_need = tile_bytes > cell_bytes ? tile_bytes : cell_bytes;
+  // fp8 copies of a pre-RoPE cache run the tile grids after the raw frames, on the same stream,
+  // with their tile maxima at the workspace's start (the raw append is done with it by then)
+  const int copy_units = fp8 && kr_pool ? n_frames * batch * heads * (vr_pool ? 2 : 1) : 0;
+  const int64_t copy_bytes = (int64_t)copy_units * a.ntiles * (int64_t)sizeof(float);
   if (ws_query) {
-    *ws_query = ws_need;
+    *ws_query = ws_need > copy_bytes ? ws_need : copy_bytes;
     return SKV_OK;
+  }
+  if (copy_units > 0) {
+    if (workspace == nullptr || workspace_bytes < copy_bytes) {
+      set_error("skv_append_ex: fp8 RoPE / PRoPE copies need a workspace of %lld bytes "
+                "(skv_append_workspace_size), got %lld", (long long)copy_bytes,
+                (long long)workspace_bytes);
+      return SKV_E_ARG;
+    }
+    if (reinterpret_cast<uintptr_t>(workspace) % 4) {
+      set_error("skv_append_ex: workspace must be 4-byte aligned");
+      return SKV_E_ARG;
+    }
   }
   bool tile_split = false;
   if (ws_need > 0 && workspace != nullptr) {
@@ -1196,7 +1286,7 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
         hipLaunchKernelGGL(fp8_slice_clear_kernel, dim3((n_words + 255) / 256), dim3(256), 0, s,
                            sy.cells, n_words);
         hipLaunchKernelGGL(append_fp8_slice_kernel, dim3(units * sy.slices), dim3(256), 0, s, a, sy);
-        return SKV_OK;
+        return copy_units ? append_fp8_copies(a, src_dtype, copy_units, workspace, s) : launch_status();
       }
     }
     if (tile_split) {
@@ -1220,6 +1310,7 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
       else
         hipLaunchKernelGGL(append_fp8_kernel<float>, grid, dim3(1024), 0, s, a);
     }
+    if (copy_units) return append_fp8_copies(a, src_dtype, copy_units, workspace, s);
   } else {
     dim3 grid(n_frames * batch * heads * a.ntiles);
     if (src_dtype == SKV_BF16 || src_dtype == SKV_F16) {
@@ -1236,12 +1327,7 @@ static int append_impl(const void* k_new, const void* v_new, int src_dtype, int6
         hipLaunchKernelGGL((append_kernel<float, 0>), grid, dim3(256), 0, s, a);
     }
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    set_error("skv_append: launch failed: %s", hipGetErrorString(e));
-    return SKV_E_LAUNCH;
-  }
-  return SKV_OK;
+  return launch_status();
 }
 
 extern "C" int skv_append(const void* k_new, const void* v_new, int src_dtype, int64_t src_sb,
@@ -1306,7 +1392,7 @@ static int append_desc(const skv_append_desc* d, skv_stream_t stream, int64_t* w
                      d->n_slots, d->dst_slots, d->n_frames, d->batch, d->heads, d->head_dim,
                      d->frame_tokens, d->kr_pool, d->rope_hw, d->grid_h, d->grid_w, d->vx_pool,
                      d->kv_xform, stream, d->k_inv_rms, d->k_rms_stride_b, d->k_norm_weight,
-                     d->workspace, d->workspace_bytes, ws_query);
+                     d->workspace, d->workspace_bytes, ws_query, d->kr_scale, d->vx_scale);
 }
 
 extern "C" int skv_append_ex(const skv_append_desc* d, skv_stream_t stream) {

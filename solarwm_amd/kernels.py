@@ -245,6 +245,8 @@ def prepare_append(
     kv_xform: torch.Tensor | None = None,
     k_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
     use_workspace: bool = True,
+    kr_scale: torch.Tensor | None = None,
+    vr_scale: torch.Tensor | None = None,
 ):
     """Validate an append once and return a zero-argument launcher that enqueues it on the stream
     current now (repeated launches skip the Python-side checks).
@@ -258,7 +260,12 @@ def prepare_append(
     norm's float32 weight); every copy and fp8 code derives from the normalised value.
     ``use_workspace=False`` keeps an fp8 append of few units on the per-unit kernels (no
     scratch); by default it takes the one-pass slice kernel (bf16 sources without ``k_norm``)
-    or the tile-grid kernels, with this stream's workspace."""
+    or the tile-grid kernels, with this stream's workspace.
+
+    fp8 pools with ``kr_pool`` (and ``vr_pool``) take float32 ``kr_scale`` (and ``vr_scale``)
+    shaped like ``kscale``: each copy is the e4m3 encoding, with its own absmax / 448 per (slot,
+    stream, head), of the value a bf16 copy would hold (f32 for f32 sources); the copies need
+    the workspace (``use_workspace=True``)."""
     lib = _lib.load()
     n_slots, b, h = check_pools(kpool, vpool, frame_tokens)
     sb, st, sh = _token_major("k_new", k_new)
@@ -299,6 +306,19 @@ def prepare_append(
     if kr_pool is not None:
         _check_rope_hw(kr_pool, kpool, rope_hw, grid_hw, frame_tokens)
         desc.kr_pool, desc.rope_hw = kr_pool.data_ptr(), rope_hw.data_ptr()
+        if kpool.dtype == torch.float8_e4m3fn:
+            if not use_workspace:
+                raise ValueError("fp8 RoPE / PRoPE copies need the workspace (use_workspace=True)")
+            named = [("kr_scale", kr_scale)] + ([("vr_scale", vr_scale)] if vr_pool is not None else [])
+            for name, t in named:
+                if t is None:
+                    raise ValueError(f"fp8 copies need {name}")
+                _require_cuda(name, t)
+                if t.dtype != torch.float32 or t.shape != kscale.shape or not t.is_contiguous():
+                    raise ValueError(f"{name} must be contiguous float32 {list(kscale.shape)}")
+            desc.kr_scale = kr_scale.data_ptr()
+            if vr_pool is not None:
+                desc.vx_scale = vr_scale.data_ptr()
         desc.grid_h, desc.grid_w = int(grid_hw[0]), int(grid_hw[1])
         moved += n * frame_tokens * b * h * HEAD_DIM * kpool.element_size()
     if k_norm is not None:
@@ -323,7 +343,7 @@ def prepare_append(
     # the workspace tensor is kept too: a later call that grows this stream's workspace drops
     # the shared reference, and this launcher's descriptor still points at the old block
     launch.keep = (k_new, v_new, kpool, vpool, kscale, vscale, slots, kr_pool, rope_hw, vr_pool,
-                   kv_xform, k_norm, desc, args, ws_tensor)
+                   kv_xform, k_norm, kr_scale, vr_scale, desc, args, ws_tensor)
     return launch
 
 
@@ -345,14 +365,18 @@ def append_frames(
     kv_xform: torch.Tensor | None = None,
     k_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
     use_workspace: bool = True,
+    kr_scale: torch.Tensor | None = None,
+    vr_scale: torch.Tensor | None = None,
 ) -> None:
     """Write frames ``src_frame0 + f`` of ``k_new``/``v_new`` ([B, L, H, D]) into ``dst_slots[f]``
     (and, with ``kr_pool``, K with its height/width RoPE pairs rotated into ``kr_pool``; with
-    ``kv_xform``, the PRoPE copies; with ``k_norm``, RMS-normalised K — see ``prepare_append``)."""
+    ``kv_xform``, the PRoPE copies; with ``k_norm``, RMS-normalised K; fp8 copies with their
+    ``kr_scale`` / ``vr_scale`` — see ``prepare_append``)."""
     prepare_append(k_new, v_new, kpool, vpool, dst_slots, frame_tokens=frame_tokens,
                    src_frame0=src_frame0, kscale=kscale, vscale=vscale, kr_pool=kr_pool,
                    rope_hw=rope_hw, grid_hw=grid_hw, vr_pool=vr_pool, kv_xform=kv_xform,
-                   k_norm=k_norm, use_workspace=use_workspace)()
+                   k_norm=k_norm, use_workspace=use_workspace, kr_scale=kr_scale,
+                   vr_scale=vr_scale)()
 
 
 def prepare_gather(

@@ -91,10 +91,10 @@ def test_signature_arity_matches_header():
 def test_rope_argument_errors_do_not_launch():
     lib = _lib.load()
     fake = ctypes.c_void_p(0x1000)
-    # fp8 pools have no RoPE copy path
+    # fp8 pools: the flat entry point carries no copy scales (skv_append_ex does)
     st = lib.skv_append_rope(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, _lib.SKV_FP8_E4M3,
                              4, _slots(0), 1, 1, 1, 128, 64, fake, fake, 8, 8, None)
-    assert st == _lib.SKV_E_UNSUPPORTED and b"fp8" in lib.skv_last_error()
+    assert st == _lib.SKV_E_ARG and b"kr_scale" in lib.skv_last_error()
     # the spatial grid must tile the frame
     st = lib.skv_append_rope(fake, fake, _lib.SKV_BF16, 8, 8, 8, 0, fake, fake, _lib.SKV_BF16,
                              4, _slots(0), 1, 1, 1, 128, 64, fake, fake, 8, 7, None)
@@ -313,6 +313,49 @@ def test_append_workspace_query():
     assert need(4, 12, 1560, _lib.SKV_BF16) == 0
     assert need(16, 24, 1560, _lib.SKV_FP8_E4M3) == 0  # 2304 units fill the chip per unit
     assert lib.skv_append_workspace_size(None, None) == _lib.SKV_E_ARG
+
+
+def test_fp8_copy_workspace_and_arguments():
+    """fp8 pools with RoPE / PRoPE copies: the copies' tile maxima (one float per 64-token tile
+    of each copied unit) join the workspace query, the copies need the workspace and their own
+    scales, all checked before anything launches."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    slots = _slots(0, 1, 2)
+    hw = (ctypes.c_float * 8)()
+
+    def desc(B, H, T, gh, prope=False):
+        d = _lib.AppendDesc(k_new=fake, v_new=fake, src_dtype=_lib.SKV_BF16, src_sb=8, src_st=8,
+                            src_sh=8, k_pool=fake, v_pool=fake, k_scale=fake, v_scale=fake,
+                            pool_dtype=_lib.SKV_FP8_E4M3, n_slots=8, dst_slots=slots, n_frames=3,
+                            batch=B, heads=H, head_dim=128, frame_tokens=T, kr_pool=fake,
+                            rope_hw=ctypes.cast(hw, ctypes.c_void_p), grid_h=gh, grid_w=T // gh,
+                            kr_scale=fake)
+        if prope:
+            d.vx_pool, d.kv_xform, d.vx_scale = fake, fake, fake
+        return d
+
+    def need(d):
+        out = ctypes.c_int64(-1)
+        assert lib.skv_append_workspace_size(ctypes.byref(d), ctypes.byref(out)) == _lib.SKV_OK
+        return out.value
+
+    # 2304 raw units fill the chip (no raw workspace); the K copy: 3 x 16 x 24 units x 25 tiles
+    assert need(desc(16, 24, 1560, 30)) == 3 * 16 * 24 * 25 * 4
+    assert need(desc(16, 24, 1560, 30, prope=True)) == 2 * 3 * 16 * 24 * 25 * 4
+    # C5: the raw one-pass cells are larger than the copy maxima
+    assert need(desc(4, 12, 1560, 30)) == max(128 + 288 * 512, 144 * 25 * 4)
+    d = desc(16, 24, 1560, 30)
+    assert lib.skv_append_ex(ctypes.byref(d), None) == _lib.SKV_E_ARG  # no workspace
+    assert b"workspace" in lib.skv_last_error()
+    d = desc(4, 12, 1560, 30)
+    d.kr_scale = None
+    assert lib.skv_append_ex(ctypes.byref(d), None) == _lib.SKV_E_ARG
+    assert b"kr_scale" in lib.skv_last_error()
+    d = desc(4, 12, 1560, 30, prope=True)
+    d.vx_scale = None
+    assert lib.skv_append_ex(ctypes.byref(d), None) == _lib.SKV_E_ARG
+    assert b"vx_scale" in lib.skv_last_error()
 
 
 def test_library_launches_nothing_cooperatively():

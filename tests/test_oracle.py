@@ -590,3 +590,76 @@ def test_fp8_normalised_bars_reject_a_wrong_frame_scale(B, H, Lq, T, n):
         e = (got - want).abs() / rms_v
         assert float(e.max()) > FP8_NORM_MAX or float(e.mean()) > FP8_NORM_MEAN, (
             float(e.max()), float(e.mean()))
+
+
+# ---------------------------------------------------------------------------------------------
+# fp8 pre-RoPE caches: the effective inputs that make the oracle's own RoPE / PRoPE path attend
+# with the decoded fp8 copies
+# ---------------------------------------------------------------------------------------------
+def _copy_absmax(x, T):
+    """Per (frame, stream, head) absmax of token-major x [B, n*T, H, D]."""
+    B, L, H, D = x.shape
+    return x.reshape(B, L // T, T, H, D).abs().amax(dim=(2, 4))
+
+
+def test_fp8_rope_copy_effective_pins():
+    """Rotating fp8_rope_copy_effective's output forward again gives the decoded copy (the
+    conjugate table undoes the rotation); the decoded copy's per-(frame, head) absmax is the bf16
+    roped copy's, not raw K's (the scale comes from the copy); K with zero spatial channels and
+    e4m3 grid values at a power-of-two scale passes unchanged."""
+    T, grid = 16, (4, 4)
+    f = ref.wan_rope_freqs()
+    g = torch.Generator().manual_seed(71)
+    k = (torch.randn(2, 3 * T, 2, 128, generator=g) * 3).to(torch.bfloat16)
+    k[0, 5, 1, 60], k[0, 5, 1, 61] = 40.0, 0.0  # a spatial pair that rotation spreads
+    keff = ref.fp8_rope_copy_effective(k, grid, f, T)
+    assert keff.dtype == torch.float64
+    fwd = ref.rope_frames(keff, grid, [0, 0, 0], f)
+    copy = ref.rope_frames(k.double(), grid, [0, 0, 0], f).to(torch.bfloat16)
+    assert float((fwd - ref.fp8_fake_quant_frames(copy.float(), T).double()).abs().max()) < 1e-9
+    amax_copy = _copy_absmax(copy.double(), T)
+    amax_raw = _copy_absmax(k.double(), T)
+    assert not torch.allclose(amax_copy, amax_raw)  # the data tells the two scales apart
+    assert torch.allclose(_copy_absmax(fwd, T), amax_copy, rtol=1e-6, atol=0)
+    # exactly representable: spatial channels 0, temporal channels on the e4m3 grid of scale 1/4
+    mag = torch.randint(0, 0x7F, (2 * T * 44,), generator=g)  # 0x7f / 0xff are NaN
+    sign = torch.randint(0, 2, (2 * T * 44,), generator=g) * 0x80
+    vals = torch.tensor([ref.e4m3_decode(int(c)) for c in (mag | sign).tolist()])
+    exact = torch.zeros(1, 2 * T, 1, 128)
+    exact[..., :44] = vals.reshape(1, 2 * T, 1, 44) / 4
+    exact[0, :, 0, 0] = 112.0  # absmax 448 / 4 in every frame: scale 1/4, every value on grid
+    exact = exact.to(torch.bfloat16)
+    assert torch.equal(ref.fp8_rope_copy_effective(exact, grid, f, T), exact.double())
+
+
+def test_fp8_prope_copies_effective_pins():
+    """With identity cameras the PRoPE copies reduce to the RoPE copy of K and the plain fp8
+    frames of V; with real cameras, RoPE then P⁻¹ on K's spatial groups (and P⁻¹ on V) of the
+    effective inputs give the decoded copies, whose per-(frame, head) absmax is the bf16 copy's."""
+    from oracle import prope_ref as pr
+
+    from .cameras import per_token, trajectory
+
+    T, grid, B = 16, (4, 4), 2
+    f = ref.wan_rope_freqs()
+    g = torch.Generator().manual_seed(72)
+    k = torch.randn(B, 2 * T, 2, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, 2 * T, 2, 128, generator=g).to(torch.bfloat16)
+    eye = torch.eye(4, dtype=torch.float64).expand(B, 2 * T, 4, 4)
+    ke, ve = pr.fp8_prope_copies_effective(k, v, eye, grid, f, T)
+    assert torch.equal(ke, ref.fp8_rope_copy_effective(k, grid, f, T))
+    assert torch.equal(ve, ref.fp8_fake_quant_frames(v.float(), T).double())
+    vm, ks = trajectory(B, 2, seed=73, t_scale=0.8)
+    _, _, p_inv = pr.projection_matrices(per_token(vm, T).double(), per_token(ks, T).double())
+    ke, ve = pr.fp8_prope_copies_effective(k, v, p_inv, grid, f, T)
+    kr = ref.rope_frames(ke, grid, [0, 0], f)
+    kx = kr.clone()
+    kx[..., 44:] = pr.apply_tiled(kr[..., 44:], p_inv)
+    copy = ref.rope_frames(k.double(), grid, [0, 0], f)
+    copy[..., 44:] = pr.apply_tiled(copy[..., 44:], p_inv)
+    copy = copy.to(torch.bfloat16)
+    assert float((kx - ref.fp8_fake_quant_frames(copy.float(), T).double()).abs().max()) < 1e-9
+    assert torch.allclose(_copy_absmax(kx, T), _copy_absmax(copy.double(), T), rtol=1e-6, atol=0)
+    vx = pr.apply_tiled(ve, p_inv)
+    vcopy = pr.apply_tiled(v.double(), p_inv).to(torch.bfloat16)
+    assert float((vx - ref.fp8_fake_quant_frames(vcopy.float(), T).double()).abs().max()) < 1e-9
