@@ -564,7 +564,23 @@ def gather_bandwidth(device, iters=24):
     moved = launches[0].bytes_moved
     del kpool, vpool, ko, vo, launches
     torch.cuda.empty_cache()
-    return moved / (ms / 1e3) / 1e9, ms
+    # the same bytes as one plain device copy (torch copy_ of 255.6 MB), three source /
+    # destination pairs in rotation (767 MB each side, three times the 256 MB MALL) so that
+    # neither the reads nor the rewrites are served from the cache
+    n = moved // 4  # bf16 elements per side: K+V of 8 frames
+    gd = torch.Generator(device=device).manual_seed(6)
+    pairs = [(torch.randn(n, generator=gd, device=device, dtype=torch.bfloat16),
+              torch.empty(n, device=device, dtype=torch.bfloat16)) for _ in range(3)]
+    it2 = iter(range(1 << 30))
+
+    def copy():
+        src, dst = pairs[next(it2) % 3]
+        dst.copy_(src)
+
+    copy_ms = _back_to_back_ms(copy, iters)
+    del pairs
+    torch.cuda.empty_cache()
+    return moved / (ms / 1e3) / 1e9, ms, moved / (copy_ms / 1e3) / 1e9
 
 
 def eviction_latency(cfg, iters=2000):
@@ -1308,12 +1324,18 @@ def main():
     log(f"[bench] append ({cfg['chunk_f']} frames, back to back, {n_src} cold sources): "
         f"{app_gbps:.0f} GB/s, {app_ms * 1e3:.1f} us")
 
-    gbps, g_ms = gather_bandwidth(dev)
+    gbps, g_ms, g_copy = gather_bandwidth(dev)
     result["gather_gbps"] = round(gbps, 1)
     result["gather_frac_hbm"] = round(gbps / HBM_PEAK_GBPS, 4)
     result["gather_avg_launch_us"] = round(g_ms * 1e3, 2)
+    result["gather_copy_ceiling_gbps"] = round(g_copy, 1)
+    result["gather_copy_ceiling_note"] = ("torch copy_ of the same 255.6 MB, three cold source / "
+                                          "destination pairs in rotation")
+    result["append_gather_target_note"] = (
+        "north-star target 70% of HBM peak: a plain device copy of the append's bytes reaches "
+        "append_copy_ceiling_gbps and of the gather's gather_copy_ceiling_gbps on this GPU")
     log(f"[bench] gather (C4 bank, 8 of 256 frames, fresh indices per launch): {gbps:.0f} GB/s, "
-        f"{g_ms * 1e3:.1f} us")
+        f"{g_ms * 1e3:.1f} us; same-size copy {g_copy:.0f} GB/s")
     result["eviction"] = eviction_latency(cfg)
     log(f"[bench] eviction: {result['eviction']['host_us_per_layer_pass']} us host per layer pass, "
         f"{result['eviction']['reference_bytes_avoided_per_layer_pass'] / 1e6:.1f} MB of reference "

@@ -132,11 +132,15 @@ def cached_self_attention(
     memory_v: torch.Tensor | None = None,
     rope: dict[str, Any] | None = None,
     prope: dict[str, Any] | None = None,
+    memory_positions: Sequence[int] | None = None,
 ):
     """Returns ``(x [B, Lq, H, D], (current_end, local_end_index, cache_update_info))``.
 
     ``memory_k``/``memory_v`` ([B, M, H, D], already gathered) are placed ahead of the window,
     as the H3 memory path orders ``[bank | history | current]`` (memory_kv_attention.py:97-137).
+    With ``rope`` they are pre-RoPE too and frame f of the bank is rotated at temporal position
+    ``memory_positions[f]`` (the H3 path rotates bank rows at their own positions,
+    memory_kv_attention.py:112-114, :122-131; which positions is the caller's choice here).
 
     ``rope`` (``{"freqs", "grid_hw", "use_echorope", "rope_train_frames"}``) makes ``q``/``k``
     pre-RoPE, as the reference stores them: the cache keeps raw K and the query chunk, sink
@@ -263,10 +267,14 @@ def cached_self_attention(
             q = rope_frames(q, rope["grid_hw"], range(pos["q_start"], pos["q_start"] + nb), rope["freqs"])
             k_cat = rope_frames(k_cat, rope["grid_hw"], range(pos["local_start"], pos["local_start"] + nw),
                                 rope["freqs"])
-    if rope is not None and memory_k is not None:
-        raise NotImplementedError("RoPE with memory-bank frames is outside this restatement")
     if memory_k is not None:
-        k_cat = torch.cat([memory_k.to(k_cat.dtype), k_cat], dim=1)
+        mk = memory_k.to(k_cat.dtype)
+        if rope is not None:
+            nm = mk.shape[1] // frame_seqlen
+            if memory_positions is None or len(memory_positions) != nm:
+                raise ValueError("RoPE with memory-bank frames needs one position per bank frame")
+            mk = rope_frames(mk, rope["grid_hw"], list(memory_positions), rope["freqs"])
+        k_cat = torch.cat([mk, k_cat], dim=1)
         v_cat = torch.cat([memory_v.to(v_cat.dtype), v_cat], dim=1)
     if k_cat.shape[1] == 0:
         raise RuntimeError("KV-cache attention window is empty")

@@ -183,6 +183,7 @@ def attend_cached(
     *,
     sink_recache_after_switch: bool = False,
     memory_frames: Sequence[int] | None = None,
+    memory_positions: Sequence[int] | None = None,
     softmax_scale: float | None = None,
     out: torch.Tensor | None = None,
     camera: CameraPass | None = None,
@@ -197,7 +198,9 @@ def attend_cached(
     The chunk is appended into staging slots, the visible window is the reference's
     ``cat[sink, local]`` (including the chunk), optionally preceded by memory-bank frames
     ``memory_frames`` (bank indices, in order), and nothing in the committed cache changes until
-    :func:`apply_cache_updates`.  ``camera`` (from ``prope.stage_camera_cache``, once per forward
+    :func:`apply_cache_updates`.  In a pre-RoPE cache the bank frames take the temporal RoPE
+    positions ``memory_positions`` (one per bank frame; memory_kv_attention.py:97-137 rotates
+    bank rows at their own positions ahead of the window's), the window its own.  ``camera`` (from ``prope.stage_camera_cache``, once per forward
     for all layers) applies fused PRoPE after RoPE (causal_model.py:1170-1199) and returns the
     output mapped back by the query cameras.  ``norm_q`` / ``norm_k`` (the layer's WanRMSNorm
     modules, or ``(weight, eps)``) take the raw projections: K is normalised inside the append
@@ -220,8 +223,15 @@ def attend_cached(
     )
     T = g.frame_tokens
     rope = kv_cache.rope
-    if rope is not None and memory_frames:
-        raise NotImplementedError("memory-bank frames with RoPE on load are not supported")
+    n_mem = len(memory_frames) if memory_frames else 0
+    if rope is not None and n_mem:
+        if memory_positions is None or len(memory_positions) != n_mem:
+            raise ValueError("memory-bank frames in a pre-RoPE cache need memory_positions "
+                             "(one temporal position per bank frame)")
+        if camera is not None:
+            raise NotImplementedError("memory-bank frames with fused PRoPE are not supported")
+    elif memory_positions is not None and (rope is None or not n_mem):
+        raise ValueError("memory_positions apply to bank frames of a pre-RoPE cache")
     if camera is not None:
         if kv_cache.camera is None or camera.camera is not kv_cache.camera:
             raise ValueError("camera pass was staged for a different cache (allocate with prope=)")
@@ -263,6 +273,8 @@ def attend_cached(
             vpool, vscale = kv_cache.vrpool, kv_cache.vrscale
         else:
             qpos, kpos = window_positions(kv_cache, plan, window, nb, int(current_start))
+            if n_mem:
+                kpos = [int(p) for p in memory_positions] + list(kpos)
             rope_args = (rope.hw, rope.cfg.grid_hw, rope.temporal(qpos, kpos))
         if kv_cache.dtype == torch.float8_e4m3fn and q.dtype != torch.bfloat16:
             # the fp8 RoPE kernels take bf16 queries (the bf16-pool kernels round to bf16 on load)

@@ -445,12 +445,19 @@ class SlotKVCache(Mapping):
         return self.slots.bank_slots(indices)
 
     def write_bank(self, indices: Sequence[int], k: torch.Tensor, v: torch.Tensor) -> None:
-        """Store frames of ``k``/``v`` ([B, len(indices)*T, H, D]) in memory-bank entries."""
-        if self.rope is not None:
-            raise NotImplementedError("memory-bank frames with RoPE on load are not supported")
+        """Store frames of ``k``/``v`` ([B, len(indices)*T, H, D]) in memory-bank entries.  A
+        pre-RoPE cache also writes each frame's height/width-roped K copy (their temporal
+        positions are given per attention call, ``attend_cached(memory_positions=...)``);
+        camera-aware caches keep no per-bank-frame cameras, so they take no bank frames."""
+        if self.camera is not None:
+            raise NotImplementedError("memory-bank frames in a camera-aware (PRoPE) cache are not "
+                                      "supported")
+        rope = self.rope
         kernels.append_frames(
             k, v, self.kpool, self.vpool, self.bank_slots(indices),
             frame_tokens=self.geom.frame_tokens, kscale=self.kscale, vscale=self.vscale,
+            kr_pool=self.krpool, rope_hw=rope.hw if rope is not None else None,
+            grid_hw=rope.cfg.grid_hw if rope is not None else None, kr_scale=self.krscale,
         )
 
     def logical_kv(self) -> tuple[torch.Tensor, torch.Tensor]:

@@ -663,3 +663,65 @@ def test_fp8_prope_copies_effective_pins():
     vx = pr.apply_tiled(ve, p_inv)
     vcopy = pr.apply_tiled(v.double(), p_inv).to(torch.bfloat16)
     assert float((vx - ref.fp8_fake_quant_frames(vcopy.float(), T).double()).abs().max()) < 1e-9
+
+
+def _rope_brute(x, grid_hw, t_pos):
+    """Independent RoPE of one frame x [T, H, D] (float64): pair i of token (h, w) turns by
+    t_pos * theta^(-2i/44) (pairs 0..21), h * theta^(-2(i-22)/42) (22..42) or
+    w * theta^(-2(i-43)/42) (43..63), theta = 10000, the model's table definition."""
+    gh, gw = grid_hw
+    out = x.clone()
+    for tok in range(gh * gw):
+        h, w = divmod(tok, gw)
+        for i in range(64):
+            if i < 22:
+                ang = t_pos * 10000.0 ** (-2 * i / 44)
+            elif i < 43:
+                ang = h * 10000.0 ** (-2 * (i - 22) / 42)
+            else:
+                ang = w * 10000.0 ** (-2 * (i - 43) / 42)
+            c, s = math.cos(ang), math.sin(ang)
+            a, b = x[tok, :, 2 * i], x[tok, :, 2 * i + 1]
+            out[tok, :, 2 * i], out[tok, :, 2 * i + 1] = a * c - b * s, a * s + b * c
+    return out
+
+
+def test_memory_frames_with_rope_pin():
+    """cached_self_attention with rope and memory frames: bank frame f is rotated at
+    memory_positions[f] and placed ahead of the window.  Checked against attention over keys
+    rotated one pair at a time from the textbook angles (no shared code with rope_frames)."""
+    T, grid, H = 4, (2, 2), 1
+    g = torch.Generator().manual_seed(81)
+    cache = ref.allocate_kv_cache(1, 1, 3 * T, H, 128, torch.float64)[0]
+    orope = {"freqs": ref.wan_rope_freqs(), "grid_hw": grid, "use_echorope": False,
+             "rope_train_frames": None}
+    ks, vs = [], []
+    for c in range(2):  # two committed frames, no sink: window positions 0, 1, then the chunk
+        q, k, v = (torch.randn(1, T, H, 128, generator=g, dtype=torch.float64) for _ in range(3))
+        _, upd = ref.cached_self_attention(q, k, v, cache, current_start=c * T, frame_seqlen=T,
+                                           sink_size=0, local_attn_size=3,
+                                           attn_fn=lambda *a: torch.zeros(0), rope=orope)
+        ref.apply_cache_updates([cache], [(0, upd)])
+        ks.append(k)
+        vs.append(v)
+    q, k, v = (torch.randn(1, T, H, 128, generator=g, dtype=torch.float64) for _ in range(3))
+    mk, mv = (torch.randn(1, 2 * T, H, 128, generator=g, dtype=torch.float64) for _ in range(2))
+    mpos = [7, 3]
+    x, _ = ref.cached_self_attention(q, k, v, cache, current_start=2 * T, frame_seqlen=T,
+                                     sink_size=0, local_attn_size=3, rope=orope, memory_k=mk,
+                                     memory_v=mv, memory_positions=mpos,
+                                     attn_fn=lambda a, b, c: ref.attention(
+                                         a, b, c, round_inputs_to_bf16=False))
+    # window: the two committed frames and the chunk at 0, 1, 2; the query at 2
+    keys = [_rope_brute(mk[0, f * T:(f + 1) * T], grid, mpos[f]) for f in range(2)]
+    keys += [_rope_brute(kk[0], grid, p) for kk, p in zip(ks + [k], (0, 1, 2))]
+    vals = torch.cat([mv[0]] + [vv[0] for vv in vs + [v]], dim=0)
+    qr = _rope_brute(q[0], grid, 2)
+    kk = torch.cat(keys, dim=0)
+    logits = torch.einsum("thd,khd->htk", qr, kk) / math.sqrt(128)
+    want = torch.einsum("htk,khd->thd", torch.softmax(logits, dim=-1), vals)
+    assert float((x[0] - want).abs().max()) < 1e-10
+    with pytest.raises(ValueError, match="one position per bank frame"):
+        ref.cached_self_attention(q, k, v, cache, current_start=2 * T, frame_seqlen=T,
+                                  sink_size=0, local_attn_size=3, rope=orope, memory_k=mk,
+                                  memory_v=mv, memory_positions=[1])
