@@ -905,8 +905,8 @@ def single_frame_leg(device, iters=20):
 def segments_leg(device, iters=5):
     """Segmented attention at the config-2 head shape (H12, 1560 tok/frame):
     * teacher forcing over [clean | noisy] x 6 frames (2 chunks of 3, sink 1 chunk, 1 prior clean
-      chunk; causal_model.py:337-471): ours (one launch per query chunk over its frame list)
-      vs the reference's op, FlexAttention with a block mask of the same rule
+      chunk; causal_model.py:337-471): ours (one segmented launch: every query chunk over its
+      own frame list; one launch per chunk timed beside it) vs the reference's op, FlexAttention with a block mask of the same rule
       (causal_model.py:984-989; torch.compile'd, timed after compiling), and vs SDPA with the
       dense boolean mask (its fallback);
     * H3 rollout window (sgf_attention.py:236-258): a 5-frame chunk over a 1000-token prefix,
@@ -916,7 +916,7 @@ def segments_leg(device, iters=5):
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    from solarwm_amd.segments import (ChunkListKVCache, teacher_forcing_attention,
+    from solarwm_amd.segments import (ChunkListKVCache, attend_segments, teacher_forcing_attention,
                                       teacher_forcing_frame_lists, windowed_attention)
 
     T, H = 1560, 12
@@ -945,6 +945,25 @@ def segments_leg(device, iters=5):
                                                                "max_prior_clean_chunks", "sink_size")})
     tf_flops = sum(4.0 * nb * T * len(fr) * T * H * 128 for _, fr in lists)
     ours_tf = timed(lambda: teacher_forcing_attention(q, k, v, **kw))
+    # the same attention as one launch per query chunk (the segments' frame lists over the same
+    # staged pools)
+    from solarwm_amd import kernels
+
+    kp, vp = kernels.staging_pools(2 * F, 1, H, T, torch.bfloat16, device)
+    kernels.append_frames(k, v, kp, vp, list(range(2 * F)), frame_tokens=T)
+    o_per = torch.empty_like(q)
+
+    def per_chunk():
+        for f0, frames in lists:
+            s = slice(f0 * T, (f0 + nb) * T)
+            kernels.attention_frames(q[:, s], kp, vp, frames, frame_tokens=T, out=o_per[:, s])
+
+    per_tf = timed(per_chunk)
+    o_one = torch.empty_like(q)
+    segs = [(nb * T, frames, None) for _, frames in lists]
+    one_tf = timed(lambda: attend_segments(q, kp, vp, segs, frame_tokens=T, out=o_one))
+    torch.cuda.synchronize()
+    tf_launch_diff = float((o_one.float() - o_per.float()).abs().max())
     # the dense mask of the same rule, built on the host from the frame lists
     mask = torch.zeros(L, L, dtype=torch.bool)
     for f0, frames in lists:
@@ -972,7 +991,7 @@ def segments_leg(device, iters=5):
     except Exception as e:  # the baseline only: report why it is missing
         flex_note = f"FlexAttention unavailable: {type(e).__name__}: {str(e)[:160]}"
     ref_tf = flex_tf if flex_tf is not None else sdpa_tf
-    del mask, qt, kt, vt, q, k, v
+    del mask, qt, kt, vt, q, k, v, o_per, o_one
 
     cf, P = 5, 1000
     cache = ChunkListKVCache(num_layers=1, batch=1, heads=H, frame_tokens=T, chunk_frames=cf,
@@ -1004,6 +1023,9 @@ def segments_leg(device, iters=5):
         "teacher_forcing_reference": "flex_attention + block mask" if flex_tf is not None else "SDPA + dense mask",
         "teacher_forcing_speedup": round(ref_tf / ours_tf, 2),
         "teacher_forcing_sdpa_dense_mask_ms": round(sdpa_tf, 3),
+        "teacher_forcing_attention_ms": round(one_tf, 3),
+        "teacher_forcing_per_chunk_launches_ms": round(per_tf, 3),
+        "teacher_forcing_launch_max_abs_diff": tf_launch_diff,
         "h3_window_ms": round(ours_w, 3),
         "h3_window_tflops": round(w_flops / (ours_w / 1e3) / 1e12, 1),
         "h3_window_reference_ms": round(ref_w, 3),

@@ -64,6 +64,7 @@ enum skv_status {
 
 #define SKV_MAX_APPEND_FRAMES 64
 #define SKV_MAX_FRAMES 256
+#define SKV_MAX_SEGMENTS 64
 
 /* Library version as an integer (major * 10000 + minor * 100 + patch). */
 int skv_version(void);
@@ -270,6 +271,12 @@ int skv_append_workspace_size(const skv_append_desc* desc, int64_t* bytes);
  * rope_t selects RoPE on load, q_xform_t (with q_xform_s, out_xform) RoPE + PRoPE.
  * frame_lens (mask NONE only) lets frames hold fewer than frame_tokens keys, so a window can
  * mix whole frames with spans of other lengths (the H3 prefix rows, memory_kv_attention.py).
+ * Segments (n_segments > 0, up to SKV_MAX_SEGMENTS; bf16 pools, bf16 or f32 queries, mask NONE,
+ * no RoPE / PRoPE): the queries are n_segments consecutive row ranges of seg_rows[s] rows
+ * (summing to q_len), and segment s attends only its own seg_frames[s] consecutive entries of
+ * frame_slots / frame_lens (the lists of all segments end to end, summing to n_frames), in one
+ * launch: the teacher-forcing block mask (causal_model.py:337-471) and the H3 segment layouts
+ * (sgf_attention.py:236-258, memory_kv_attention.py:39-140) are such lists.
  */
 typedef struct skv_attention_desc {
   const void* q;
@@ -302,6 +309,9 @@ typedef struct skv_attention_desc {
                                 keys past it are masked), for spans that are not whole frames */
   void* workspace;            /* device, optional, 16-byte aligned: enables the balanced key split */
   int64_t workspace_bytes;    /* its size; must cover skv_attention_plan's workspace_bytes */
+  const int32_t* seg_rows;    /* host, n_segments entries: query rows of each segment */
+  const int32_t* seg_frames;  /* host, n_segments entries: frame-list entries of each segment */
+  int n_segments;             /* 0: one segment (every query over the whole frame list) */
 } skv_attention_desc;
 
 int skv_attention_ex(const skv_attention_desc* desc, skv_stream_t stream);

@@ -28,6 +28,7 @@ SKV_E_LAUNCH = -3
 
 SKV_MAX_APPEND_FRAMES = 64
 SKV_MAX_FRAMES = 256
+SKV_MAX_SEGMENTS = 64
 SKV_NOALLOC_SCRATCH_BYTES = 68157440
 
 # Every symbol include/solarkv.h declares, with (restype, argtypes).
@@ -67,6 +68,7 @@ class AttentionDesc(ctypes.Structure):
         ("rope_hw", _vp), ("grid_h", _i32), ("grid_w", _i32), ("rope_t", _vp), ("n_qframes", _i32),
         ("q_xform_t", _vp), ("q_xform_s", _vp), ("out_xform", _vp), ("frame_lens", _i32p),
         ("workspace", _vp), ("workspace_bytes", _i64),
+        ("seg_rows", _i32p), ("seg_frames", _i32p), ("n_segments", _i32),
     ]
 
 

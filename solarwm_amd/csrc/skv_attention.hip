@@ -106,6 +106,12 @@ struct AttnArgs {
   int qt_base;
   float* part_o;   // [2*n_wg][256][128] unnormalised O
   float* part_ml;  // [2*n_wg][256][2] (running max in log2 units, row sum)
+  // Segments (the SEG instances; n_seg = 0 otherwise): the queries are n_seg consecutive row
+  // ranges of seg_rows[s] rows, each attending its own seg_nf[s] consecutive entries of the
+  // frame list; a segment's q-tiles start at its first row, n_qtiles counts them all.
+  int n_seg;
+  int32_t seg_rows[SKV_MAX_SEGMENTS];
+  int32_t seg_nf[SKV_MAX_SEGMENTS];
 };
 
 // Wan's split of a head's 64 complex channel pairs (2i, 2i+1): 22 temporal, 21 height, 21 width
@@ -167,19 +173,38 @@ __device__ inline float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The frame list a walk reads: entries [fb, fb + nf) of the launch's list.  A plain launch walks
+// the whole list (no state: fb is 0 and nf the launch's frame count); a segmented launch walks its
+// segment's sub-list, set when the work-group has found its segment.
+template <bool SEG>
+struct FrameRange {
+  __device__ int fb() const { return 0; }
+  __device__ int nf(const AttnArgs& a) const { return a.n_frames; }
+  __device__ void range(int, int) {}
+};
+
+template <>
+struct FrameRange<true> {
+  int b = 0, n = 0;
+  __device__ int fb() const { return b; }
+  __device__ int nf(const AttnArgs&) const { return n; }
+  __device__ void range(int first, int count) { b = first; n = count; }
+};
+
 // Walks key tiles in frame-list order.  The frame's pool offset and valid length are read when
 // the walk enters the frame, so advancing by one tile costs a few scalar adds: no division by
 // the tiles per frame and no table load on the tiles in between.  Every member is wave-uniform.
-struct TileWalk {
-  int j = 0, t = 0;   // frame index in the list, tile inside the frame
-  int32_t slot = 0;   // slots[j]
+template <bool SEG = false>
+struct TileWalk : FrameRange<SEG> {
+  int j = 0, t = 0;   // frame index in the walked list, tile inside the frame
+  int32_t slot = 0;   // the frame's slot
   int64_t base = 0;   // element offset of frame j's (b, h) block: slot * slot_stride + kbh
   int flen = 0;       // valid keys of frame j
   __device__ void open(const AttnArgs& a, int64_t kbh) {
-    if (j < a.n_frames) {
-      slot = a.slots[j];
+    if (j < this->nf(a)) {
+      slot = a.slots[this->fb() + j];
       base = (int64_t)slot * a.slot_stride + kbh;
-      flen = a.flen[j];
+      flen = a.flen[this->fb() + j];
     }
   }
   __device__ void start(const AttnArgs& a, int64_t kbh, int tg) {
@@ -203,13 +228,15 @@ struct TileWalk {
 // enters frame j; advancing by one tile costs a few scalar ops.  Past the last frame, off_n
 // repeats off (the keys there are masked and their rows are only read, in bounds, so that the
 // staged values stay finite).  Every member is wave-uniform.
-struct PackedWalk {
+template <bool SEG = false>
+struct PackedWalk : FrameRange<SEG> {
   int j = 0, t0 = 0;
   uint32_t off = 0, off_n = 0;  // byte offsets of frames j and j + 1's (b, h) blocks
   __device__ void open(const AttnArgs& a, int64_t kbh) {
-    if (j < a.n_frames) {
-      off = (uint32_t)(((int64_t)a.slots[j] * a.slot_stride + kbh) * 2);
-      off_n = j + 1 < a.n_frames ? (uint32_t)(((int64_t)a.slots[j + 1] * a.slot_stride + kbh) * 2) : off;
+    const int nf = this->nf(a), fb = this->fb();
+    if (j < nf) {
+      off = (uint32_t)(((int64_t)a.slots[fb + j] * a.slot_stride + kbh) * 2);
+      off_n = j + 1 < nf ? (uint32_t)(((int64_t)a.slots[fb + j + 1] * a.slot_stride + kbh) * 2) : off;
     }
   }
   __device__ void start(const AttnArgs& a, int64_t kbh, int g) {
@@ -514,10 +541,14 @@ constexpr size_t attn_lds_bytes(int nw, int rm, int kt_bytes, bool split, bool p
 
 // PK: key tiles packed across frame boundaries (PackedWalk; whole frames of T = 8k tokens, 2-byte
 // pools, no RoPE): a window of n frames takes ceil(n T / 64) tiles instead of n ceil(T / 64).
-template <int NW, typename QT, typename KT, int RM, bool SPLIT = false, bool PK = false>
+// SEG: the grid's q-tiles belong to consecutive query segments, each over its own slice of the
+// frame list (AttnArgs::n_seg); no RoPE, no mask, no split.
+template <int NW, typename QT, typename KT, int RM, bool SPLIT = false, bool PK = false,
+          bool SEG = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   static_assert(!PK || (RM == 0 && sizeof(KT) == 2), "packed tiles: 2-byte pools, no RoPE");
+  static_assert(!SEG || (RM == 0 && !SPLIT), "segments: no RoPE, no split");
   constexpr int kBQ = NW * 32;
   // LDS map: kRing K buffers, then kRing V^T buffers (tile x in buffer x mod kRing), then (PRoPE)
   // kWN matrix buffers.  A step reads K(tau+1) and V(tau-1) and loads K(tau+kL+1) and V(tau+kL-1);
@@ -568,6 +599,23 @@ void attn_kernel(AttnArgs a) {
   const int qt = (qg + a.qt_base) % a.n_qtiles;
   const int bh = (qg + a.qt_base) / a.n_qtiles;
   const int h = bh % a.H, b = bh / a.H;
+  // the q-tile's query rows [qr0 + qtl * kBQ, ...) < qend and its frame list [fb, fb + nfr)
+  int qr0 = 0, qend = a.Lq, qtl = qt, fb = 0, nfr = a.n_frames;
+  if constexpr (SEG) {
+    // q-tiles are dealt last segment first: later segments attend longer lists in the callers'
+    // layouts (teacher forcing, memory KV), so the longest work-groups start first
+    qtl = a.n_qtiles - 1 - qt;
+    qend = 0;
+    for (int sg = 0; sg < a.n_seg; ++sg) {  // wave-uniform scan of the segment table
+      const int rows = a.seg_rows[sg], nq = (rows + kBQ - 1) / kBQ;
+      qr0 = qend;
+      qend += rows;
+      nfr = a.seg_nf[sg];
+      if (qtl < nq) break;
+      qtl -= nq;
+      fb += nfr;
+    }
+  }
 
   // SPLIT: an opaque copy per segment, so lane-derived values are recomputed here instead of
   // hoisted out of the segment loop, where they would stay live through the tile loop
@@ -575,9 +623,9 @@ void attn_kernel(AttnArgs a) {
   if constexpr (SPLIT) asm volatile("" : "+v"(tid));
   const int lane = tid & 63, w = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
-  const int q0 = qt * kBQ;
+  const int q0 = qr0 + qtl * kBQ;
   const int qrow = q0 + w * 32 + n;
-  const bool qlive = qrow < a.Lq;
+  const bool qlive = qrow < qend;
 
   // Q^T operand: lane (n, hh) holds q[qrow][k*16 + hh*8 .. +7] for k = 0..7.
   etx8 qf[8];
@@ -713,7 +761,7 @@ void attn_kernel(AttnArgs a) {
   };
 
   // Visibility limits (keys indexed 0..n_keys-1 in frame-list order; n_keys < 2^31).
-  const int n_keys = (int)a.n_keys;
+  const int n_keys = SEG ? nfr * a.T : (int)a.n_keys;
   int lim_lane = n_keys, lim_lo = n_keys, lim_hi = n_keys;
   if (a.mask_mode == SKV_MASK_CHUNK_CAUSAL) {
     const int qlast = min(q0 + kBQ, a.Lq) - 1;
@@ -724,8 +772,7 @@ void attn_kernel(AttnArgs a) {
   int ntau;
   {
     const int jf = lim_hi / a.T;
-    ntau = jf >= a.n_frames ? a.n_frames * a.ntiles_f
-                            : jf * a.ntiles_f + (lim_hi - jf * a.T + kTile - 1) / kTile;
+    ntau = jf >= nfr ? nfr * a.ntiles_f : jf * a.ntiles_f + (lim_hi - jf * a.T + kTile - 1) / kTile;
     if constexpr (PK) ntau = (lim_hi + kTile - 1) / kTile;  // lim_hi <= n_keys
     if constexpr (SPLIT) ntau = te - tb;  // no mask: the segment's tiles
   }
@@ -737,29 +784,29 @@ void attn_kernel(AttnArgs a) {
   loader.init(w, lane, a.Tp);
   auto tile_base = [&](int tau) -> int64_t {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
-    return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
+    return (int64_t)a.slots[fb + j] * a.slot_stride + kbh + (int64_t)t * kTile * kHeadDim;
   };
   [[maybe_unused]] auto tile_vbase = [&](int tau) -> int64_t {  // the same tile of V^T
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
-    return (int64_t)a.slots[j] * a.slot_stride + kbh + (int64_t)t * kTile;
+    return (int64_t)a.slots[fb + j] * a.slot_stride + kbh + (int64_t)t * kTile;
   };
   // fp8 pools: scales are [n_slots][B][H]; (b, h) of this workgroup is bh
   constexpr bool kFp8Pool = sizeof(KT) == 1;
   const int64_t n_bh = (int64_t)a.B * a.H;
   [[maybe_unused]] auto tile_scale = [&](const float* sc, int tau) -> float {
     const int j = (tb + tau) / a.ntiles_f;
-    return sc[(int64_t)a.slots[j] * n_bh + bh];
+    return sc[(int64_t)a.slots[fb + j] * n_bh + bh];
   };
   // mask decision for tile tau (uniform): returns true if any key of the tile may be hidden
   auto tile_needs_mask = [&](int tau, int& tok0, int& key0, int& tj) -> bool {
     const int tg = tb + tau, j = tg / a.ntiles_f, t = tg - j * a.ntiles_f;
     tok0 = t * kTile;
     key0 = j * a.T + tok0;
-    tj = a.flen[j];
+    tj = a.flen[fb + j];
     return (tok0 + kTile > tj) || (key0 + kTile > lim_lo);
   };
   // the same decision for the tile a walk stands on
-  auto walk_needs_mask = [&](const TileWalk& wk, int& tok0, int& key0) -> bool {
+  auto walk_needs_mask = [&](const TileWalk<SEG>& wk, int& tok0, int& key0) -> bool {
     tok0 = wk.t * kTile;
     key0 = wk.j * a.T + tok0;
     return (tok0 + kTile > wk.flen) || (key0 + kTile > lim_lo);
@@ -794,7 +841,8 @@ void attn_kernel(AttnArgs a) {
   f32x16 (&s_cur)[2] = sA;
   if (ntau > 0) {
     if constexpr (PK) {
-      PackedWalk p;
+      PackedWalk<SEG> p;
+      p.range(fb, nfr);
       p.start(a, kbh, tb);
 #pragma unroll
       for (int x = 0; x <= kL; ++x) {
@@ -866,8 +914,13 @@ void attn_kernel(AttnArgs a) {
   for (int i = 0; i < 16; ++i) zero16[i] = 0.f;
   // Tiles addressed in step tau: K(tau+2) (kw), V(tau) (vw) and the mask / RoPE frame of
   // QK(tau+1) (mw); the walks advance one tile per step.
-  TileWalk kw, vw, mw;
-  [[maybe_unused]] PackedWalk kp, vp;
+  TileWalk<SEG> kw, vw, mw;
+  [[maybe_unused]] PackedWalk<SEG> kp, vp;
+  kw.range(fb, nfr);
+  vw.range(fb, nfr);
+  mw.range(fb, nfr);
+  kp.range(fb, nfr);
+  vp.range(fb, nfr);
   if constexpr (PK) {
     kp.start(a, kbh, tb + kL + 1);
     vp.start(a, kbh, tb + kL - 1);
@@ -1454,14 +1507,14 @@ void attn_fp8_kernel(AttnArgs a) {
   i32x8 pA = {0, 0, 0, 0, 0, 0, 0, 0}, pB;
   // Prologue: K(0), K(1), K(2) and V(0) resident, V(-1)'s buffer zeroed so PV(-1) of step 0 adds
   // nothing; then QK(0).
-  TileWalk w0;  // tile 0 of the segment: V(0) and the scales of its frame
+  TileWalk<> w0;  // tile 0 of the segment: V(0) and the scales of its frame
   w0.start(a, kbh, tb);
   if (ntau > 0) {
 #pragma unroll
     for (int x = 0; x <= kL; ++x)
       if (x < ntau) if (kload) stage(ktile(x), kb_lds(x));
     if (!kload) {
-      TileWalk wv = w0;
+      TileWalk<> wv = w0;
 #pragma unroll
       for (int x = 0; x < kL - 1; ++x) {
         if (x < ntau) stage(vpool + wv.base + wv.t * kTile, vb_lds(x));
@@ -1480,7 +1533,7 @@ void attn_fp8_kernel(AttnArgs a) {
   }
   // Tiles addressed in step tau: K(tau+3) (kw), V(tau+1) (vw), the mask and the scales of
   // tile tau+1 (mw); the walks advance one tile per step.
-  TileWalk kw, vw, mw;
+  TileWalk<> kw, vw, mw;
   kw.start(a, kbh, tb + kL + 1);
   vw.start(a, kbh, tb + kL - 1);
   mw.start(a, kbh, tb + 1);
@@ -1892,7 +1945,9 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
                           const float* q_inv_rms = nullptr, int64_t q_rms_sb = 0,
                           const float* q_norm_weight = nullptr,
                           const int32_t* frame_lens = nullptr, void* workspace = nullptr,
-                          int64_t workspace_bytes = 0, skv_launch_plan* plan = nullptr) {
+                          int64_t workspace_bytes = 0, skv_launch_plan* plan = nullptr,
+                          const int32_t* seg_rows = nullptr, const int32_t* seg_frames = nullptr,
+                          int n_segments = 0) {
   if (!q || !k_pool || !v_pool || !frame_slots || !out) {
     set_error("skv_attention: null pointer argument");
     return SKV_E_ARG;
@@ -1995,6 +2050,38 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
               (long long)workspace_bytes);
     return SKV_E_ARG;
   }
+  // segments: consecutive query ranges, each over its own consecutive run of the frame list
+  int64_t seg_qtiles = 0;
+  int seg_max_frames = 0;
+  if (n_segments != 0) {
+    if (n_segments < 0 || n_segments > SKV_MAX_SEGMENTS || !seg_rows || !seg_frames) {
+      set_error("skv_attention_ex: n_segments=%d needs seg_rows and seg_frames and at most %d "
+                "segments", n_segments, SKV_MAX_SEGMENTS);
+      return SKV_E_ARG;
+    }
+    if (pool_dtype != SKV_BF16 || q_dtype == SKV_F16 || rope || mask_mode != SKV_MASK_NONE) {
+      set_error("skv_attention_ex: segments need bf16 pools, bf16 or f32 queries, mask NONE and "
+                "no RoPE / PRoPE");
+      return SKV_E_UNSUPPORTED;
+    }
+    int64_t rows = 0, frames = 0;
+    for (int sgi = 0; sgi < n_segments; ++sgi) {
+      if (seg_rows[sgi] < 1 || seg_frames[sgi] < 1) {
+        set_error("skv_attention_ex: segment %d has %d rows and %d frames (both must be >= 1)",
+                  sgi, seg_rows[sgi], seg_frames[sgi]);
+        return SKV_E_ARG;
+      }
+      rows += seg_rows[sgi];
+      frames += seg_frames[sgi];
+      seg_qtiles += (seg_rows[sgi] + 255) / 256;
+      seg_max_frames = seg_frames[sgi] > seg_max_frames ? seg_frames[sgi] : seg_max_frames;
+    }
+    if (rows != q_len || frames != n_frames) {
+      set_error("skv_attention_ex: segments cover %lld rows and %lld frames, expected q_len=%d and "
+                "n_frames=%d", (long long)rows, (long long)frames, q_len, n_frames);
+      return SKV_E_ARG;
+    }
+  }
   if (q_len == 0) {
     if (plan) *plan = skv_launch_plan{0, 0, 0, 0, 0, 0};
     return SKV_OK;
@@ -2060,6 +2147,18 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   };
   int nw = fill(256, 1) * 1.04 >= fill(128, 2) ? 8 : 4;
   a.n_qtiles = (q_len + nw * 32 - 1) / (nw * 32);
+  a.n_seg = n_segments;
+  if (n_segments > 0) {  // 8-wave groups; each segment's q-tiles start at its first row
+    nw = 8;
+    a.n_qtiles = (int)seg_qtiles;
+    for (int sgi = 0; sgi < n_segments; ++sgi) {
+      a.seg_rows[sgi] = seg_rows[sgi];
+      a.seg_nf[sgi] = seg_frames[sgi];
+    }
+    // key tiles of the longest segment's list (reported by the plan)
+    a.nt = a.packed ? (int)(((int64_t)seg_max_frames * frame_tokens + kTile - 1) / kTile)
+                    : seg_max_frames * a.ntiles_f;
+  }
   a.n_wg = a.n_qtiles * heads * batch;
   // Balanced key split: when the grid leaves many CUs idle (few q-tiles, e.g. one frame of
   // queries), one 8-wave workgroup per CU takes an equal share of all (q-tile, key tile) units;
@@ -2080,7 +2179,8 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   const int nt = a.nt;
   const int64_t qt8 = (int64_t)((q_len + kSplitBQ - 1) / kSplitBQ) * heads * batch;
   const int64_t units8 = qt8 * nt;
-  if (mask_mode == SKV_MASK_NONE && nt >= 8 && units8 >= 4 * n_cu && n_cu <= kMaxSplitWg) {
+  if (mask_mode == SKV_MASK_NONE && n_segments == 0 && nt >= 8 && units8 >= 4 * n_cu &&
+      n_cu <= kMaxSplitWg) {
     auto t_tile = [&](int64_t busy) { return 1.0 + 0.62 * (double)busy / n_cu; };
     auto t_grid = [&](int64_t wg, int per_cu, double per_tile) {  // rounds of nt tiles
       const int64_t slots = (int64_t)n_cu * per_cu, full = wg / slots, last = wg - full * slots;
@@ -2189,6 +2289,16 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
     t.qt_base = (int)full_wg;
     launch<8>(t, q_dtype, pool_dtype, rm, s);
     combine(t, n_tail);
+  } else if (a.n_seg > 0) {
+    dim3 grid(a.n_wg), block(512);
+    const size_t lds = attn_lds_bytes(8, 0, 2, false, a.packed);
+    if (a.packed) {
+      if (q_dtype == SKV_BF16) hipLaunchKernelGGL((attn_kernel<8, bf16, bf16, 0, false, true, true>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((attn_kernel<8, float, bf16, 0, false, true, true>), grid, block, lds, s, a);
+    } else {
+      if (q_dtype == SKV_BF16) hipLaunchKernelGGL((attn_kernel<8, bf16, bf16, 0, false, false, true>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((attn_kernel<8, float, bf16, 0, false, false, true>), grid, block, lds, s, a);
+    }
   } else {
     if (nw == 8)
       launch<8>(a, q_dtype, pool_dtype, rm, s);
@@ -2281,7 +2391,8 @@ static int attention_desc(const skv_attention_desc* d, skv_stream_t stream,
                         d->out_sb, d->out_st, d->out_sh, d->rope_hw, d->grid_h, d->grid_w,
                         d->rope_t, d->n_qframes, d->q_xform_t, d->q_xform_s, d->out_xform, stream,
                         d->q_inv_rms, d->q_rms_stride_b, d->q_norm_weight, d->frame_lens,
-                        d->workspace, d->workspace_bytes, plan);
+                        d->workspace, d->workspace_bytes, plan, d->seg_rows, d->seg_frames,
+                        d->n_segments);
 }
 
 extern "C" int skv_attention_ex(const skv_attention_desc* d, skv_stream_t stream) {

@@ -458,6 +458,7 @@ def attention_desc(
     prope: tuple[torch.Tensor, tuple[int, int], torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     q_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
     frame_lens: Sequence[int] | None = None,
+    segments: Sequence[tuple[int, int]] | None = None,
 ) -> tuple[_lib.AttentionDesc, torch.Tensor, tuple]:
     """Validate an attention launch and return ``(descriptor, out, keep-alive objects)`` for
     ``skv_attention_ex`` (no workspace set).  Arguments as :func:`attention_frames`."""
@@ -500,9 +501,26 @@ def attention_desc(
         flens = _lib.int32_array(frame_lens)
         d.frame_lens = flens
         keep.append(flens)
+    if segments is not None:
+        if not 1 <= len(segments) <= _lib.SKV_MAX_SEGMENTS:
+            raise ValueError(f"1..{_lib.SKV_MAX_SEGMENTS} segments per launch, got {len(segments)}")
+        rows = [int(r) for r, _ in segments]
+        nfs = [int(f) for _, f in segments]
+        if min(rows) < 1 or min(nfs) < 1:
+            raise ValueError("every segment needs at least one query row and one frame")
+        if sum(rows) != q.shape[1] or sum(nfs) != len(frame_slots):
+            raise ValueError(f"segments cover {sum(rows)} rows and {sum(nfs)} frames; q has "
+                             f"{q.shape[1]} rows and the list {len(frame_slots)} frames")
+        if kpool.dtype != torch.bfloat16 or q.dtype == torch.float16 or mask_mode != _lib.SKV_MASK_NONE:
+            raise ValueError("segments need bfloat16 pools, bfloat16 or float32 queries and no mask")
+        sr, sf = _lib.int32_array(rows), _lib.int32_array(nfs)
+        d.seg_rows, d.seg_frames, d.n_segments = sr, sf, len(segments)
+        keep += [sr, sf]
     nq = q.shape[1] // frame_tokens
     if rope is not None and prope is not None:
         raise ValueError("give rope= or prope=, not both")
+    if (rope is not None or prope is not None) and segments is not None:
+        raise ValueError("segments take no rope= / prope=")
     if rope is not None or prope is not None:
         rhw, ghw = (rope or prope)[0], (rope or prope)[1]
         _check_rope_hw(kpool, kpool, rhw, ghw, frame_tokens)
@@ -568,6 +586,7 @@ def attention_frames(
     prope: tuple[torch.Tensor, tuple[int, int], torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
     q_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
     frame_lens: Sequence[int] | None = None,
+    segments: Sequence[tuple[int, int]] | None = None,
     use_workspace: bool = True,
 ) -> torch.Tensor:
     """softmax(q kᵀ·scale) v over the keys of ``frame_slots`` (in order); returns [B, Lq, H, D].
@@ -587,6 +606,11 @@ def attention_frames(
     ``frame_lens``: valid keys of each listed frame (``1..frame_tokens``), for windows that mix
     whole frames with shorter spans; keys past a frame's length are masked (mask NONE only).
 
+    ``segments = [(rows, n_frames), ...]``: one launch for several query segments, each over its
+    own frame list: segment s is the next ``rows`` query rows and attends the next ``n_frames``
+    entries of ``frame_slots`` (and ``frame_lens``).  At most ``SKV_MAX_SEGMENTS``; bfloat16
+    pools, bfloat16 or float32 queries, no mask, no RoPE; segments never take the key split.
+
     Under-filled grids take the balanced key split with this stream's workspace
     (``use_workspace=False`` keeps them on the unsplit kernel)."""
     lib = _lib.load()
@@ -594,7 +618,7 @@ def attention_frames(
         q, kpool, vpool, frame_slots, frame_tokens=frame_tokens, softmax_scale=softmax_scale,
         kscale=kscale, vscale=vscale, mask_mode=mask_mode, q_pos0=q_pos0,
         chunk_tokens=chunk_tokens, out=out, rope=rope, prope=prope, q_norm=q_norm,
-        frame_lens=frame_lens)
+        frame_lens=frame_lens, segments=segments)
     if use_workspace:
         plan = _lib.LaunchPlan()
         _lib.check("skv_attention_plan", lib.skv_attention_plan(ctypes.byref(d), ctypes.byref(plan)))
@@ -604,8 +628,11 @@ def attention_frames(
     t0 = _tic("attention")
     _lib.check("skv_attention_ex", lib.skv_attention_ex(ctypes.byref(d), _stream(q.device)))
     # algorithmic FLOPs: QKᵀ and PV over every key (masking is not discounted)
-    _toc("attention", t0, 4.0 * d.batch * d.heads * q.shape[1] * len(frame_slots) * frame_tokens
-         * HEAD_DIM)
+    if segments is None:
+        pairs = q.shape[1] * len(frame_slots) * frame_tokens
+    else:
+        pairs = sum(r * f for r, f in segments) * frame_tokens
+    _toc("attention", t0, 4.0 * d.batch * d.heads * pairs * HEAD_DIM)
     del keep
     return out
 

@@ -11,9 +11,11 @@ Each of these reference paths attends query segments to unions of key spans:
   each with its own key spans.
 
 Here the key spans live in pool slots (frames of T tokens; spans that are not whole frames use
-partly filled slots with per-frame lengths) and each query segment is one launch of the
-attention kernel over its frame list, so no mask is materialised and masked-out blocks cost
-nothing.  The H3 rotary and camera transforms are applied by the caller (inputs are
+partly filled slots with per-frame lengths) and each query segment attends its own frame list,
+so no mask is materialised and masked-out blocks cost nothing.  Consecutive segments share one
+launch of the segmented kernel (up to ``SKV_MAX_SEGMENTS`` segments and ``SKV_MAX_FRAMES``
+listed frames per launch; bf16 pools): its grid holds every segment's q-tiles, so short
+segments no longer leave the chip idle between launches.  The H3 rotary and camera transforms are applied by the caller (inputs are
 post-transform Q/K/V), as the reference applies them before its attention call.
 """
 
@@ -23,9 +25,47 @@ from typing import Sequence
 
 import torch
 
-from . import kernels
+from . import _lib, kernels
 
 _GEOM_ERR = "num_frames must be a positive multiple of num_frame_per_block"
+
+
+def attend_segments(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
+                    segs: Sequence[tuple[int, Sequence[int], Sequence[int] | None]], *,
+                    frame_tokens: int, softmax_scale: float | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention of consecutive query segments, each over its own frame list: ``segs`` is
+    ``[(rows, frame list, frame lengths or None), ...]`` covering ``q``'s rows in order.  Runs of
+    consecutive segments go to one launch (``attention_frames(segments=...)``) while they fit the
+    launch limits; float32 pools take one launch per segment."""
+    if sum(r for r, _, _ in segs) != q.shape[1]:
+        raise ValueError(f"segments cover {sum(r for r, _, _ in segs)} rows, q has {q.shape[1]}")
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    T = frame_tokens
+    one_launch = kpool.dtype == torch.bfloat16 and q.dtype in (torch.bfloat16, torch.float32)
+    groups: list[list[tuple[int, Sequence[int], Sequence[int] | None]]] = []
+    n_frames = 0
+    for seg in segs:
+        if (not groups or not one_launch or len(groups[-1]) == _lib.SKV_MAX_SEGMENTS
+                or n_frames + len(seg[1]) > _lib.SKV_MAX_FRAMES):
+            groups.append([])
+            n_frames = 0
+        groups[-1].append(seg)
+        n_frames += len(seg[1])
+    r0 = 0
+    for grp in groups:
+        rows = sum(r for r, _, _ in grp)
+        frames = [f for _, fr, _ in grp for f in fr]
+        lens = None
+        if any(ln is not None for _, _, ln in grp):
+            lens = [x for _, fr, ln in grp for x in (ln if ln is not None else [T] * len(fr))]
+        s = slice(r0, r0 + rows)
+        kernels.attention_frames(q[:, s], kpool, vpool, frames, frame_tokens=T,
+                                 softmax_scale=softmax_scale, out=out[:, s], frame_lens=lens,
+                                 segments=[(r, len(fr)) for r, fr, _ in grp] if len(grp) > 1 else None)
+        r0 += rows
+    return out
 
 
 def teacher_forcing_frame_lists(*, num_frames: int, num_frame_per_block: int,
@@ -74,12 +114,9 @@ def teacher_forcing_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     kernels.append_frames(k.to(kv_dtype), v.to(kv_dtype), kp, vp, list(range(2 * num_frames)),
                           frame_tokens=T)
     qq = q if q.dtype in (torch.bfloat16, torch.float32) else q.to(kv_dtype)
-    out = torch.empty(qq.shape, dtype=qq.dtype, device=q.device)
-    rows = num_frame_per_block * T
-    for f0, frames in lists:
-        s = slice(f0 * T, f0 * T + rows)
-        kernels.attention_frames(qq[:, s], kp, vp, frames, frame_tokens=T,
-                                 softmax_scale=softmax_scale, out=out[:, s])
+    rows = num_frame_per_block * T  # the lists come in query order: chunk c starts at row c * rows
+    out = attend_segments(qq, kp, vp, [(rows, frames, None) for _, frames in lists],
+                          frame_tokens=T, softmax_scale=softmax_scale)
     return out.to(q.dtype)
 
 
@@ -217,18 +254,15 @@ def memory_kv_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache
     (ts, tl), (anc, al), (bk, bl), (au, aul) = cache.write_spans(layer, spans)
     hist, staging = cache.stage_chunk(layer, chunk_index, k[:, prefix:], v[:, prefix:])
     kp, vp = cache.pools[layer]
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     full = [T] * len(hist)
-    segs = [((0, shared), ts + anc, tl + al)]
+    segs = [(shared, ts + anc, tl + al)]
     if n_bank:
-        segs.append(((shared, bank_end), ts + anc + bk + hist, tl + al + bl + full))
+        segs.append((bank_end - shared, ts + anc + bk + hist, tl + al + bl + full))
     if audio_rows:
-        segs.append(((bank_end, prefix), ts + anc + au, tl + al + aul))
-    segs.append(((prefix, prefix + chunk_rows), ts + anc + bk + au + hist + staging,
+        segs.append((audio_rows, ts + anc + au, tl + al + aul))
+    segs.append((chunk_rows, ts + anc + bk + au + hist + staging,
                  tl + al + bl + aul + full + [T] * len(staging)))
-    for (a, b), frames, lens in segs:
-        kernels.attention_frames(q[:, a:b], kp, vp, frames, frame_tokens=T,
-                                 softmax_scale=softmax_scale, out=out[:, a:b], frame_lens=lens)
+    out = attend_segments(q, kp, vp, segs, frame_tokens=T, softmax_scale=softmax_scale)
     if commit:
         cache.commit_staged(layer, chunk_index, staging)
     return out

@@ -358,6 +358,58 @@ def test_fp8_copy_workspace_and_arguments():
     assert b"vx_scale" in lib.skv_last_error()
 
 
+def test_segmented_launch_plans_and_arguments():
+    """One launch for several query segments: each segment's q-tiles start at its first row (8
+    waves, 256 rows), the grid holds every segment's q-tiles, the key split is never taken and
+    the reported key tiles are the longest segment's; bad tables are rejected before anything
+    launches."""
+    from solarwm_amd.segments import teacher_forcing_frame_lists
+
+    lib = _lib.load()
+    # the bench's teacher-forcing shape: [clean | noisy] x 6 frames of 1560 tokens, chunks of 3
+    lists = teacher_forcing_frame_lists(num_frames=6, num_frame_per_block=3,
+                                        max_prior_clean_chunks=1, sink_size=3)
+    assert [len(f) for _, f in lists] == [3, 6, 3, 6]
+    frames = [f for _, fr in lists for f in fr]
+    d, _keep = _attn_desc(1, 12, 4 * 4680, 1560, len(frames))
+    table = _slots(*frames)
+    rows, nfs = _slots(*[4680] * 4), _slots(*[len(f) for _, f in lists])
+    d.frame_slots, d.n_slots = table, 12
+    d.seg_rows, d.seg_frames, d.n_segments = rows, nfs, 4
+    d.workspace, d.workspace_bytes = 0x2000, SPLIT_BYTES
+    plan = _plan(d)
+    assert (plan.waves_per_group, plan.split, plan.n_workgroups) == (8, 0, 4 * 19 * 12)
+    assert plan.workspace_bytes == 0
+    assert plan.key_tiles == -(-6 * 1560 // 64)  # packed tiles of the 6-frame lists
+    # ragged segment rows: 300 rows take 2 q-tiles, 1 row takes 1
+    d2, _k2 = _attn_desc(2, 3, 301, 64, 3)
+    r2, f2 = _slots(300, 1), _slots(2, 1)
+    d2.seg_rows, d2.seg_frames, d2.n_segments = r2, f2, 2
+    plan = _plan(d2)
+    assert (plan.waves_per_group, plan.n_workgroups, plan.key_tiles) == (8, 3 * 3 * 2, 2)
+
+    def err(desc, code, text):
+        assert lib.skv_attention_plan(ctypes.byref(desc), ctypes.byref(_lib.LaunchPlan())) == code
+        assert text in lib.skv_last_error(), lib.skv_last_error()
+
+    d2.n_segments = _lib.SKV_MAX_SEGMENTS + 1
+    err(d2, _lib.SKV_E_ARG, b"n_segments")
+    d2.n_segments, d2.seg_frames = 2, None
+    err(d2, _lib.SKV_E_ARG, b"seg_frames")
+    bad = _slots(299, 1)
+    d2.seg_frames, d2.seg_rows = f2, bad
+    err(d2, _lib.SKV_E_ARG, b"q_len=301")
+    zero = _slots(301, 0)
+    d2.seg_rows, d2.seg_frames = r2, zero
+    err(d2, _lib.SKV_E_ARG, b"must be >= 1")
+    d2.seg_frames = f2
+    d2.mask_mode = _lib.SKV_MASK_CHUNK_CAUSAL
+    err(d2, _lib.SKV_E_UNSUPPORTED, b"mask NONE")
+    d3, _k3 = _attn_desc(1, 2, 301, 64, 3, pool=_lib.SKV_FP8_E4M3)
+    d3.seg_rows, d3.seg_frames, d3.n_segments = r2, f2, 2
+    err(d3, _lib.SKV_E_UNSUPPORTED, b"bf16 pools")
+
+
 def test_library_launches_nothing_cooperatively():
     """No entry point launches a kernel cooperatively: the one-pass fp8 append sizes its grid
     from the occupancy query and launches it plainly (its waits are bounded).  A cooperative
