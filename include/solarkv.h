@@ -341,6 +341,43 @@ typedef struct skv_launch_plan {
 int skv_attention_plan(const skv_attention_desc* desc, skv_launch_plan* plan);
 
 /*
+ * H3 transforms (MiniMax-H3 backend).  H3's attention segments take rotate-half MM-RoPE on head
+ * channels [0, 96) and its camera PRoPE on channels [96, 128) (eight 4-vectors per row, each
+ * multiplied by the row's 4x4 matrix) before attention, and the output matrix on the attention
+ * output's channels [96, 128) after it (sgf_attention.py:192-203, :580-659;
+ * torch_prope.py:187-241).
+ *
+ * skv_h3_rope_prope — one pass over a [batch][rows][heads][128] bf16 tensor (any strides with
+ * unit channel stride), replacing fused_prope.py:196-255 (rope_prope, the SGF rotary + camera
+ * projection) and, with cos = sin = NULL, fused_prope.py:30-93 (prope_project):
+ *   channels [0, 48) and [48, 96), x1 and x2, with c = bf16(cos[t]), s = bf16(sin[t]):
+ *     y1 = bf16(bf16(x1 c1) + bf16(-x2 s1)),  y2 = bf16(bf16(x2 c2) + bf16(x1 s2));
+ *   channels [96, 128), 4-vector v of row t: y_i = bf16(((M_i0 v_0 + M_i1 v_1) + M_i2 v_2)
+ *     + M_i3 v_3) in fp32 with M = matrix[b][t] rounded to bf16 (products of bf16 values are
+ *     exact in fp32, so this is the reference kernel's expression, bit for bit).
+ * cos / sin: [rows][96] (row stride table_stride elements), bf16 or f32, or both NULL to copy
+ * channels [0, 96).  matrix: [batch or 1][rows][4][4], bf16 or f32 (matrix_sb = 0 broadcasts
+ * one set over the batch), or NULL to copy channels [96, 128).  out may be x itself (every
+ * row is read before any of it is written) but must not otherwise overlap it.
+ */
+typedef struct skv_h3_xform_desc {
+  const void* x;
+  int64_t x_sb, x_st, x_sh;
+  void* out;
+  int64_t out_sb, out_st, out_sh;
+  int batch, rows, heads, head_dim;
+  const void* cos;
+  const void* sin;
+  int table_dtype;
+  int64_t table_stride;
+  const void* matrix;
+  int matrix_dtype;
+  int64_t matrix_sb, matrix_st;
+} skv_h3_xform_desc;
+
+int skv_h3_rope_prope(const skv_h3_xform_desc* desc, skv_stream_t stream);
+
+/*
  * skv_attention_ex_noalloc — skv_attention_ex that allocates nothing and takes no workspace:
  * the balanced key split keeps its partial results in a static device array of
  * SKV_NOALLOC_SCRATCH_BYTES per GPU (2 records x 256 rows x 130 floats for each of up to 256

@@ -72,6 +72,18 @@ class AttentionDesc(ctypes.Structure):
     ]
 
 
+class H3XformDesc(ctypes.Structure):
+    """``skv_h3_xform_desc`` (include/solarkv.h), field for field."""
+
+    _fields_ = [
+        ("x", _vp), ("x_sb", _i64), ("x_st", _i64), ("x_sh", _i64),
+        ("out", _vp), ("out_sb", _i64), ("out_st", _i64), ("out_sh", _i64),
+        ("batch", _i32), ("rows", _i32), ("heads", _i32), ("head_dim", _i32),
+        ("cos", _vp), ("sin", _vp), ("table_dtype", _i32), ("table_stride", _i64),
+        ("matrix", _vp), ("matrix_dtype", _i32), ("matrix_sb", _i64), ("matrix_st", _i64),
+    ]
+
+
 class LaunchPlan(ctypes.Structure):
     """``skv_launch_plan`` (include/solarkv.h): the launch skv_attention_ex would make."""
 
@@ -130,6 +142,7 @@ SIGNATURES: dict[str, tuple] = {
     "skv_attention_ex_noalloc": (_i32, [ctypes.POINTER(AttentionDesc), _vp]),
     "skv_noalloc_init": (_i32, []),
     "skv_append_workspace_size": (_i32, [ctypes.POINTER(AppendDesc), ctypes.POINTER(_i64)]),
+    "skv_h3_rope_prope": (_i32, [ctypes.POINTER(H3XformDesc), _vp]),
 }
 
 _lock = threading.Lock()

@@ -25,7 +25,7 @@ from typing import Sequence
 
 import torch
 
-from . import _lib, kernels
+from . import _lib, h3, kernels
 
 _GEOM_ERR = "num_frames must be a positive multiple of num_frame_per_block"
 
@@ -266,3 +266,117 @@ def memory_kv_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache
     if commit:
         cache.commit_staged(layer, chunk_index, staging)
     return out
+
+
+class H3WindowCache:
+    """H3's rollout with its own transforms: the raw chunk-list KV cache (H3RawKVCache,
+    sgf_attention.py:40-63) and the transformed attention window of the chunk being evaluated
+    (the KV window of _windowed_rollout_attention, sgf_attention.py:580-659).
+
+    H3 rotates and projects every key of a chunk's window with positions and cameras of that
+    window, so the cache keeps raw K/V (a ring of ``window`` chunks per layer) and builds the
+    window's transformed prefix and history frames once per chunk and layer, in pool slots;
+    each evaluation of the chunk (denoising steps, the commit pass) transforms only its own
+    rows.  The prefix and the tables of a chunk must stay the same over its evaluations, as in
+    the reference's KV window; ``invalidate`` forces a rebuild."""
+
+    def __init__(self, *, num_layers: int, batch: int, heads: int, frame_tokens: int,
+                 prefix_rows: int, chunk_frames: int = 5, window: int = 5, device="cuda"):
+        T = frame_tokens
+        self.T, self.cf, self.window, self.P = T, chunk_frames, window, int(prefix_rows)
+        self.C = chunk_frames * T
+        self.pf = -(-self.P // T)
+        bf = torch.bfloat16
+        shape = (num_layers, window, batch, self.C, heads, 128)
+        self.raw_k = torch.empty(shape, dtype=bf, device=device)
+        self.raw_v = torch.empty(shape, dtype=bf, device=device)
+        self.entries: list[list[tuple[int, int]]] = [[] for _ in range(num_layers)]
+        n_slots = self.pf + (window + 1) * chunk_frames
+        self.pools = [kernels.new_pools(n_slots, batch, heads, T, bf, device)[:2]
+                      for _ in range(num_layers)]
+        self.built: list[int | None] = [None] * num_layers
+        rows = max(self.pf * T, self.C)
+        self._tk = torch.empty((batch, rows, heads, 128), dtype=bf, device=device)
+        self._tv = torch.empty_like(self._tk)
+
+    def clear(self) -> None:
+        self.entries = [[] for _ in self.entries]
+        self.invalidate()
+
+    def invalidate(self) -> None:
+        self.built = [None] * len(self.built)
+
+    def history(self, layer: int, chunk_index: int) -> list[tuple[int, int]]:
+        entries = self.entries[layer]
+        expected = list(range(max(0, chunk_index - self.window), chunk_index))
+        if [e[0] for e in entries] != expected:
+            raise RuntimeError(f"H3 KV history differs at layer={layer}, chunk={chunk_index}")
+        return entries
+
+    def _to_slots(self, layer, k, v, cos, sin, matrix, slots) -> None:
+        """Transform raw rows k / v ([B, n, H, 128]) and append them to whole frame slots; rows
+        past n in the last slot are zeros (masked by the frame lengths)."""
+        n, rows = k.shape[1], len(slots) * self.T
+        tk, tv = self._tk[:, :rows], self._tv[:, :rows]
+        h3.rope_prope(k, cos, sin, matrix, out=tk[:, :n])
+        h3.rope_prope(v, None, None, matrix, out=tv[:, :n])
+        if n < rows:
+            tk[:, n:].zero_()
+            tv[:, n:].zero_()
+        kp, vp = self.pools[layer]
+        kernels.append_frames(tk, tv, kp, vp, list(slots), frame_tokens=self.T)
+
+    def attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer: int,
+               chunk_index: int, *, prefix: tuple[torch.Tensor, torch.Tensor],
+               q_rotary: tuple[torch.Tensor, torch.Tensor],
+               k_rotary: tuple[torch.Tensor, torch.Tensor], q_matrix: torch.Tensor,
+               kv_matrix: torch.Tensor, out_matrix: torch.Tensor, commit: bool = False,
+               softmax_scale: float | None = None) -> torch.Tensor:
+        """One evaluation of chunk ``chunk_index``: raw chunk rows q / k / v [B, C, H, 128]
+        bf16, the raw prefix K / V [B, prefix_rows, H, 128]; ``k_rotary`` (cos, sin) and
+        ``kv_matrix`` cover the window's key rows [prefix | history chunks | chunk],
+        ``q_rotary``, ``q_matrix`` and ``out_matrix`` the chunk's rows (the reference's kr, qr
+        and camera matrices).  Returns the projected attention output [B, C, H, 128]."""
+        T, P, C = self.T, self.P, self.C
+        if q.shape[1] != C or k.shape != q.shape or v.shape != q.shape:
+            raise ValueError(f"q/k/v must be one chunk of {C} rows")
+        pk, pv = prefix
+        if pk.shape[1] != P or pv.shape != pk.shape:
+            raise ValueError(f"the prefix must be {P} rows")
+        hist = self.history(layer, chunk_index)
+        nh = len(hist)
+        total = P + (nh + 1) * C
+        kc, ks = k_rotary
+        if kc.shape[0] != total or kv_matrix.shape[1] != total:
+            raise ValueError(f"k_rotary and kv_matrix need {total} rows (prefix, {nh} history "
+                             f"chunks, the chunk), got {kc.shape[0]} / {kv_matrix.shape[1]}")
+        cf = self.cf
+        pslots = list(range(self.pf))
+        hslots = [self.pf + i * cf + j for i in range(nh) for j in range(cf)]
+        cslots = [self.pf + nh * cf + j for j in range(cf)]
+        if self.built[layer] != chunk_index:
+            if P:
+                self._to_slots(layer, pk, pv, kc[:P], ks[:P], kv_matrix[:, :P], pslots)
+            for i, (_, ring) in enumerate(hist):
+                r0 = P + i * C
+                self._to_slots(layer, self.raw_k[layer, ring], self.raw_v[layer, ring],
+                               kc[r0:r0 + C], ks[r0:r0 + C], kv_matrix[:, r0:r0 + C],
+                               hslots[i * cf:(i + 1) * cf])
+            self.built[layer] = chunk_index
+        r0 = P + nh * C
+        self._to_slots(layer, k, v, kc[r0:], ks[r0:], kv_matrix[:, r0:], cslots)
+        qt = h3.rope_prope(q, q_rotary[0], q_rotary[1], q_matrix)
+        lens = [T] * (self.pf - 1) + [P - (self.pf - 1) * T] if P else []
+        lens += [T] * (len(hslots) + cf)
+        kp, vp = self.pools[layer]
+        out = kernels.attention_frames(qt, kp, vp, pslots + hslots + cslots, frame_tokens=T,
+                                       softmax_scale=softmax_scale, frame_lens=lens)
+        h3.rope_prope(out, None, None, out_matrix, out=out)
+        if commit:
+            kept = [*hist, (chunk_index, -1)][-self.window:]
+            used = {r for _, r in kept if r >= 0}
+            ring = min(r for r in range(self.window) if r not in used)
+            self.raw_k[layer, ring].copy_(k)
+            self.raw_v[layer, ring].copy_(v)
+            self.entries[layer] = [(c, r if r >= 0 else ring) for c, r in kept]
+        return out

@@ -145,7 +145,8 @@ def test_prope_argument_errors_do_not_launch():
 
 @pytest.mark.parametrize("cname,pyname", [("skv_append_desc", "AppendDesc"),
                                           ("skv_attention_desc", "AttentionDesc"),
-                                          ("skv_launch_plan", "LaunchPlan")])
+                                          ("skv_launch_plan", "LaunchPlan"),
+                                          ("skv_h3_xform_desc", "H3XformDesc")])
 def test_descriptor_layout_matches_header(tmp_path, cname, pyname):
     """The ctypes mirrors of the descriptor structs have the C compiler's size and offsets."""
     import shutil
