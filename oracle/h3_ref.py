@@ -28,8 +28,11 @@ Pinning (tests/test_oracle_h3.py):
   compose (rotating by a then b equals rotating by a + b), within bf16 rounding; the
   projection equals a float64 matrix product within one bf16 rounding and is bit-exact against
   an explicit per-element loop in the stated sum order.
-* ``windowed_rollout_attention`` — identity transforms (cos = 1, sin = 0, identity matrices)
-  reduce it to segments_ref.windowed_rollout_attention exactly.
+* ``windowed_rollout_attention`` / ``memory_kv_attention`` — identity transforms (cos = 1,
+  sin = 0, identity matrices) reduce them to segments_ref's windowed_rollout_attention /
+  memory_kv_attention exactly; the memory form's per-row transform equals transforming each
+  segment's gathered rows with the same rows of the tables (the reference's per-segment
+  ``calculate``), checked on a layout with every span.
 """
 
 from __future__ import annotations
@@ -129,4 +132,26 @@ def windowed_rollout_attention(q, k, v, prefix_k, prefix_v, cache: sr.H3RawKVCac
     o = sr.attention(qt, kt, vt).to(torch.bfloat16)
     if commit:
         cache.commit(layer, chunk_index, k, v)
+    return prope_project(o, out_matrix)
+
+
+def memory_kv_attention(q, k, v, history_k, history_v, *, text_rows: int, frame_rows: int,
+                        n_bank: int, audio_rows: int, rotary, history_rotary, q_matrix,
+                        kv_matrix, out_matrix, history_kv_matrix) -> torch.Tensor:
+    """MemoryKVAttention.attend with its transforms (memory_kv_attention.py:39-140): every
+    packed row [text | anchor | bank | audio | chunk] is rotated and projected with its own
+    rotary row and camera in every segment it enters, so the transforms apply per row here
+    (q with ``q_matrix``, k / v with ``kv_matrix``, raw history rows with ``history_rotary``
+    and ``history_kv_matrix``), then segments_ref's segmented attention, rounded to bf16, then
+    the output rows projected by ``out_matrix``."""
+    qt = rope_prope(q, rotary[0], rotary[1], q_matrix)
+    kt = rope_prope(k, rotary[0], rotary[1], kv_matrix)
+    vt = prope_project(v, kv_matrix)
+    if history_k.shape[1]:
+        hk = rope_prope(history_k, history_rotary[0], history_rotary[1], history_kv_matrix)
+        hv = prope_project(history_v, history_kv_matrix)
+    else:
+        hk, hv = history_k, history_v
+    o = sr.memory_kv_attention(qt, kt, vt, hk, hv, text_rows=text_rows, frame_rows=frame_rows,
+                               n_bank=n_bank, audio_rows=audio_rows).to(torch.bfloat16)
     return prope_project(o, out_matrix)

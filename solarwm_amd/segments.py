@@ -286,16 +286,19 @@ class H3WindowCache:
         self.T, self.cf, self.window, self.P = T, chunk_frames, window, int(prefix_rows)
         self.C = chunk_frames * T
         self.pf = -(-self.P // T)
+        # prefix slots: the window's prefix, or the memory layout's four spans (text, anchor,
+        # bank, audio), each starting a frame, so up to three more partly filled frames
+        self.ns = self.pf + 3
         bf = torch.bfloat16
         shape = (num_layers, window, batch, self.C, heads, 128)
         self.raw_k = torch.empty(shape, dtype=bf, device=device)
         self.raw_v = torch.empty(shape, dtype=bf, device=device)
         self.entries: list[list[tuple[int, int]]] = [[] for _ in range(num_layers)]
-        n_slots = self.pf + (window + 1) * chunk_frames
+        n_slots = self.ns + (window + 1) * chunk_frames
         self.pools = [kernels.new_pools(n_slots, batch, heads, T, bf, device)[:2]
                       for _ in range(num_layers)]
-        self.built: list[int | None] = [None] * num_layers
-        rows = max(self.pf * T, self.C)
+        self.built: list[tuple[str, int] | None] = [None] * num_layers
+        rows = max((self.pf + 1) * T, self.C)  # the largest span or chunk, in whole frames
         self._tk = torch.empty((batch, rows, heads, 128), dtype=bf, device=device)
         self._tv = torch.empty_like(self._tk)
 
@@ -350,33 +353,113 @@ class H3WindowCache:
         if kc.shape[0] != total or kv_matrix.shape[1] != total:
             raise ValueError(f"k_rotary and kv_matrix need {total} rows (prefix, {nh} history "
                              f"chunks, the chunk), got {kc.shape[0]} / {kv_matrix.shape[1]}")
-        cf = self.cf
         pslots = list(range(self.pf))
-        hslots = [self.pf + i * cf + j for i in range(nh) for j in range(cf)]
-        cslots = [self.pf + nh * cf + j for j in range(cf)]
-        if self.built[layer] != chunk_index:
+        hslots, cslots = self._history_slots(nh)
+        if self.built[layer] != ("window", chunk_index):
             if P:
                 self._to_slots(layer, pk, pv, kc[:P], ks[:P], kv_matrix[:, :P], pslots)
-            for i, (_, ring) in enumerate(hist):
-                r0 = P + i * C
-                self._to_slots(layer, self.raw_k[layer, ring], self.raw_v[layer, ring],
-                               kc[r0:r0 + C], ks[r0:r0 + C], kv_matrix[:, r0:r0 + C],
-                               hslots[i * cf:(i + 1) * cf])
-            self.built[layer] = chunk_index
+            self._build_history(layer, hist, kc[P:P + nh * C], ks[P:P + nh * C],
+                                kv_matrix[:, P:P + nh * C], hslots)
+            self.built[layer] = ("window", chunk_index)
         r0 = P + nh * C
         self._to_slots(layer, k, v, kc[r0:], ks[r0:], kv_matrix[:, r0:], cslots)
         qt = h3.rope_prope(q, q_rotary[0], q_rotary[1], q_matrix)
         lens = [T] * (self.pf - 1) + [P - (self.pf - 1) * T] if P else []
-        lens += [T] * (len(hslots) + cf)
+        lens += [T] * (len(hslots) + self.cf)
         kp, vp = self.pools[layer]
         out = kernels.attention_frames(qt, kp, vp, pslots + hslots + cslots, frame_tokens=T,
                                        softmax_scale=softmax_scale, frame_lens=lens)
         h3.rope_prope(out, None, None, out_matrix, out=out)
         if commit:
-            kept = [*hist, (chunk_index, -1)][-self.window:]
-            used = {r for _, r in kept if r >= 0}
-            ring = min(r for r in range(self.window) if r not in used)
-            self.raw_k[layer, ring].copy_(k)
-            self.raw_v[layer, ring].copy_(v)
-            self.entries[layer] = [(c, r if r >= 0 else ring) for c, r in kept]
+            self._commit(layer, chunk_index, hist, k, v)
+        return out
+
+    def _history_slots(self, nh: int) -> tuple[list[int], list[int]]:
+        cf, base = self.cf, self.ns
+        return ([base + i * cf + j for i in range(nh) for j in range(cf)],
+                [base + nh * cf + j for j in range(cf)])
+
+    def _build_history(self, layer, hist, cos, sin, matrix, hslots) -> None:
+        """Transform the raw history chunks with the window's rows of the tables into their
+        slots (once per chunk and layer)."""
+        C, cf = self.C, self.cf
+        for i, (_, ring) in enumerate(hist):
+            self._to_slots(layer, self.raw_k[layer, ring], self.raw_v[layer, ring],
+                           cos[i * C:(i + 1) * C], sin[i * C:(i + 1) * C],
+                           matrix[:, i * C:(i + 1) * C], hslots[i * cf:(i + 1) * cf])
+
+    def _commit(self, layer, chunk_index, hist, k, v) -> None:
+        """Keep the chunk's raw K/V as the newest history entry (the oldest rolls off)."""
+        kept = [*hist, (chunk_index, -1)][-self.window:]
+        used = {r for _, r in kept if r >= 0}
+        ring = min(r for r in range(self.window) if r not in used)
+        self.raw_k[layer, ring].copy_(k)
+        self.raw_v[layer, ring].copy_(v)
+        self.entries[layer] = [(c, r if r >= 0 else ring) for c, r in kept]
+
+    def attend_memory(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer: int,
+                      chunk_index: int, *, text_rows: int, n_bank: int, audio_rows: int,
+                      rotary: tuple[torch.Tensor, torch.Tensor],
+                      history_rotary: tuple[torch.Tensor, torch.Tensor] | None,
+                      q_matrix: torch.Tensor, kv_matrix: torch.Tensor, out_matrix: torch.Tensor,
+                      history_kv_matrix: torch.Tensor | None, commit: bool = False,
+                      softmax_scale: float | None = None) -> torch.Tensor:
+        """H3 memory-KV attention with its transforms (MemoryKVAttention.attend,
+        memory_kv_attention.py:39-140) on raw packed rows ``[text | anchor frame | bank frames
+        | audio | chunk]``: every row keeps one rotary row and one camera in every segment it
+        enters (``rotary``, ``q_matrix`` / ``kv_matrix`` / ``out_matrix`` per packed row), the
+        raw history chunks take ``history_rotary`` and ``history_kv_matrix`` (the window's
+        rows; None without history), so each row is transformed once and the segments run as
+        one segmented launch; outputs are projected per row.  Shared rows see the shared rows,
+        bank rows shared + bank + history, audio rows shared + audio, the chunk everything."""
+        T, C = self.T, self.C
+        shared = text_rows + T
+        bank_end = shared + n_bank * T
+        prefix = bank_end + audio_rows
+        if q.shape[1] != prefix + C or k.shape != q.shape or v.shape != q.shape:
+            raise ValueError("Memory KV packed layout mismatch")
+        if rotary[0].shape[0] != prefix + C or kv_matrix.shape[1] != prefix + C:
+            raise ValueError(f"rotary and matrices need one row per packed row ({prefix + C})")
+        hist = self.history(layer, chunk_index)
+        nh = len(hist)
+        if nh and (history_rotary is None or history_rotary[0].shape[0] != nh * C
+                   or history_kv_matrix is None or history_kv_matrix.shape[1] != nh * C):
+            raise ValueError(f"history_rotary and history_kv_matrix need {nh * C} rows")
+        cos, sin = rotary
+        nxt, spans = 0, []
+        for a, b in ((0, text_rows), (text_rows, shared), (shared, bank_end), (bank_end, prefix)):
+            nf = -(-(b - a) // T)
+            if nf > self.ns - nxt:
+                raise ValueError(f"the prefix spans need more than the cache's {self.ns} span "
+                                 f"frames (built for {self.P} prefix rows)")
+            slots = list(range(nxt, nxt + nf))
+            if nf:
+                self._to_slots(layer, k[:, a:b], v[:, a:b], cos[a:b], sin[a:b],
+                               kv_matrix[:, a:b], slots)
+            lens = [T] * (nf - 1) + [(b - a) - (nf - 1) * T] if nf else []
+            spans.append((slots, lens))
+            nxt += nf
+        hslots, cslots = self._history_slots(nh)
+        if self.built[layer] != ("memory", chunk_index):
+            if nh:
+                self._build_history(layer, hist, history_rotary[0], history_rotary[1],
+                                    history_kv_matrix, hslots)
+            self.built[layer] = ("memory", chunk_index)
+        self._to_slots(layer, k[:, prefix:], v[:, prefix:], cos[prefix:], sin[prefix:],
+                       kv_matrix[:, prefix:], cslots)
+        (ts, tl), (an, al), (bk, bl), (au, aul) = spans
+        full = [T] * len(hslots)
+        segs = [(shared, ts + an, tl + al)]
+        if n_bank:
+            segs.append((bank_end - shared, ts + an + bk + hslots, tl + al + bl + full))
+        if audio_rows:
+            segs.append((audio_rows, ts + an + au, tl + al + aul))
+        segs.append((C, ts + an + bk + au + hslots + cslots,
+                     tl + al + bl + aul + full + [T] * self.cf))
+        qt = h3.rope_prope(q, cos, sin, q_matrix)
+        kp, vp = self.pools[layer]
+        out = attend_segments(qt, kp, vp, segs, frame_tokens=T, softmax_scale=softmax_scale)
+        h3.rope_prope(out, None, None, out_matrix, out=out)
+        if commit:
+            self._commit(layer, chunk_index, hist, k[:, prefix:], v[:, prefix:])
         return out

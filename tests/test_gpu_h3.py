@@ -5,7 +5,9 @@ The transform kernel is bit-exact against the oracle's bf16 chain (rotary on [0,
 projection on [96, 128)) for every table / matrix dtype, strided BHSD views, broadcast matrices,
 row counts that leave a partial block, and in place.  The rollout window (raw chunk-list cache,
 window transformed once per chunk, chunk rows per evaluation) follows the oracle's evaluation of
-sgf_attention.py:580-659 within the attention bars of tests/helpers.py.
+sgf_attention.py:580-659, and the memory-KV layout with per-row transforms (one segmented
+launch) the oracle's memory_kv_attention.py:39-140, within the attention bars of
+tests/helpers.py.
 """
 
 import pytest
@@ -130,3 +132,41 @@ def test_h3_window_rollout_vs_oracle(gpu, P, nb):
     assert [e[0] for e in cache.history(1, 8)] == [3, 4, 5, 6, 7]
     with pytest.raises(RuntimeError):
         cache.history(0, 2)
+
+
+@pytest.mark.parametrize("n_bank,audio_rows", [(2, 70), (0, 0)])
+def test_h3_memory_kv_vs_oracle(gpu, n_bank, audio_rows):
+    """H3WindowCache.attend_memory over three chunks (history rolling in) against the oracle's
+    memory-KV evaluation with the same per-row tables and matrices."""
+    _say("h3 memory kv", n_bank, audio_rows)
+    T, H, cf, text = 64, 2, 2, 100
+    C = cf * T
+    prefix = text + T + n_bank * T + audio_rows
+    g = torch.Generator().manual_seed(21 + n_bank)
+    cache = H3WindowCache(num_layers=1, batch=1, heads=H, frame_tokens=T, prefix_rows=prefix,
+                          chunk_frames=cf, window=5, device=gpu)
+    oc = sr.H3RawKVCache()
+    for c in range(3):
+        L = prefix + C
+        cos, sin = _tables(L, g, BF)
+        hrows = min(c, 5) * C
+        hc, hs = _tables(hrows, g, BF)
+        qm, km, om = (_matrices(1, L, g) for _ in range(3))
+        hm = _matrices(1, hrows, g)
+        q, k, v = (torch.randn(1, L, H, 128, generator=g).to(BF) for _ in range(3))
+        dev = lambda t: t.to(gpu)  # noqa: E731
+        got = cache.attend_memory(dev(q), dev(k), dev(v), 0, c, text_rows=text, n_bank=n_bank,
+                                  audio_rows=audio_rows, rotary=(dev(cos), dev(sin)),
+                                  history_rotary=(dev(hc), dev(hs)) if hrows else None,
+                                  q_matrix=dev(qm), kv_matrix=dev(km), out_matrix=dev(om),
+                                  history_kv_matrix=dev(hm) if hrows else None, commit=True)
+        hist = oc.history(0, c)
+        hk = torch.cat([e[1] for e in hist], 1) if hist else k[:, :0]
+        hv = torch.cat([e[2] for e in hist], 1) if hist else v[:, :0]
+        want = ref.memory_kv_attention(q, k, v, hk, hv, text_rows=text, frame_rows=T,
+                                       n_bank=n_bank, audio_rows=audio_rows, rotary=(cos, sin),
+                                       history_rotary=(hc, hs), q_matrix=qm, kv_matrix=km,
+                                       out_matrix=om, history_kv_matrix=hm)
+        oc.commit(0, c, k[:, prefix:], v[:, prefix:])
+        torch.cuda.synchronize()
+        assert_attn_close(got, want)

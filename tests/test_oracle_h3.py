@@ -202,3 +202,41 @@ def test_identity_transforms_reduce_to_the_plain_window():
             out_matrix=eye[:, : cf * T], commit=True)
         want = sr.windowed_rollout_attention(q, k, v, pk, pv, c2, 0, c, commit=True)
         assert torch.equal(got, want.to(BF))
+
+
+def test_memory_form_identity_and_per_segment_transforms():
+    g = torch.Generator().manual_seed(8)
+    T, H, text, n_bank, audio, C = 8, 2, 5, 2, 3, 16
+    prefix = text + T + n_bank * T + audio
+    L = prefix + C
+    q, k, v = (torch.randn(1, L, H, 128, generator=g).to(BF) for _ in range(3))
+    hk, hv = (torch.randn(1, 2 * C, H, 128, generator=g).to(BF) for _ in range(2))
+    kw = dict(text_rows=text, frame_rows=T, n_bank=n_bank, audio_rows=audio)
+    ones, zeros = torch.ones(L, 96), torch.zeros(L, 96)
+    eye = torch.eye(4).expand(1, L, 4, 4)
+    heye = torch.eye(4).expand(1, 2 * C, 4, 4)
+    got = h3.memory_kv_attention(q, k, v, hk, hv, rotary=(ones, zeros),
+                                 history_rotary=(ones[:2 * C], zeros[:2 * C]), q_matrix=eye,
+                                 kv_matrix=eye, out_matrix=eye, history_kv_matrix=heye, **kw)
+    assert torch.equal(got, sr.memory_kv_attention(q, k, v, hk, hv, **kw).to(BF))
+    # per-segment transforms of the gathered rows (the reference's calculate) give the same
+    cos, sin = (torch.randn(L, 96, generator=g) for _ in range(2))
+    hc, hs = (torch.randn(2 * C, 96, generator=g) for _ in range(2))
+    qm, km, om = (torch.randn(1, L, 4, 4, generator=g) * 0.5 for _ in range(3))
+    hm = torch.randn(1, 2 * C, 4, 4, generator=g) * 0.5
+    got = h3.memory_kv_attention(q, k, v, hk, hv, rotary=(cos, sin), history_rotary=(hc, hs),
+                                 q_matrix=qm, kv_matrix=km, out_matrix=om, history_kv_matrix=hm,
+                                 **kw)
+    keys = torch.cat([k[:, :prefix], hk, k[:, prefix:]], 1)
+    vals = torch.cat([v[:, :prefix], hv, v[:, prefix:]], 1)
+    kc = torch.cat([cos[:prefix], hc, cos[prefix:]])
+    kcs = torch.cat([sin[:prefix], hs, sin[prefix:]])
+    kmm = torch.cat([km[:, :prefix], hm, km[:, prefix:]], 1)
+    segs = sr.memory_kv_segments(history_rows=2 * C, chunk_rows=C, **kw)
+    for qs, qe, ivs in segs:
+        idx = torch.cat([torch.arange(a, b) for a, b in ivs])
+        qt = h3.rope_prope(q[:, qs:qe], cos[qs:qe], sin[qs:qe], qm[:, qs:qe])
+        kt = h3.rope_prope(keys[:, idx], kc[idx], kcs[idx], kmm[:, idx])
+        vt = h3.prope_project(vals[:, idx], kmm[:, idx])
+        o = h3.prope_project(sr.attention(qt, kt, vt).to(BF), om[:, qs:qe])
+        assert torch.equal(got[:, qs:qe], o), (qs, qe)
