@@ -1039,6 +1039,87 @@ def segments_leg(device, iters=5):
     return out
 
 
+def h3_leg(device, iters=20):
+    """H3's transforms (H12 x 128, 1560-token frames, a 5-frame chunk over a 1000-row prefix
+    and 5 history chunks, the segments leg's window):
+    * ``skv_h3_rope_prope`` over the window's 47800 key rows (rotary + camera projection), bytes
+      = read + write of the rows (tables and matrices excluded), cold sources (three rotating
+      inputs over the 256 MB MALL), vs the same transform as the reference's eager torch ops
+      (rotate-half in bf16, per-row 4x4 einsum, cat: sgf_attention.py:199-203 with
+      torch_prope.py:79-93);
+    * one evaluation of a chunk through H3WindowCache with its window already built (the four
+      denoising evaluations after the first): transforms of the chunk's q / k / v, their append,
+      attention over the window, the output projection."""
+    import torch
+
+    from solarwm_amd import h3
+    from solarwm_amd.segments import H3WindowCache
+
+    T, H, cf, P = 1560, 12, 5, 1000
+    C = cf * T
+    rows = P + 6 * C
+    g = torch.Generator(device=device).manual_seed(33)
+    bf = torch.bfloat16
+    xs = [torch.randn(1, rows, H, 128, generator=g, device=device, dtype=bf) for _ in range(3)]
+    outs = [torch.empty_like(x) for x in xs]
+    theta = torch.rand(rows, 48, generator=g, device=device) * 20.0
+    cos = torch.cat([theta.cos(), theta.cos()], 1).to(bf)
+    sin = torch.cat([theta.sin(), theta.sin()], 1).to(bf)
+    m = (torch.randn(1, rows, 4, 4, generator=g, device=device) * 0.6).to(bf)
+    it = iter(range(1 << 30))
+
+    def ours():
+        i = next(it) % 3
+        h3.rope_prope(xs[i], cos, sin, m, out=outs[i])
+
+    ms = _back_to_back_ms(ours, iters)
+    nbytes = 2 * rows * H * 128 * 2
+
+    def eager():
+        x = xs[next(it) % 3]
+        x1, x2 = x[..., :48], x[..., 48:96]
+        c, s_ = cos[None, :, None], sin[None, :, None]
+        rot = torch.cat([x1 * c[..., :48] - x2 * s_[..., :48], x2 * c[..., 48:] + x1 * s_[..., 48:]], -1)
+        cam = torch.einsum("bsij,bshpj->bshpi", m, x[..., 96:].reshape(1, rows, H, 8, 4))
+        torch.cat([rot, cam.reshape(1, rows, H, 32)], -1)
+
+    eager_ms = _back_to_back_ms(eager, iters)
+    del xs, outs
+    torch.cuda.empty_cache()
+    cache = H3WindowCache(num_layers=1, batch=1, heads=H, frame_tokens=T, prefix_rows=P,
+                          chunk_frames=cf, window=5, device=device)
+    rnd = lambda *sh: torch.randn(*sh, generator=g, device=device, dtype=bf)  # noqa: E731
+    pk, pv = rnd(1, P, H, 128), rnd(1, P, H, 128)
+    qrot = (cos[:C], sin[:C])
+    qm = m[:, :C]
+    for c in range(5):
+        total = P + (c + 1) * C
+        cache.attend(rnd(1, C, H, 128), rnd(1, C, H, 128), rnd(1, C, H, 128), 0, c, prefix=(pk, pv),
+                     q_rotary=qrot, k_rotary=(cos[:total], sin[:total]), q_matrix=qm,
+                     kv_matrix=m[:, :total], out_matrix=qm, commit=True)
+    q, k, v = rnd(1, C, H, 128), rnd(1, C, H, 128), rnd(1, C, H, 128)
+
+    def evaluate():
+        cache.attend(q, k, v, 0, 5, prefix=(pk, pv), q_rotary=qrot, k_rotary=(cos, sin),
+                     q_matrix=qm, kv_matrix=m, out_matrix=qm)
+
+    eval_ms = _back_to_back_ms(evaluate, 5)
+    flops = 4.0 * C * rows * H * 128
+    del cache
+    torch.cuda.empty_cache()
+    return {
+        "rope_prope_us": round(ms * 1e3, 1),
+        "rope_prope_gbps": round(nbytes / (ms / 1e3) / 1e9, 1),
+        "rope_prope_hbm_frac": round(nbytes / (ms / 1e3) / 8e12, 4),
+        "rope_prope_eager_torch_us": round(eager_ms * 1e3, 1),
+        "rope_prope_speedup": round(eager_ms / ms, 2),
+        "window_evaluation_ms": round(eval_ms, 3),
+        "window_evaluation_tflops": round(flops / (eval_ms / 1e3) / 1e12, 1),
+        "workload": (f"H{H} x 128, {T}-token frames, {cf}-frame chunk over a {P}-row prefix and "
+                     f"5 history chunks ({rows} key rows); bf16"),
+    }
+
+
 def c5_quality(device, hs=slice(4, 6), rows=slice(1500, 1756)):
     """Config 5 cache memory and attention error on one steady-state layer pass, attributed:
     the fp8-cache output against the bf16-cache output splits into what the e4m3 cache itself
@@ -1436,6 +1517,8 @@ def main():
         log(f"[bench] aux commit_path: {aux['commit_path']}")
         aux["segments"] = segments_leg(dev)
         log(f"[bench] aux segments: {aux['segments']}")
+        aux["h3"] = h3_leg(dev)
+        log(f"[bench] aux h3: {aux['h3']}")
         aux["single_frame"] = single_frame_leg(dev)
         log(f"[bench] aux single_frame: {aux['single_frame']}")
         aux["sharp_logits"] = sharp_logits_leg(dev)

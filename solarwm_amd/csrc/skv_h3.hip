@@ -19,25 +19,57 @@ struct H3Args {
   int64_t tab_st;
   const void* m;
   int64_t m_sb, m_st;
-  int rows, heads;
+  int batch, rows, heads;
 };
 
-constexpr int kRowsPerBlock = 16;  // 16 rows x 16 vectors of 8 channels = 256 threads
+// A block moves kPairs (row, head) pairs of 256 B, heads fastest, so that a contiguous
+// [rows][heads][128] tensor is read and written as one 16 KB run per block; 16 threads per
+// pair, kIter pairs per thread with every load issued before the first store.
+constexpr int kIter = 4;
+constexpr int kPairs = 16 * kIter;
+
+// Every product and sum below is rounded where the reference rounds it: no contraction into
+// FMAs (a fused x2 s1 + t would skip the bf16 rounding of the product).
+#pragma clang fp contract(off)
 
 __device__ inline float bf16r(float x) { return (float)(bf16)x; }
 
-// 8 consecutive table values as floats rounded to bf16 (the reference rounds f32 tables)
-template <typename TT>
-__device__ inline void load8r(const TT* p, float (&o)[8]) {
-  const Vec8<TT> v = Vec8<TT>::load(p);
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 rounding of two values with one packed convert (nearest even, as bf16r)
+__device__ inline void bf16r2(float& a, float& b) {
+  const uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  a = __uint_as_float(r << 16);
+  b = __uint_as_float(r & 0xffff0000u);
+}
+
+// 8 table / matrix values as floats rounded to bf16 (bf16 inputs are exact already)
+template <typename T>
+__device__ inline void to_f32r(const Vec8<T>& v, float (&o)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const u32x4 r = v.r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = bf16r((float)v.get(i));
+    for (int w = 0; w < 4; ++w) {
+      o[2 * w] = __uint_as_float(r[w] << 16);
+      o[2 * w + 1] = __uint_as_float(r[w] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      o[e] = v.get(e);
+      o[e + 1] = v.get(e + 1);
+      bf16r2(o[e], o[e + 1]);
+    }
+  }
 }
 
 __device__ inline void unpack8(const u32x4& r, float (&o)[8]) {
-  const bf16x8 b = __builtin_bit_cast(bf16x8, r);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = (float)b[i];
+  for (int w = 0; w < 4; ++w) {
+    o[2 * w] = __uint_as_float(r[w] << 16);
+    o[2 * w + 1] = __uint_as_float(r[w] & 0xffff0000u);
+  }
 }
 
 __device__ inline u32x4 pack8(const float (&y)[8]) {
@@ -47,86 +79,129 @@ __device__ inline u32x4 pack8(const float (&y)[8]) {
   return __builtin_bit_cast(u32x4, b);
 }
 
-// grid (ceil(rows / 16), heads, batch), block 256: thread (r, v) owns channels 8v .. 8v+7 of
-// row blockIdx.x * 16 + r.  Rotary vectors (v < 12) also read their partner half (v +- 6) and
-// the row's cos / sin at their own channels; camera vectors (v >= 12) read the row's matrix.
-// Every load of the block precedes the barrier and every store follows it, so out may be x.
-template <typename TT, typename MT, bool ROPE, bool CAM>
+// grid ceil(B * rows * H / kPairs), block 256: thread (j, v) owns channels 8v .. 8v+7 of pairs
+// blockIdx.x * kPairs + 16 i + j, i < kIter (pair = (b * rows + row) * H + h).  Every load of
+// the block (features, the row's cos / sin at the thread's channels, the row's matrix) is
+// issued before the barrier and every store follows it, so out may be x.  A rotary vector
+// (v < 12) takes its partner half (v +- 6) from the partner lane, which loaded it.
+// DENSE: x and out are contiguous [B][rows][heads][128], so pair p starts at element 128 p.
+template <typename TT, typename MT, bool ROPE, bool CAM, bool DENSE>
 __global__ __launch_bounds__(256) void h3_rope_prope_kernel(H3Args a) {
-  const int tid = threadIdx.x, r = tid >> 4, v = tid & 15;
-  const int row = blockIdx.x * kRowsPerBlock + r, h = blockIdx.y, b = blockIdx.z;
-  const bool live = row < a.rows;
-  const bf16* xr = a.x + (int64_t)b * a.x_sb + (int64_t)h * a.x_sh + (int64_t)row * a.x_st;
-  u32x4 own = u32x4{0u, 0u, 0u, 0u}, part = own;
-  float c[8], s[8], m[16];
-  if (live) {
-    own = *reinterpret_cast<const u32x4*>(xr + 8 * v);
-    if constexpr (ROPE) {
-      if (v < 12) {
-        const int p = v < 6 ? v + 6 : v - 6;
-        part = *reinterpret_cast<const u32x4*>(xr + 8 * p);
-        load8r(static_cast<const TT*>(a.cos) + (int64_t)row * a.tab_st + 8 * v, c);
-        load8r(static_cast<const TT*>(a.sin) + (int64_t)row * a.tab_st + 8 * v, s);
-      }
-    }
-    if constexpr (CAM) {
-      if (v >= 12) {
-        const MT* mp = static_cast<const MT*>(a.m) + (int64_t)b * a.m_sb + (int64_t)row * a.m_st;
-        float m0[8], m1[8];
-        load8r(mp, m0);
-        load8r(mp + 8, m1);
+  const int tid = threadIdx.x, j = tid >> 4, v = tid & 15;
+  const int n_pairs = a.batch * a.rows * a.heads;  // < 2^31 (checked on the host)
+  int row_of[kIter], b_of[kIter], h_of[kIter], pair_of[kIter];
+  u32x4 own[kIter];
+  Vec8<TT> tc[kIter], ts[kIter];
+  Vec8<MT> m0[kIter], m1[kIter];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          m[i] = m0[i];
-          m[8 + i] = m1[i];
-        }
+  for (int i = 0; i < kIter; ++i) {
+    const int pair = (int)blockIdx.x * kPairs + 16 * i + j;
+    own[i] = u32x4{0u, 0u, 0u, 0u};
+    row_of[i] = -1;
+    if (pair < n_pairs) {
+      const int h = pair % a.heads, br = pair / a.heads;
+      const int row = br % a.rows, b = br / a.rows;
+      row_of[i] = row;
+      pair_of[i] = pair;
+      b_of[i] = b;
+      h_of[i] = h;
+      const int64_t xo = DENSE ? (int64_t)pair * kHeadDim
+                               : (int64_t)b * a.x_sb + (int64_t)h * a.x_sh + (int64_t)row * a.x_st;
+      own[i] = *reinterpret_cast<const u32x4*>(a.x + xo + 8 * v);
+      if (ROPE && v < 12) {
+        tc[i] = Vec8<TT>::load(static_cast<const TT*>(a.cos) + (int64_t)row * a.tab_st + 8 * v);
+        ts[i] = Vec8<TT>::load(static_cast<const TT*>(a.sin) + (int64_t)row * a.tab_st + 8 * v);
+      }
+      if (CAM && v >= 12) {
+        const MT* mp = static_cast<const MT*>(a.m) + (int64_t)b * a.m_sb + (int64_t)row * a.m_st;
+        m0[i] = Vec8<MT>::load(mp);
+        m1[i] = Vec8<MT>::load(mp + 8);
       }
     }
   }
   __syncthreads();
-  if (!live) return;
-  u32x4 res = own;
-  if (ROPE && v < 12) {
-    float xo[8], xp[8], y[8];
-    unpack8(own, xo);
-    unpack8(part, xp);
-    if (v < 6) {  // y1 = x1 c1 - x2 s1 (x1 own, x2 partner)
+  const int partner = (tid & 63 & ~15) | (v < 6 ? v + 6 : v < 12 ? v - 6 : v);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = bf16r(bf16r(xo[i] * c[i]) + bf16r(-xp[i] * s[i]));
-    } else {      // y2 = x2 c2 + x1 s2 (x2 own, x1 partner)
+  for (int i = 0; i < kIter; ++i) {
+    u32x4 part = own[i];
+    if constexpr (ROPE) {  // every lane takes part (the shuffle is wave-wide)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = bf16r(bf16r(xo[i] * c[i]) + bf16r(xp[i] * s[i]));
+      for (int w = 0; w < 4; ++w) part[w] = (uint32_t)__shfl((int)own[i][w], partner, 64);
     }
-    res = pack8(y);
-  }
-  if (CAM && v >= 12) {
-    float xo[8], y[8];
-    unpack8(own, xo);
+    if (row_of[i] < 0) continue;
+    const int row = row_of[i], b = b_of[i], h = h_of[i];
+    u32x4 res = own[i];
+    if (ROPE && v < 12) {
+      // y1 = x1 c1 + (-x2) s1 (v < 6: x1 own, x2 partner); y2 = x2 c2 + x1 s2 (x2 own, x1
+      // partner); negating the bf16 partner is exact
+      float xo[8], xp[8], c[8], sn[8], p[8], q[8], y[8];
+      unpack8(own[i], xo);
+      unpack8(part ^ (v < 6 ? u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u}
+                            : u32x4{0u, 0u, 0u, 0u}), xp);
+      to_f32r(tc[i], c);
+      to_f32r(ts[i], sn);
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float* mi = m + 4 * i;
-        const float* xv = xo + 4 * g;
-        // bf16 x bf16 products are exact in fp32: the sum order alone fixes the result
-        y[4 * g + i] = ((mi[0] * xv[0] + mi[1] * xv[1]) + mi[2] * xv[2]) + mi[3] * xv[3];
+      for (int e = 0; e < 8; ++e) {
+        p[e] = xo[e] * c[e];
+        q[e] = xp[e] * sn[e];
       }
-    res = pack8(y);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        bf16r2(p[e], p[e + 1]);
+        bf16r2(q[e], q[e + 1]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = p[e] + q[e];
+      res = pack8(y);
+    }
+    if (CAM && v >= 12) {
+      float m[16], xo[8], y[8];
+      {
+        float ma[8], mb[8];
+        to_f32r(m0[i], ma);
+        to_f32r(m1[i], mb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          m[e] = ma[e];
+          m[8 + e] = mb[e];
+        }
+      }
+      unpack8(own[i], xo);
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float* mi = m + 4 * r;
+          const float* xv = xo + 4 * g;
+          // bf16 x bf16 products are exact in fp32: the sum order alone fixes the result
+          y[4 * g + r] = ((mi[0] * xv[0] + mi[1] * xv[1]) + mi[2] * xv[2]) + mi[3] * xv[3];
+        }
+      res = pack8(y);
+    }
+    const int64_t oo = DENSE ? (int64_t)pair_of[i] * kHeadDim
+                             : (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
+    *reinterpret_cast<u32x4*>(a.out + oo + 8 * v) = res;
   }
-  bf16* orow = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)row * a.o_st;
-  *reinterpret_cast<u32x4*>(orow + 8 * v) = res;
+}
+
+template <typename TT, typename MT, bool DENSE>
+void launch_h3(const H3Args& a, bool rope, bool cam, dim3 grid, hipStream_t s) {
+  if (rope && cam)
+    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, true, true, DENSE>), grid, dim3(256), 0, s, a);
+  else if (rope)
+    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, true, false, DENSE>), grid, dim3(256), 0, s, a);
+  else if (cam)
+    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, false, true, DENSE>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, false, false, DENSE>), grid, dim3(256), 0, s, a);
 }
 
 template <typename TT, typename MT>
-void launch_h3(const H3Args& a, bool rope, bool cam, dim3 grid, hipStream_t s) {
-  if (rope && cam)
-    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, true, true>), grid, dim3(256), 0, s, a);
-  else if (rope)
-    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, true, false>), grid, dim3(256), 0, s, a);
-  else if (cam)
-    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, false, true>), grid, dim3(256), 0, s, a);
+void launch_h3(const H3Args& a, bool rope, bool cam, bool dense, dim3 grid, hipStream_t s) {
+  if (dense)
+    launch_h3<TT, MT, true>(a, rope, cam, grid, s);
   else
-    hipLaunchKernelGGL((h3_rope_prope_kernel<TT, MT, false, false>), grid, dim3(256), 0, s, a);
+    launch_h3<TT, MT, false>(a, rope, cam, grid, s);
 }
 
 // byte extent [lo, hi) of a [batch][rows][heads][128] view of 2-byte elements
@@ -152,7 +227,8 @@ extern "C" int skv_h3_rope_prope(const skv_h3_xform_desc* d, skv_stream_t stream
     set_error("skv_h3_rope_prope: head_dim=%d unsupported (built for %d)", d->head_dim, kHeadDim);
     return SKV_E_UNSUPPORTED;
   }
-  if (d->batch <= 0 || d->rows < 0 || d->heads <= 0 || d->batch > 65535 || d->heads > 65535) {
+  if (d->batch <= 0 || d->rows < 0 || d->heads <= 0 ||
+      (int64_t)d->batch * d->rows * d->heads + kPairs >= ((int64_t)1 << 31)) {
     set_error("skv_h3_rope_prope: bad sizes (batch=%d rows=%d heads=%d)", d->batch, d->rows,
               d->heads);
     return SKV_E_ARG;
@@ -208,17 +284,20 @@ extern "C" int skv_h3_rope_prope(const skv_h3_xform_desc* d, skv_stream_t stream
   }
   H3Args a{static_cast<const bf16*>(d->x), static_cast<bf16*>(d->out), d->x_sb, d->x_st,
            d->x_sh, d->out_sb, d->out_st, d->out_sh, d->cos, d->sin, d->table_stride,
-           d->matrix, d->matrix_sb, d->matrix_st, d->rows, d->heads};
-  const dim3 grid((unsigned)((d->rows + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)d->heads,
-                  (unsigned)d->batch);
+           d->matrix, d->matrix_sb, d->matrix_st, d->batch, d->rows, d->heads};
+  const int64_t n_pairs = (int64_t)d->batch * d->rows * d->heads;
+  const dim3 grid((unsigned)((n_pairs + kPairs - 1) / kPairs));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool tf = rope && d->table_dtype == SKV_F32, mf = cam && d->matrix_dtype == SKV_F32;
+  const int64_t st = (int64_t)d->heads * kHeadDim, sb = st * d->rows;
+  const bool dense = d->x_sh == kHeadDim && d->x_st == st && (d->batch == 1 || d->x_sb == sb) &&
+                     d->out_sh == kHeadDim && d->out_st == st && (d->batch == 1 || d->out_sb == sb);
   if (tf) {
-    if (mf) launch_h3<float, float>(a, rope, cam, grid, s);
-    else launch_h3<float, bf16>(a, rope, cam, grid, s);
+    if (mf) launch_h3<float, float>(a, rope, cam, dense, grid, s);
+    else launch_h3<float, bf16>(a, rope, cam, dense, grid, s);
   } else {
-    if (mf) launch_h3<bf16, float>(a, rope, cam, grid, s);
-    else launch_h3<bf16, bf16>(a, rope, cam, grid, s);
+    if (mf) launch_h3<bf16, float>(a, rope, cam, dense, grid, s);
+    else launch_h3<bf16, bf16>(a, rope, cam, dense, grid, s);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
