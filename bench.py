@@ -51,9 +51,14 @@ HBM_PEAK_GBPS = 8000.0
 # on `bench.py --probe`: FETCH_SIZE x2.0 (337.45 MB) + WRITE_SIZE x1.0 (14.38 MB); the scale
 # factors are what the same counters read for a 1 GiB device copy.  Counters cannot be read
 # from inside the process, so the figure is recorded here for the config it was measured on.
-ATTN_TRAFFIC_BYTES = {"c2": 351.83e6}
+# Config 5 (one attention call = the unsplit launch, the tail-split launch and the merge, as
+# the roofline's achieved figure is per call): 591.0 + 473.0 + 49.9 MB read, 48.5 + 68.2 +
+# 9.1 MB written (profiles/attn_fp8_c5_counters.txt).
+ATTN_TRAFFIC_BYTES = {"c2": 351.83e6, "c5": 1239.7e6}
+ATTN_TRAFFIC_FILES = {"c2": "profiles/attn_kernel_c2_traffic.txt",
+                      "c5": "profiles/attn_fp8_c5_counters.txt"}
 ATTN_TRAFFIC_SOURCE = ("recorded constant, not measured in this run: rocprofv3 --pmc FETCH_SIZE "
-                       "and WRITE_SIZE runs of `bench.py --probe` (profiles/attn_kernel_c2_traffic.txt)")
+                       "and WRITE_SIZE runs of `bench.py --probe --config {cfg}` ({file})")
 # Launch timing inside the timed rollout: HIP events around every 7th launch of each kind
 # (7 is coprime with the 150 launches of a chunk, so the samples rotate over layers and
 # passes).  A timing event waits for the work before it; events around every launch cost
@@ -1393,8 +1398,13 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4),
             "traffic": ATTN_TRAFFIC_BYTES.get(args.config),
-            "traffic_per": "steady-state launch (Lk = cache window), rocprofv3 FETCH_SIZE + WRITE_SIZE",
-            "traffic_source": ATTN_TRAFFIC_SOURCE,
+            "traffic_per": ("steady-state launch (Lk = cache window), rocprofv3 FETCH_SIZE + WRITE_SIZE"
+                            if cfg["cache"] == "bf16" else
+                            "steady-state call (Lk = cache window): unsplit launch + tail-split "
+                            "launch + merge, rocprofv3 FETCH_SIZE + WRITE_SIZE"),
+            "traffic_source": (ATTN_TRAFFIC_SOURCE.format(cfg=args.config,
+                                                          file=ATTN_TRAFFIC_FILES[args.config])
+                               if args.config in ATTN_TRAFFIC_FILES else None),
             "launches_timed": st["attn_launches"],
             "timed_every": EVENT_EVERY,
             "avg_launch_ms": round(st["attn_avg_ms"], 4),
