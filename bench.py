@@ -1511,6 +1511,10 @@ def main():
         log(f"[bench] aux c2_rope: {aux['c2_rope']}")
         aux["c2_prope"] = c2_rope(dev, prope=True)
         log(f"[bench] aux c2_prope: {aux['c2_prope']}")
+        notes = {"c5_rope": "fp8 raw frames plus an fp8 RoPE copy of K; attn_fp8_kernel turns "
+                            "the query's temporal pairs per key frame and multiplies e4m3 codes",
+                 "c5_prope": "fp8 raw frames plus fp8 PRoPE copies; the attention decodes each "
+                             "staged tile to bf16 and multiplies in bf16"}
         for name, kw in (("c5_rope", dict(rope=True)), ("c5_prope", dict(prope=True))):
             log(f"[bench] aux {name}: fp8 cache with RoPE on load")
             r = steady_state("c5", dev, timed=2, **kw)
@@ -1520,8 +1524,7 @@ def main():
                          "attn_frac_bf16_peak": round(r["attn_tflops"] / BF16_PEAK_TFLOPS, 4),
                          "append_avg_us": round(r["append_avg_us"], 2),
                          "workload": r["workload"],
-                         "note": "fp8 raw frames plus fp8 RoPE (PRoPE) copies; the attention "
-                                 "decodes each staged tile to bf16 and multiplies in bf16"}
+                         "note": notes[name]}
             log(f"[bench] aux {name}: {aux[name]}")
         aux["commit_path"] = commit_path(dev)
         log(f"[bench] aux commit_path: {aux['commit_path']}")

@@ -24,6 +24,14 @@ Pinning (tests/test_oracle.py):
 * ``memory_gather`` — index semantics checked against per-frame slicing.
 * ``fp8_fake_quant_frames`` / ``fp8_fake_quant_rows`` — compositions of the pinned
   ``fp8_quantize``; checked for block independence and exact decoding of representable values.
+* ``fp8_rope_query_frames`` / ``fp8_rope_attention`` — every logit of the quantised query
+  against the RoPE copy stays within the e4m3 error bound of the float64 RoPE logits
+  (rope_frames at p_q and p_k; a reversed angle, a wrong temporal/spatial split or a scale that
+  lets a rotation clip fail it, planted rows included); identical keys give the mean of V; with
+  every angle zero (one-token frames, equal positions) and zero temporal channels the query is
+  ``fp8_fake_quant_rows``'s.
+* ``cached_self_attention(rope={"attend": ...})`` — with an attend that rotates at the given
+  positions it equals the built-in RoPE path exactly (sink and no-sink windows, memory frames).
 * ``rope_params`` / ``wan_rope_freqs`` / ``rope_frames`` — angles against ``math.cos`` /
   ``math.sin`` of position × theta^(-2j/d) computed independently; the temporal/height/width
   channel split; rotation preserves each pair's norm; position 0 is the identity; scores depend
@@ -145,7 +153,10 @@ def cached_self_attention(
     ``rope`` (``{"freqs", "grid_hw", "use_echorope", "rope_train_frames"}``) makes ``q``/``k``
     pre-RoPE, as the reference stores them: the cache keeps raw K and the query chunk, sink
     frames and local frames are rotated at the positions of ``rope_positions`` before attention
-    (causal_model.py:1135-1199 with _rope_sink_local_and_query / _rope_q_and_window_k).
+    (causal_model.py:1135-1199 with _rope_sink_local_and_query / _rope_q_and_window_k).  With
+    ``rope["attend"]`` (a callable ``(q, k, v, q_positions, k_positions) -> x``) nothing is
+    rotated here: the callable receives the raw query, the raw window (memory frames first) and
+    the frame positions the rotation would use, and its result is the attention output.
 
     ``prope`` (``{"q_viewmats", "q_ks", "kv_viewmats", "kv_ks"}`` plus optional ``"transform"``
     and ``"emulate_bf16"``) applies fused PRoPE after RoPE (causal_model.py:1170-1199): query
@@ -243,12 +254,17 @@ def cached_self_attention(
                 max_attention_size=max_attention_size, frame_seqlen=frame_seqlen,
                 table_len=rope["freqs"].shape[0], rope_train_frames=rope.get("rope_train_frames"),
                 current_start_frame=current_start // frame_seqlen, sink_branch=True)
-            q = rope_frames(q, rope["grid_hw"], range(pos["q_start"], pos["q_start"] + nb), rope["freqs"])
-            k_sink = rope_frames(k_sink, rope["grid_hw"], range(k_sink.shape[1] // frame_seqlen), rope["freqs"])
             nl = k_loc.shape[1] // frame_seqlen
-            if nl > 0:
-                k_loc = rope_frames(k_loc, rope["grid_hw"], range(pos["local_start"], pos["local_start"] + nl),
-                                    rope["freqs"])
+            q_pos = list(range(pos["q_start"], pos["q_start"] + nb))
+            k_pos = list(range(k_sink.shape[1] // frame_seqlen)) + list(
+                range(pos["local_start"], pos["local_start"] + nl))
+            if "attend" not in rope:
+                q = rope_frames(q, rope["grid_hw"], q_pos, rope["freqs"])
+                k_sink = rope_frames(k_sink, rope["grid_hw"], range(k_sink.shape[1] // frame_seqlen),
+                                     rope["freqs"])
+                if nl > 0:
+                    k_loc = rope_frames(k_loc, rope["grid_hw"], range(pos["local_start"], pos["local_start"] + nl),
+                                        rope["freqs"])
         k_cat = torch.cat([k_sink, k_loc], dim=1)
         v_cat = torch.cat([v_sink, v_loc], dim=1)
     else:
@@ -264,20 +280,28 @@ def cached_self_attention(
                 frame_seqlen=frame_seqlen, table_len=rope["freqs"].shape[0], sink_branch=False)
             if nw == 0:
                 raise RuntimeError("EchoRoPE attention got an empty K window")
-            q = rope_frames(q, rope["grid_hw"], range(pos["q_start"], pos["q_start"] + nb), rope["freqs"])
-            k_cat = rope_frames(k_cat, rope["grid_hw"], range(pos["local_start"], pos["local_start"] + nw),
-                                rope["freqs"])
+            q_pos = list(range(pos["q_start"], pos["q_start"] + nb))
+            k_pos = list(range(pos["local_start"], pos["local_start"] + nw))
+            if "attend" not in rope:
+                q = rope_frames(q, rope["grid_hw"], q_pos, rope["freqs"])
+                k_cat = rope_frames(k_cat, rope["grid_hw"], k_pos, rope["freqs"])
     if memory_k is not None:
         mk = memory_k.to(k_cat.dtype)
         if rope is not None:
             nm = mk.shape[1] // frame_seqlen
             if memory_positions is None or len(memory_positions) != nm:
                 raise ValueError("RoPE with memory-bank frames needs one position per bank frame")
-            mk = rope_frames(mk, rope["grid_hw"], list(memory_positions), rope["freqs"])
+            k_pos = list(memory_positions) + k_pos
+            if "attend" not in rope:
+                mk = rope_frames(mk, rope["grid_hw"], list(memory_positions), rope["freqs"])
         k_cat = torch.cat([mk, k_cat], dim=1)
         v_cat = torch.cat([memory_v.to(v_cat.dtype), v_cat], dim=1)
     if k_cat.shape[1] == 0:
         raise RuntimeError("KV-cache attention window is empty")
+    if rope is not None and "attend" in rope:
+        if prope is not None:
+            raise NotImplementedError("rope['attend'] with PRoPE is outside this restatement")
+        return rope["attend"](q, k_cat, v_cat, q_pos, k_pos), (current_end, local_end_index, info)
     if prope is not None:
         if memory_k is not None:
             raise NotImplementedError("PRoPE with memory-bank frames is outside this restatement")
@@ -458,11 +482,99 @@ def fp8_rope_copy_effective(k: torch.Tensor, grid_hw: tuple[int, int], freqs: to
     the decoded copy exactly, so the oracle's own RoPE path runs on the quantised values.  Not
     a reference function: the reference has no fp8 cache (BASELINE config 5 defines the scales).
     """
-    nf = k.shape[1] // frame_seqlen
-    zero = [0] * nf
-    copy = rope_frames(k.double(), grid_hw, zero, freqs).to(torch.bfloat16)
-    deq = fp8_fake_quant_frames(copy.float(), frame_seqlen).double()
+    zero = [0] * (k.shape[1] // frame_seqlen)
+    deq = fp8_rope_copy_decoded(k, grid_hw, freqs, frame_seqlen).double()
     return rope_frames(deq, grid_hw, zero, freqs.conj())
+
+
+def fp8_rope_copy_decoded(k: torch.Tensor, grid_hw: tuple[int, int], freqs: torch.Tensor,
+                          frame_seqlen: int) -> torch.Tensor:
+    """Raw K [B, n*T, H, D] -> the decoded fp8 RoPE copy a pre-RoPE fp8 cache attends with
+    (float32): height/width pairs rotated in float64 and rounded to bf16 (the bf16 copy, temporal
+    pairs raw), then quantised per (frame, stream, head) with its own absmax/448 and decoded."""
+    zero = [0] * (k.shape[1] // frame_seqlen)
+    copy = rope_frames(k.double(), grid_hw, zero, freqs).to(torch.bfloat16)
+    return fp8_fake_quant_frames(copy.float(), frame_seqlen)
+
+
+def _inv_freq_f64(dim: int, theta: float) -> torch.Tensor:
+    return 1.0 / torch.pow(torch.tensor(theta, dtype=torch.float64),
+                           torch.arange(0, dim, 2, dtype=torch.float64) / dim)
+
+
+def fp8_rope_query_frames(q: torch.Tensor, grid_hw: tuple[int, int], q_positions: Sequence[int],
+                          k_positions: Sequence[int], frame_seqlen: int,
+                          theta: float = 10000.0) -> torch.Tensor:
+    """The e4m3 query the fp8 RoPE-on-load attention multiplies key frame j with, decoded:
+    float32 [n_k, B, Lq, H, D] for q [B, n_q*T, H, D] whose frame f sits at ``q_positions[f]``.
+
+    Not a reference function (the reference has no fp8 cache; BASELINE config 5 defines the
+    scales): it states the quantisation contract of this repository's kernel so that a test can
+    reproduce its codes exactly.  Every product and sum is an IEEE float32 operation rounded on
+    its own; tables are float32 cos / sin of float64 angles:
+    * q rounded to bf16; the height/width pairs (22..42, 43..63) turned by the token's own h / w
+      (angle h·w_j, w·w_j with w_j = theta^(-2j/42)): u' = bf16(u c - v s), v' = bf16(u s + v c);
+    * row bound = max(|u'|, |v'| over those pairs, sqrt(u u + v v) over the temporal pairs
+      0..21), inv = 448 / bound (0 for an all-zero row), scale = bound / 448 — a bound no
+      rotation of a temporal pair can exceed;
+    * per key frame j: the temporal pairs turned by the angle (p_q - p_k[j])·w_i with w_i =
+      theta^(-2i/44), rounded to bf16; code = RNE_e4m3(clamp(x · inv, ±448)); value = code · scale.
+    """
+    gh, gw = grid_hw
+    B, L, H, D = q.shape
+    T = frame_seqlen
+    if L != len(q_positions) * T or T != gh * gw:
+        raise ValueError("fp8_rope_query_frames: q needs len(q_positions) frames of gh*gw tokens")
+    ct, ch, cw = rope_split(D)
+    x = q.to(torch.bfloat16).float().reshape(B, L, H, D // 2, 2)
+    u, v = x[..., 0], x[..., 1]
+    tok = torch.arange(L) % T
+    inv_s = _inv_freq_f64(2 * ch, theta)
+    ang_s = torch.cat([(tok // gw).double()[:, None] * inv_s, (tok % gw).double()[:, None] * inv_s], 1)
+    c, s = torch.cos(ang_s).float()[None, :, None, :], torch.sin(ang_s).float()[None, :, None, :]
+    us, vs = u[..., ct:], v[..., ct:]
+    u2 = (us * c - vs * s).to(torch.bfloat16).float()
+    v2 = (us * s + vs * c).to(torch.bfloat16).float()
+    ut, vt = u[..., :ct], v[..., :ct]
+    bound = torch.maximum(torch.maximum(u2.abs(), v2.abs()).amax(-1),
+                          torch.sqrt(ut * ut + vt * vt).amax(-1))
+    e4 = torch.tensor(E4M3_MAX, dtype=torch.float32)
+    inv = torch.where(bound > 0, e4 / bound, torch.zeros_like(bound))[..., None]
+    scale = (bound / e4)[..., None]
+    inv_t = _inv_freq_f64(2 * ct, theta)
+    pq = torch.tensor(list(q_positions), dtype=torch.float64)[torch.arange(L) // T]
+    out = []
+    for pk in k_positions:
+        ang = (pq - float(pk))[:, None] * inv_t
+        c, s = torch.cos(ang).float()[None, :, None, :], torch.sin(ang).float()[None, :, None, :]
+        u3 = (ut * c - vt * s).to(torch.bfloat16).float()
+        v3 = (ut * s + vt * c).to(torch.bfloat16).float()
+        y = torch.stack([torch.cat([u3, u2], -1), torch.cat([v3, v2], -1)], -1).reshape(B, L, H, D)
+        codes = (y * inv).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+        out.append(codes.float() * scale)
+    return torch.stack(out)
+
+
+def fp8_rope_attention(q: torch.Tensor, k_copy: torch.Tensor, v: torch.Tensor,
+                       grid_hw: tuple[int, int], q_positions: Sequence[int],
+                       k_positions: Sequence[int], frame_seqlen: int, theta: float = 10000.0,
+                       softmax_scale: float | None = None) -> torch.Tensor:
+    """Attention of the fp8 RoPE-on-load path with its quantised queries, float64 softmax.
+
+    ``k_copy`` [B, n_k*T, H, D]: the keys as the cache's RoPE copy holds them (height/width
+    pairs rotated, temporal pairs raw; ``fp8_rope_copy_decoded``); key frame j sits at
+    ``k_positions[j]``.  Logits of key frame j are ``fp8_rope_query_frames(...)[j] · k_copy_j``
+    (the temporal turn by p_q - p_k on the query equals RoPE at p_q on q and p_k on k); softmax
+    over every key in float64, times ``v``.  Returns float64 [B, Lq, H, D].
+    """
+    B, L, H, D = q.shape
+    T, nk = frame_seqlen, len(k_positions)
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    qd = fp8_rope_query_frames(q, grid_hw, q_positions, k_positions, T, theta).double()
+    kc = k_copy.double().reshape(B, nk, T, H, D)
+    logits = torch.einsum("jblhd,bjthd->bhljt", qd, kc).reshape(B, H, L, nk * T) * scale
+    p = torch.softmax(logits, dim=-1)
+    return torch.einsum("bhlk,bkhd->blhd", p, v.double())
 
 
 def e4m3_decode(code: int) -> float:

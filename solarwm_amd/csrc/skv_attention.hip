@@ -1245,8 +1245,21 @@ constexpr int kOp8 = 2048;
 // slower than 4 at C5: the waves drift further apart between barriers).  4-wave groups keep two
 // buffers (with four they spill a register).
 constexpr int fp8_ring(int nw) { return nw == 8 ? 4 : 2; }
-// dynamic LDS of attn_fp8_kernel: the K and V^T rings (4 operand blocks of kOp8 bytes per tile)
-constexpr int fp8_lds_bytes(int nw) { return 2 * fp8_ring(nw) * 4 * kOp8; }
+// dynamic LDS of attn_fp8_kernel: the K and V^T rings (4 operand blocks of kOp8 bytes per tile);
+// for RoPE on load (RM = 1) also each wave's 4 KB of query channels 0..63 in bf16 (the temporal
+// pairs unrotated), from which the temporal part of the fp8 query is rebuilt per key frame, and
+// one table slot per ring buffer: the temporal angles (22 pairs x cos, sin = 176 B) of the
+// q-tile's query frames (at most 5) against the key frame a tile opens
+constexpr int kFp8QRows = 4096;
+constexpr int kFp8TabSlot = 1024;
+constexpr int kFp8TabFrames = 5;
+static_assert(kFp8TabFrames * 8 * kRopeT <= kFp8TabSlot && kFp8TabFrames * 11 <= 64,
+              "one 64-lane DMA of 16 B pieces fills a table slot");
+static_assert((256 - 1) / 64 + 2 <= kFp8TabFrames, "256 rows of >= 64-token frames span <= 5 frames");
+constexpr int fp8_lds_bytes(int nw, int rm = 0) {
+  return 2 * fp8_ring(nw) * 4 * kOp8 +
+         (rm == 1 ? nw * kFp8QRows + fp8_ring(nw) * kFp8TabSlot : 0);
+}
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 __device__ inline int key_perm64(int kb, int r) {
@@ -1331,9 +1344,15 @@ __device__ inline void qk64(const char* kl, const i32x8 (&q8)[2], const f32x16& 
   }
 }
 
-template <int NW, typename QT, bool SPLIT = false>
+// RM = 1: RoPE on load (the K pool is the fp8 copy with its height/width pairs rotated, the
+// temporal pairs raw).  The query's height/width pairs are rotated once at load; its temporal
+// pairs (channels 0..43, which lie in the lane's first 32-channel slice) are turned by the angle
+// of (query frame, key frame) and quantised again whenever the key walk enters a frame.  The
+// row scale bounds every rotation: max(spatial |q|, temporal pair norms) / 448.
+template <int NW, typename QT, bool SPLIT = false, int RM = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fp8_kernel(AttnArgs a) {
+  static_assert(RM == 0 || RM == 1, "fp8 MFMA attention: no RoPE or RoPE on load");
   constexpr int kBQ = NW * 32;
   constexpr int kDma = 16 / NW;     // 1 KB DMA parts per wave per tile (8 for K, 8 for V^T)
   constexpr int kBuf = 4 * kOp8;    // one K (or V^T) tile
@@ -1380,6 +1399,8 @@ void attn_fp8_kernel(AttnArgs a) {
   // Q row quantisation: lane (n, hh) holds channels cs*64 + 32 hh .. +31 for cs = 0, 1.
   i32x8 q8[2];
   float q_scale;
+  [[maybe_unused]] int qfi = 0;        // RM = 1: query frame of this lane's row
+  [[maybe_unused]] float q_inv = 0.f;  // RM = 1: 448 / the row's bound
   {
     float qv[64];  // qv[cs * 32 + j] = channel cs * 64 + 32 hh + j
     const QT* qp = static_cast<const QT*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh +
@@ -1401,11 +1422,52 @@ void attn_fp8_kernel(AttnArgs a) {
         }
       }
     float amax = 0.f;
+    if constexpr (RM == 1) {
+      // height/width pairs (global pair index cs * 32 + 16 hh + m >= 22) turned by the query's
+      // own position, in fp32 from the values above, then rounded to bf16 (the roped bf16
+      // query); temporal pairs stay as loaded and bound the scale by their norms.  Every product
+      // and sum rounds on its own (no contraction), so the fp8 codes are a fixed function of the
+      // inputs that a CPU restatement reproduces exactly.
+#pragma clang fp contract(off)
+      const int qr = qlive ? qrow : a.Lq - 1;
+      qfi = qr / a.T;
+      const int tt = qr - qfi * a.T, hq = tt / a.gw, wq = tt - hq * a.gw;
+      // every lane loads an in-bounds table entry and selects (no lane-divergent branches)
 #pragma unroll
-    for (int j = 0; j < 64; ++j) amax = fmaxf(amax, __builtin_fabsf(qv[j]));
+      for (int cs = 0; cs < 2; ++cs)
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          const int pr = cs * 32 + hh * 16 + m;
+          const bool temporal = pr < kRopeT;
+          float& u = qv[cs * 32 + 2 * m];
+          float& v = qv[cs * 32 + 2 * m + 1];
+          const int idx = pr < kRopeT + kRopeHW ? hq * kRopeHW + max(pr - kRopeT, 0)
+                                                : (a.gh + wq) * kRopeHW + (pr - kRopeT - kRopeHW);
+          const float2 cn = *reinterpret_cast<const float2*>(a.rope_hw + 2 * idx);
+          const float u2 = (float)(bf16)(u * cn.x - v * cn.y), v2 = (float)(bf16)(u * cn.y + v * cn.x);
+          const float bound = temporal ? __builtin_sqrtf(u * u + v * v)
+                                       : fmaxf(__builtin_fabsf(u2), __builtin_fabsf(v2));
+          amax = fmaxf(amax, bound);
+          u = temporal ? u : u2;
+          v = temporal ? v : v2;
+        }
+      // slice 0 (channels 32 hh .. +31) to this wave's LDS rows: chunk c of lane L at c KB + 16 L
+      char* qs = lds + fp8_lds_bytes(NW) + w * kFp8QRows + lane * 16;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        bf16x8 t;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = (bf16)qv[8 * c + e];
+        *reinterpret_cast<bf16x8*>(qs + c * 1024) = t;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 64; ++j) amax = fmaxf(amax, __builtin_fabsf(qv[j]));
+    }
     amax = pair_max(amax);
     const float inv = amax > 0.f ? 448.0f / amax : 0.f;
     q_scale = amax / 448.0f;
+    q_inv = inv;
     auto cl = [&](float x) { return fminf(fmaxf(x * inv, -448.f), 448.f); };
 #pragma unroll
     for (int cs = 0; cs < 2; ++cs)
@@ -1475,6 +1537,67 @@ void attn_fp8_kernel(AttnArgs a) {
   auto kb_lds = [&](int i) { return lds + (i & (kRing - 1)) * kBuf; };
   auto vb_lds = [&](int i) { return lds + (kRing + (i & (kRing - 1))) * kBuf; };
 
+  // RM = 1: the temporal angles of the q-tile's query frames qf_lo .. (at most kFp8TabFrames,
+  // checked by the host) against key frame j -> the table slot of the tile x that opens frame j
+  // (slot x mod kRing, written with K(x) and read before QK(x), so it lives like K(x)'s buffer).
+  // Lane i moves 16 bytes: pairs 2 (i % 11) .. +1 of query frame qf_lo + i / 11; lanes past the
+  // q-tile's frames repeat frame qf_lo's pieces into the slot's unread tail.
+  [[maybe_unused]] const int qf_lo = q0 / a.T;
+  [[maybe_unused]] char* const tab_lds = lds + fp8_lds_bytes(NW) + NW * kFp8QRows;
+  [[maybe_unused]] auto stage_tab = [&](int x, int j) __attribute__((always_inline)) {
+    if constexpr (RM == 1) {
+      const int count = (min(q0 + kBQ, a.Lq) - 1) / a.T - qf_lo + 1;
+      const int f = lane / 11, pp = lane - 11 * f;
+      Stage64<1> st;
+      st.goff[0] = (uint32_t)((((qf_lo + (f < count ? f : 0)) * a.n_frames + j) * kRopeT + 2 * pp) * 8);
+      st.loff[0] = (x & (kRing - 1)) * kFp8TabSlot;
+      st(reinterpret_cast<const uint8_t*>(a.rope_t), tab_lds);
+    }
+  };
+  // RM = 1: q8[0] (channels 32 hh .. +31) rebuilt for the key frame tile x opens: the temporal
+  // pairs (global index 16 hh + 4 c + m < 22) turned by the angle of (this row's query frame,
+  // that key frame) in fp32, rounded to bf16 and quantised with the row's scale; the other pairs
+  // of the slice (roped at load) take an exact identity turn and quantise as before.  Every lane
+  // reads an in-bounds table entry and selects.
+  [[maybe_unused]] auto requant = [&](int x) __attribute__((always_inline)) {
+    if constexpr (RM == 1) {
+#pragma clang fp contract(off)
+      // pairs 16 hh .. +15 of the row's query frame (128 B from a 32-aligned offset inside the
+      // slot: (qfi - qf_lo) * 176 + 128 hh + 128 <= 4 * 176 + 256 < kFp8TabSlot), 4 pairs per
+      // chunk c read by an asm block: the compiler's own LDS reads of a DMA-written buffer would
+      // first wait for every DMA in flight (the next tiles' K and V), which the barrier after the
+      // slot's DMA already covers
+      const uint32_t tab = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(
+          tab_lds + (x & (kRing - 1)) * kFp8TabSlot + (qfi - qf_lo) * (8 * kRopeT) + hh * 128);
+      const char* qs = lds + fp8_lds_bytes(NW) + w * kFp8QRows + lane * 16;
+      auto cl = [&](float v) { return fminf(fmaxf(v * q_inv, -448.f), 448.f); };
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        f32x4 tq[2];  // cos, sin of pairs 16 hh + 4 c .. +1, then +2 .. +3
+        asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(tq[0]), "=&v"(tq[1])
+                     : "v"(tab + 32 * c));
+        const bf16x8 t = *reinterpret_cast<const bf16x8*>(qs + c * 1024);
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = (float)t[e];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          // pair 16 hh + 4 c + m: temporal below 22; the others read past the frame's 22 pairs
+          // (values discarded by the select)
+          const bool temporal = hh * 16 + c * 4 + m < kRopeT;
+          const float cr = temporal ? tq[m >> 1][2 * (m & 1)] : 1.0f;
+          const float sr = temporal ? tq[m >> 1][2 * (m & 1) + 1] : 0.0f;
+          const float u = y[2 * m], v = y[2 * m + 1];
+          y[2 * m] = (float)(bf16)(u * cr - v * sr);
+          y[2 * m + 1] = (float)(bf16)(u * sr + v * cr);
+        }
+        q8[0][2 * c] = pack_fp8x4(cl(y[0]), cl(y[1]), cl(y[2]), cl(y[3]));
+        q8[0][2 * c + 1] = pack_fp8x4(cl(y[4]), cl(y[5]), cl(y[6]), cl(y[7]));
+      }
+    }
+  };
+
   float sv_max = 0.f;
   for (int j = 0; j < a.n_frames; ++j)
     sv_max = fmaxf(sv_max, a.vscale[(int64_t)a.slots[j] * a.B * a.H + sc_bh]);
@@ -1521,11 +1644,22 @@ void attn_fp8_kernel(AttnArgs a) {
         wv.next(a, kbh);
       }
     }
+    if constexpr (RM == 1) {  // the angles for tile 0's frame and for frames tiles 1..kL open
+      if (wu == 0) {
+        stage_tab(0, w0.j);
+#pragma unroll
+        for (int x = 1; x <= kL; ++x) {
+          const int g = tb + x, j = g / a.ntiles_f;
+          if (x < ntau && g == j * a.ntiles_f) stage_tab(x, j);
+        }
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 8 / NW; ++r)
       *reinterpret_cast<u32x4*>(vb_lds(-1) + (tid + NW * 64 * r) * 16) = u32x4{0u, 0u, 0u, 0u};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if constexpr (RM == 1) requant(0);  // the query for the frame of tile 0
     qk64(kb_lds(0) + lane16, q8, zero16, sA);
     int tok0, key0, tj;
     if (tile_needs_mask(0, tok0, key0, tj)) mask_tile64(sA, hh, tok0, tj, key0, lim_lane);
@@ -1610,13 +1744,19 @@ void attn_fp8_kernel(AttnArgs a) {
   // at the barrier
   auto step = [&](int tau, const int cb, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2], i32x8& pprev,
                   i32x8& pb) __attribute__((always_inline)) {
-    if (tau + kL + 1 < ntau) if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(tau + kL + 1));
+    if (tau + kL + 1 < ntau) {
+      if (kload) stage(kpool + kw.base + (int64_t)kw.t * kTile * kHeadDim, kb_lds(tau + kL + 1));
+      if constexpr (RM == 1)  // tile tau+kL+1 opens frame kw.j: its angles travel with K
+        if (wu == 0 && kw.t == 0) stage_tab(tau + kL + 1, kw.j);
+    }
     if (tau + kL - 1 < ntau) if (!kload) stage(vpool + vw.base + vw.t * kTile, vb_lds(tau + kL - 1));
     if (tau > 0) settle(s_nxt, pprev);  // s_nxt still holds the scores of tile tau-1
     if (open_slot >= 0) {  // tile tau opens a key frame
       open_scales(open_slot);
       open_slot = -1;
     }
+    if constexpr (RM == 1)  // QK(tau+1) below takes the query of tile tau+1's frame
+      if (tau + 1 < ntau && mw.t == 0) requant(tau + 1);
     const char* kl = kb_lds(tau + 1) + lane16;  // K(tau+1) (stale data on the last step)
     const char* vl = vb_lds(tau - 1) + lane16;  // V(tau-1) (zeros on the first step)
 
@@ -1849,20 +1989,39 @@ static void launch(const AttnArgs& a, int q_dtype, int pool_dtype, int rm, hipSt
     }
     return;
   }
-  if (pool_dtype == SKV_FP8_E4M3 && rm > 0) {  // bf16 queries (checked by the caller)
+  // fp8 pools with RoPE on load: the fp8-MFMA kernel (query temporal pairs rebuilt per key
+  // frame) when a q-tile spans at most kFp8TabFrames query frames (frames of >= 64 tokens);
+  // shorter frames and fused PRoPE take the bf16 kernel staging decoded tiles (PRoPE's
+  // per-key-frame W is unbounded, so the query cannot keep one fp8 scale).  bf16 queries
+  // (checked by the caller).
+  if (pool_dtype == SKV_FP8_E4M3 && rm == 1 && a.T < kTile) {
     if constexpr (NW == 8) {
       if (a.split) {
-        if (rm == 2)
-          hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 2, true>), grid, block, attn_lds_bytes(NW, 2, 1, true, false), s, a);
-        else
-          hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 1, true>), grid, block, attn_lds_bytes(NW, 1, 1, true, false), s, a);
+        hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 1, true>), grid, block, attn_lds_bytes(NW, 1, 1, true, false), s, a);
         return;
       }
     }
-    if (rm == 2)
-      hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 2>), grid, block, attn_lds_bytes(NW, 2, 1, false, false), s, a);
-    else
-      hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 1>), grid, block, attn_lds_bytes(NW, 1, 1, false, false), s, a);
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 1>), grid, block, attn_lds_bytes(NW, 1, 1, false, false), s, a);
+    return;
+  }
+  if (pool_dtype == SKV_FP8_E4M3 && rm == 1) {
+    if constexpr (NW == 8) {
+      if (a.split) {
+        hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, true, 1>), grid, block, fp8_lds_bytes(NW, 1), s, a);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((attn_fp8_kernel<NW, bf16, false, 1>), grid, block, fp8_lds_bytes(NW, 1), s, a);
+    return;
+  }
+  if (pool_dtype == SKV_FP8_E4M3 && rm == 2) {  // bf16 queries (checked by the caller)
+    if constexpr (NW == 8) {
+      if (a.split) {
+        hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 2, true>), grid, block, attn_lds_bytes(NW, 2, 1, true, false), s, a);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((attn_kernel<NW, bf16, fp8e4, 2>), grid, block, attn_lds_bytes(NW, 2, 1, false, false), s, a);
     return;
   }
   if (pool_dtype == SKV_FP8_E4M3) {
@@ -2025,6 +2184,11 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   }
   if (prope && (int64_t)batch * n_frames * n_qframes * kWPair >= ((int64_t)1 << 31)) {
     set_error("skv_attention_prope: q_xform_t exceeds 2^31 bytes");
+    return SKV_E_ARG;
+  }
+  if (rope && pool_dtype == SKV_FP8_E4M3 &&
+      (int64_t)n_qframes * n_frames * 8 * kRopeT >= ((int64_t)1 << 31)) {
+    set_error("skv_attention_rope: rope_t exceeds 2^31 bytes");
     return SKV_E_ARG;
   }
   if (prope && frame_tokens < kTile) {

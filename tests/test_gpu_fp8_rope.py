@@ -3,22 +3,26 @@
 An fp8 pre-RoPE cache keeps the raw frames as e4m3 codes with per-(slot, stream, head) scales, as
 the post-RoPE fp8 cache does, plus fp8 copies the attention reads: K with its height/width RoPE
 pairs rotated (and, camera-aware, P⁻¹ on K's spatial groups and P⁻¹ v), each with its own scales.
-The attention decodes each staged tile to bf16 with its frame's scale and multiplies in bf16, so
-the queries and probabilities are not quantised.
+RoPE on load over frames of at least 64 tokens runs the fp8-MFMA kernel: the query's spatial
+pairs are turned once, its temporal pairs per key frame, and it is quantised per row to e4m3 with
+a bound no turn exceeds.  Shorter frames and fused PRoPE run the bf16 kernel, which decodes each
+staged tile to bf16 with its frame's scale and multiplies in bf16.
 
 Bars:
 * raw codes and scales bit-exact against the oracle quantisation of the raw frames;
 * copy codes and scales bit-exact against the e4m3 quantisation of the bf16 (f32) copies the
   bf16 / f32 append writes for the same source (those copies are pinned against float64 in
   tests/test_gpu_rope.py and tests/test_gpu_prope.py);
-* attention bit-identical to the bf16 kernel over bf16 pools holding the decoded values
-  bf16(code x scale), in the same launch shape (split or not): the fp8 instances stage each tile
-  to those values and run the same products;
-* attention against the oracle's float64 RoPE (and PRoPE) path run on the effective inputs of
-  the decoded copies (``fp8_rope_copy_effective``, ``prope_ref.fp8_prope_copies_effective``,
-  pinned in tests/test_oracle.py): what remains is bf16 arithmetic, measured on the same data by
-  the bf16 kernel over the decoded pools (error divided by each channel's V RMS; K/V carry 1% x20
-  outlier channels, whose sharper logits put it above the N(0,1) bars of tests/helpers.py).
+* fp8-MFMA attention against ``fp8_rope_attention`` (the per-key-frame e4m3 query of the
+  kernel's contract, reproduced code for code, over the decoded copy; float64 softmax; pinned in
+  tests/test_oracle.py) with the normalised bars of the post-RoPE fp8 kernel (tests/helpers.py),
+  and on N(0,1) data against the float64 RoPE oracle with the north-star fp8 bars;
+* bf16-decode attention (frames under 64 tokens) bit-identical to the bf16 kernel over bf16
+  pools holding the decoded values bf16(code x scale), in the same launch shape, and against the
+  oracle's float64 RoPE (and PRoPE) path run on the effective inputs of the decoded copies
+  (``fp8_rope_copy_effective``, ``prope_ref.fp8_prope_copies_effective``, pinned in
+  tests/test_oracle.py): what remains is bf16 arithmetic (error divided by each channel's V RMS;
+  K/V carry 1% x20 outlier channels, whose sharper logits put it above the N(0,1) bars).
 """
 
 import pytest
@@ -31,17 +35,19 @@ from solarwm_amd import (PropeConfig, RopeConfig, apply_cache_updates, attend_ca
                          stage_camera_cache)
 
 from .cameras import per_token, trajectory
-from .helpers import MAX_ABS, MEAN_ABS
+from .helpers import (FP8_MAX_ABS, FP8_MEAN_ABS, FP8_NORM_MAX, FP8_NORM_MEAN, MAX_ABS, MEAN_ABS,
+                      assert_attn_close)
 
 pytestmark = pytest.mark.gpu
 
-# Normalised error (divided by each channel's V RMS) of bf16 attention over the decoded fp8
-# frames against the float64 oracle, on K/V with x20 outlier channels.  The kernel rounds the
-# query to bf16 after turning its temporal pairs per key frame, the oracle rounds the turned key
-# instead; on an outlier key channel that rounding moves a logit by up to ~0.03, so the largest
-# output errors reach ~0.06 while the mean stays at the bf16 level.  The bf16 kernel over the
-# same decoded pools measures the same errors (its outputs are bit-identical, checked below).  A
-# frame decoded with another frame's scale (1.25x or 2x) measures 0.3-4.5 (tests/helpers.py).
+# Normalised error (divided by each channel's V RMS) of the bf16-decode kernel (frames under 64
+# tokens) over the decoded fp8 frames against the float64 oracle, on K/V with x20 outlier
+# channels.  The kernel rounds the query to bf16 after turning its temporal pairs per key frame,
+# the oracle rounds the turned key instead; on an outlier key channel that rounding moves a logit
+# by up to ~0.03, so the largest output errors reach ~0.06 while the mean stays at the bf16
+# level.  The bf16 kernel over the same decoded pools measures the same errors (its outputs are
+# bit-identical, checked below).  A frame decoded with another frame's scale (1.25x or 2x)
+# measures 0.3-4.5 (tests/helpers.py).
 FP8_BF16_MAX, FP8_BF16_MEAN = 0.1, 2e-3
 
 BF = torch.bfloat16
@@ -127,10 +133,24 @@ def test_fp8_append_copies(gpu, B, H, gh, gw, src, prope):
     assert float(krs[0].max()) == 7.0
 
 
+def _rope_pools(k, v, B, H, gh, gw, n, slots, gpu):
+    T = gh * gw
+    hw = rope.spatial_table(RopeConfig(grid_hw=(gh, gw)), gpu)
+    kp, vp, ks8, vs8 = kernels.new_pools(n + 2, B, H, T, F8, gpu)
+    krp, krs = torch.zeros_like(kp), torch.zeros_like(ks8)
+    kd, vd = k.to(gpu), v.to(gpu)
+    for j in range(n):
+        kernels.append_frames(kd, vd, kp, vp, [slots[j]], frame_tokens=T, src_frame0=j,
+                              kscale=ks8, vscale=vs8, kr_pool=krp, rope_hw=hw, grid_hw=(gh, gw),
+                              kr_scale=krs)
+    return hw, krp, krs, vp, vs8
+
+
 @pytest.mark.parametrize("B,H,gh,gw,kpos,qpos,split", [
     (1, 2, 8, 8, [0, 4, 5, 6, 7], [6, 7], False),
     (2, 3, 10, 10, [0, 1, 2, 3, 4, 5], [3, 4, 5], False),
     (1, 2, 30, 52, [0, 1, 2, 3, 4, 5], [5], True),  # one frame of queries: the balanced split
+    (1, 2, 4, 8, [0, 2, 3, 4, 5, 6], [5, 6], False),  # 32-token frames: the bf16-decode kernel
 ])
 def test_fp8_attention_rope_vs_oracle(gpu, B, H, gh, gw, kpos, qpos, split):
     T = gh * gw
@@ -140,46 +160,68 @@ def test_fp8_attention_rope_vs_oracle(gpu, B, H, gh, gw, kpos, qpos, split):
     q = torch.randn((B, nq * T, H, 128), generator=g).to(BF)
     k, v = _outlier((B, n * T, H, 128), 13), _outlier((B, n * T, H, 128), 14)
     f = ref.wan_rope_freqs()
-    k_eff = ref.fp8_rope_copy_effective(k, (gh, gw), f, T)
     v_eff = ref.fp8_fake_quant_frames(v.float(), T).double()
-    want = ref.attention(ref.rope_frames(q, (gh, gw), qpos, f),
-                         ref.rope_frames(k_eff, (gh, gw), kpos, f), v_eff)
-    cfg = RopeConfig(grid_hw=(gh, gw))
-    hw = rope.spatial_table(cfg, gpu)
+    if T >= 64:  # the fp8-MFMA kernel's own quantised query over the decoded copy
+        want = ref.fp8_rope_attention(q, ref.fp8_rope_copy_decoded(k, (gh, gw), f, T), v_eff,
+                                      (gh, gw), qpos, kpos, T)
+        bar_max, bar_mean = FP8_NORM_MAX, FP8_NORM_MEAN
+    else:
+        k_eff = ref.fp8_rope_copy_effective(k, (gh, gw), f, T)
+        want = ref.attention(ref.rope_frames(q, (gh, gw), qpos, f),
+                             ref.rope_frames(k_eff, (gh, gw), kpos, f), v_eff)
+        bar_max, bar_mean = FP8_BF16_MAX, FP8_BF16_MEAN
     slots = torch.randperm(n + 2, generator=g)[:n].tolist()
-    kp, vp, ks8, vs8 = kernels.new_pools(n + 2, B, H, T, F8, gpu)
-    krp, krs = torch.zeros_like(kp), torch.zeros_like(ks8)
-    kd, vd = k.to(gpu), v.to(gpu)
-    for j in range(n):
-        kernels.append_frames(kd, vd, kp, vp, [slots[j]], frame_tokens=T, src_frame0=j,
-                              kscale=ks8, vscale=vs8, kr_pool=krp, rope_hw=hw, grid_hw=(gh, gw),
-                              kr_scale=krs)
+    hw, krp, krs, vp, vs8 = _rope_pools(k, v, B, H, gh, gw, n, slots, gpu)
     qd = q.to(gpu)
-    rt = (hw, (gh, gw), rope.temporal_table(qpos, kpos, cfg, gpu))
+    rt = (hw, (gh, gw), rope.temporal_table(qpos, kpos, RopeConfig(grid_hw=(gh, gw)), gpu))
     args = dict(frame_tokens=T, kscale=krs, vscale=vs8, rope=rt)
     plan = kernels.attention_plan(qd, krp, vp, slots, **args)
     assert (plan["split"] > 0) == split, plan
     outs = [kernels.attention_frames(qd, krp, vp, slots, **args)]
     if split:
         outs.append(kernels.attention_frames(qd, krp, vp, slots, use_workspace=False, **args))
-    # the bf16 kernel over bf16 pools holding the decoded values bf16(code x scale): the fp8
-    # instances stage each tile to exactly these values and run the same products
-    kdec = (krp.float() * krs[..., None, None]).to(BF)
-    vdec = (vp.float() * vs8[..., None, None]).to(BF)
-    refs = [kernels.attention_frames(qd, kdec, vdec, slots, frame_tokens=T, rope=rt,
-                                     use_workspace=ws) for ws in ((True, False) if split else (True,))]
+    refs = []
+    if T < 64:
+        # the bf16 kernel over bf16 pools holding the decoded values bf16(code x scale): the
+        # bf16-decode instances stage each tile to exactly these values and run the same products
+        kdec = (krp.float() * krs[..., None, None]).to(BF)
+        vdec = (vp.float() * vs8[..., None, None]).to(BF)
+        refs = [kernels.attention_frames(qd, kdec, vdec, slots, frame_tokens=T, rope=rt,
+                                         use_workspace=ws) for ws in ((True, False) if split else (True,))]
     torch.cuda.synchronize()
     rms_v = v_eff.pow(2).mean(dim=1, keepdim=True).sqrt()
-    for i, (out, ref_bf) in enumerate(zip(outs, refs)):
+    for i, out in enumerate(outs):
         assert out.dtype == BF and torch.isfinite(out).all()
         mode = "split" if split and i == 0 else "unsplit"
-        e_bf = (ref_bf.cpu().double() - want.double()).abs() / rms_v
         e = (out.cpu().double() - want.double()).abs() / rms_v
-        _say(f"  {mode}: bf16 kernel on decoded pools: normalised error max "
-             f"{float(e_bf.max()):.3e} mean {float(e_bf.mean()):.3e}; fp8 max {float(e.max()):.3e} "
-             f"mean {float(e.mean()):.3e}")
-        assert torch.equal(out, ref_bf), mode  # same launch shape, same arithmetic
-        assert float(e.max()) <= FP8_BF16_MAX and float(e.mean()) <= FP8_BF16_MEAN
+        _say(f"  {mode}: normalised error max {float(e.max()):.3e} mean {float(e.mean()):.3e}")
+        if refs:
+            assert torch.equal(out, refs[i]), mode  # same launch shape, same arithmetic
+        assert float(e.max()) <= bar_max and float(e.mean()) <= bar_mean
+
+
+@pytest.mark.parametrize("B,H,gh,gw,kpos,qpos", [
+    (1, 2, 30, 52, [0, 1, 2, 3, 4, 5], [5]),
+    (2, 3, 10, 10, [0, 1, 2, 3, 4, 5, 6, 7], [6, 7]),
+])
+def test_fp8_attention_rope_unit_scale_vs_bf16_oracle(gpu, B, H, gh, gw, kpos, qpos):
+    """N(0,1) Q/K/V: RoPE on load over an fp8 cache meets the north-star fp8 bar against the
+    float64 RoPE oracle over the bf16 inputs (query, key and probability roundings included)."""
+    T = gh * gw
+    n, nq = len(kpos), len(qpos)
+    _say("fp8 attention rope unit scale", B, H, gh, gw, kpos, qpos)
+    g = torch.Generator().manual_seed(15)
+    q, k, v = (torch.randn((B, L * T, H, 128), generator=g).to(BF) for L in (nq, n, n))
+    f = ref.wan_rope_freqs()
+    want = ref.attention(ref.rope_frames(q, (gh, gw), qpos, f), ref.rope_frames(k, (gh, gw), kpos, f),
+                         v, compute_dtype=torch.float32)
+    slots = list(range(n))
+    hw, krp, krs, vp, vs8 = _rope_pools(k, v, B, H, gh, gw, n, slots, gpu)
+    rt = (hw, (gh, gw), rope.temporal_table(qpos, kpos, RopeConfig(grid_hw=(gh, gw)), gpu))
+    out = kernels.attention_frames(q.to(gpu), krp, vp, slots, frame_tokens=T, kscale=krs,
+                                   vscale=vs8, rope=rt)
+    torch.cuda.synchronize()
+    assert_attn_close(out, want, FP8_MAX_ABS, FP8_MEAN_ABS)
 
 
 def _oracle_cache(B, cap, T, H, dtype):
@@ -195,8 +237,9 @@ def _oracle_cache(B, cap, T, H, dtype):
 ])
 def test_fp8_rope_rollout_vs_oracle(gpu, sink, cap, gh, gw, nb, chunks, echo, rtf, B, H):
     """Pre-RoPE fp8 rollout (2 passes per chunk, commit on the second): every pass against the
-    oracle's window RoPE over the effective inputs of the decoded copies; the committed raw codes
-    and scales equal the oracle quantisation of the oracle's raw bf16 cache."""
+    oracle's window with the fp8-MFMA kernel's quantised query (``fp8_rope_attention`` at the
+    window's RoPE positions) over the decoded copies; the committed raw codes and scales equal
+    the oracle quantisation of the oracle's raw bf16 cache."""
     T = gh * gw
     _say("fp8 rollout rope", sink, cap, gh, gw, nb, chunks, echo, rtf, B, H)
     cfg = RopeConfig(grid_hw=(gh, gw), use_echorope=echo, rope_train_frames=rtf)
@@ -220,12 +263,13 @@ def test_fp8_rope_rollout_vs_oracle(gpu, sink, cap, gh, gw, nb, chunks, echo, rt
             args = dict(current_start=start, frame_seqlen=T, sink_size=sink, local_attn_size=cap)
             seen = {}
 
-            def keep_v(qq, kk, vv):
+            def attend(qq, kk, vv, qp, kp):  # the window's copy: spatial pairs turned, temporal raw
                 seen["v"] = vv
-                return ref.attention(qq, kk, vv)
+                kc = ref.rope_frames(kk, (gh, gw), [0] * (kk.shape[1] // T), f)
+                return ref.fp8_rope_attention(qq, kc, vv, (gh, gw), qp, kp, T)
 
-            want, oinfo = ref.cached_self_attention(q, k_eff, v_eff, o_eff, rope=orope,
-                                                    attn_fn=keep_v, **args)
+            want, oinfo = ref.cached_self_attention(q, k_eff, v_eff, o_eff,
+                                                    rope=dict(orope, attend=attend), **args)
             _, rinfo = ref.cached_self_attention(q, k, v, o_raw, attn_fn=lambda *a: torch.zeros(0),
                                                  **args)
             torch.cuda.synchronize()
@@ -234,7 +278,7 @@ def test_fp8_rope_rollout_vs_oracle(gpu, sink, cap, gh, gw, nb, chunks, echo, rt
             _say(f"  chunk {c} commit {commit}: normalised max {float(e.max()):.3e} "
                  f"mean {float(e.mean()):.3e}")
             assert torch.isfinite(x).all()
-            assert float(e.max()) <= FP8_BF16_MAX and float(e.mean()) <= FP8_BF16_MEAN
+            assert float(e.max()) <= FP8_NORM_MAX and float(e.mean()) <= FP8_NORM_MEAN
             if commit:
                 apply_cache_updates([cache], [(0, info)])
                 ref.apply_cache_updates([o_eff], [(0, oinfo)])

@@ -5,9 +5,10 @@ of the window at caller-given temporal positions (``attend_cached(memory_frames=
 memory_positions=...)``), as the H3 memory path places bank rows ahead of the history at their
 own positions (memory_kv_attention.py:97-137).  Oracle: ``cached_self_attention(rope=...,
 memory_k=..., memory_positions=...)`` (pinned in tests/test_oracle.py).  bf16 caches: the bf16
-bars of tests/helpers.py; fp8 caches: the oracle runs on the effective inputs of the decoded
-copies and the error divided by each channel's V RMS stays within the bars of
-tests/test_gpu_fp8_rope.py.
+bars of tests/helpers.py; fp8 caches (64-token frames: the fp8-MFMA kernel): the oracle attends
+with that kernel's per-key-frame e4m3 query (``fp8_rope_attention`` at the positions the window
+RoPE would use) over the decoded copies, and the error divided by each channel's V RMS stays
+within the normalised fp8 bars of tests/helpers.py.
 """
 
 import pytest
@@ -16,8 +17,7 @@ import torch
 from oracle import wan_cache_ref as ref
 from solarwm_amd import RopeConfig, apply_cache_updates, attend_cached, make_kv_cache_allocator
 
-from .helpers import assert_attn_close
-from .test_gpu_fp8_rope import FP8_BF16_MAX, FP8_BF16_MEAN
+from .helpers import FP8_NORM_MAX, FP8_NORM_MEAN, assert_attn_close
 
 pytestmark = pytest.mark.gpu
 
@@ -62,15 +62,21 @@ def test_rope_cache_memory_frames_vs_oracle(gpu, dtype, sink, echo, B):
             if idx is not None:
                 mem = dict(memory_k=ref.memory_gather(bank_k_o, idx, T),
                            memory_v=ref.memory_gather(bank_v_o, idx, T), memory_positions=mpos)
+            rp = orope
+            if fp8:
+                def attend(qq, kk, vv, qp, kp):  # the copies: spatial pairs turned, temporal raw
+                    kc = ref.rope_frames(kk, (gh, gw), [0] * (kk.shape[1] // T), f)
+                    return ref.fp8_rope_attention(qq, kc, vv, (gh, gw), qp, kp, T)
+                rp = dict(orope, attend=attend)
             want, oinfo = ref.cached_self_attention(
                 q, ko, vo, oc, current_start=c * nb * T, frame_seqlen=T, sink_size=sink,
-                local_attn_size=cap, rope=orope, **mem)
+                local_attn_size=cap, rope=rp, **mem)
             torch.cuda.synchronize()
             if fp8:
                 vw = torch.cat([mem["memory_v"], vo], 1) if idx is not None else vo
                 rms_v = vw.double().pow(2).mean(dim=1, keepdim=True).sqrt()
                 e = (x.cpu().double() - want.double()).abs() / rms_v
-                assert float(e.max()) <= FP8_BF16_MAX and float(e.mean()) <= FP8_BF16_MEAN, (
+                assert float(e.max()) <= FP8_NORM_MAX and float(e.mean()) <= FP8_NORM_MEAN, (
                     c, commit, float(e.max()), float(e.mean()))
             else:
                 assert_attn_close(x, want)

@@ -725,3 +725,132 @@ def test_memory_frames_with_rope_pin():
         ref.cached_self_attention(q, k, v, cache, current_start=2 * T, frame_seqlen=T,
                                   sink_size=0, local_attn_size=3, rope=orope, memory_k=mk,
                                   memory_v=mv, memory_positions=[1])
+
+
+# --- fp8 RoPE on load: the per-key-frame quantised query ---------------------------------------
+def _turned_query_f64(q, grid, qpos, kpos, T):
+    """float64 [n_k, B, L, H, D]: bf16 q with its height/width pairs turned at the token's (h, w)
+    and its temporal pairs by (p_q - p_k) * w_i, from math.cos / math.sin of the textbook
+    angles (no shared code with the oracle's tables)."""
+    gh, gw = grid
+    B, L, H, D = q.shape
+    x = q.to(torch.bfloat16).double().reshape(B, L, H, D // 2, 2)
+    out = []
+    for pk in kpos:
+        ang = torch.zeros(L, D // 2, dtype=torch.float64)
+        for r in range(L):
+            f, t = divmod(r, T)
+            h, w = divmod(t, gw)
+            for i in range(22):
+                ang[r, i] = (qpos[f] - pk) * 10000.0 ** (-2 * i / 44)
+            for j in range(21):
+                ang[r, 22 + j] = h * 10000.0 ** (-2 * j / 42)
+                ang[r, 43 + j] = w * 10000.0 ** (-2 * j / 42)
+        c = ang.cos()[None, :, None, :]
+        s = ang.sin()[None, :, None, :]
+        u, v = x[..., 0], x[..., 1]
+        out.append(torch.stack([u * c - v * s, u * s + v * c], -1).reshape(B, L, H, D))
+    return torch.stack(out)
+
+
+def test_fp8_rope_query_frames_error_bound():
+    """Every decoded query value lies within the e4m3 + bf16 rounding bound of the float64 turned
+    query (so its logits against any key stay within sum_c bound_c |k_c|), for rows with a planted
+    temporal pair whose turns exceed every component (a scale from the component absmax would
+    clip them) and a planted spatial outlier; a reversed temporal angle breaks the bound."""
+    T, grid, qpos, kpos = 16, (4, 4), [5, 6], [0, 3, 4, 5, 6]
+    g = torch.Generator().manual_seed(91)
+    q = torch.randn(1, 2 * T, 2, 128, generator=g) * 2
+    q[0, 3, 0] *= 0.05
+    q[0, 3, 0, 0], q[0, 3, 0, 1] = 40.0, 40.0  # pair 0: norm 56.6, components 40
+    q[0, 9, 1, 100] = 60.0  # a spatial outlier
+    q = q.to(torch.bfloat16)
+    got = ref.fp8_rope_query_frames(q, grid, qpos, kpos, T).double()
+    exact = _turned_query_f64(q, grid, qpos, kpos, T)
+    xp = exact.reshape(*exact.shape[:-1], 64, 2)
+    bound_row = torch.maximum(xp[..., :22, :].pow(2).sum(-1).sqrt().amax(-1),
+                              xp[..., 22:, :].abs().amax((-2, -1)))
+    scale = (bound_row.amax(0) / 448.0)[None, ..., None]  # the row's scale (frame independent)
+    lim = exact.abs() * (2.0 ** -8 + 2.0 ** -4 * (1 + 2.0 ** -8)) + scale * 2.0 ** -10 + 1e-12
+    assert bool(((got - exact).abs() <= lim).all())
+    # the planted pair turns past its components for some key frame: clipping would show there
+    assert float(exact[:, 0, 3, 0, :2].abs().max()) > 45.0
+    # the same bound fails for the opposite temporal angle
+    flipped = _turned_query_f64(q, grid, qpos, [2 * qpos[0] - p for p in kpos], T)
+    assert not bool(((got[:, :, :T] - flipped[:, :, :T]).abs() <= lim[:, :, :T]).all())
+    # logits against the RoPE copy equal RoPE at p_q and p_k up to the same bound
+    k = torch.randn(1, len(kpos) * T, 2, 128, generator=g, dtype=torch.float64)
+    f = ref.wan_rope_freqs()
+    kc = ref.rope_frames(k, grid, [0] * len(kpos), f).reshape(1, len(kpos), T, 2, 128)
+    lg = torch.einsum("jblhd,bjthd->bhljt", got, kc)
+    want = torch.einsum("blhd,bkhd->bhlk", ref.rope_frames(q.double(), grid, qpos, f),
+                        ref.rope_frames(k, grid, kpos, f)).reshape(lg.shape)
+    lg_lim = torch.einsum("jblhd,bjthd->bhljt", lim, kc.abs())
+    assert bool(((lg - want).abs() <= lg_lim + 1e-9).all())
+
+
+def test_fp8_rope_query_frames_zero_angles_reduce_to_row_quantisation():
+    """One-token frames at equal query/key positions turn nothing; with zero temporal channels
+    the row bound is the absmax and the codes are fp8_fake_quant_rows' (pinned on fp8_quantize)."""
+    g = torch.Generator().manual_seed(92)
+    q = torch.randn(1, 3, 2, 128, generator=g) * 5
+    q[..., :44] = 0
+    q = q.to(torch.bfloat16)
+    got = ref.fp8_rope_query_frames(q, (1, 1), [4, 5, 6], [4, 5, 6], 1)
+    want = ref.fp8_fake_quant_rows(q)
+    for j in range(3):  # frame j's own rows meet key frame j at angle 0
+        assert torch.equal(got[j, :, j], want[:, j])
+
+
+def test_fp8_rope_attention_pins():
+    """Zero keys give the mean of V over the window; against float64 RoPE attention the output
+    moves only by the query's e4m3 rounding (values paired with the wrong key frame fail)."""
+    T, grid, qpos, kpos = 16, (4, 4), [4, 5], [0, 2, 3, 4, 5]
+    g = torch.Generator().manual_seed(93)
+    q = torch.randn(1, 2 * T, 2, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 5 * T, 2, 128, generator=g, dtype=torch.float64)
+    v = torch.randn(1, 5 * T, 2, 128, generator=g, dtype=torch.float64)
+    x0 = ref.fp8_rope_attention(q, torch.zeros_like(k), v, grid, qpos, kpos, T)
+    assert float((x0 - v.mean(dim=1, keepdim=True)).abs().max()) < 1e-12
+    f = ref.wan_rope_freqs()
+    kc = ref.rope_frames(k, grid, [0] * 5, f)
+    got = ref.fp8_rope_attention(q, kc, v, grid, qpos, kpos, T)
+    want = ref.attention(ref.rope_frames(q.double(), grid, qpos, f), ref.rope_frames(k, grid, kpos, f),
+                         v, round_inputs_to_bf16=False)
+    err = (got - want).abs()
+    assert float(err.max()) < 0.05 and float(err.mean()) < 5e-3
+    vs = v.reshape(1, 5, T, 2, 128).roll(1, dims=1).reshape(v.shape)  # V of the wrong frames
+    bad = ref.fp8_rope_attention(q, kc, vs, grid, qpos, kpos, T)
+    assert float((bad - want).abs().mean()) > 10 * float(err.mean())
+
+
+def test_cached_attention_rope_attend_hook():
+    """rope['attend'] receives the raw query and window and the frame positions; an attend that
+    rotates at those positions reproduces the built-in RoPE path exactly (sink and no-sink
+    windows, memory frames ahead of the window)."""
+    T, grid, H = 12, (3, 4), 2
+    f = ref.wan_rope_freqs()
+
+    def attend(q, k, v, qp, kp):
+        return ref.attention(ref.rope_frames(q, grid, qp, f), ref.rope_frames(k, grid, kp, f), v)
+
+    for sink, cap, echo in ((1, 5, True), (0, 4, True), (1, 5, False)):
+        g = torch.Generator().manual_seed(94 + sink + cap)
+        rope = {"freqs": f, "grid_hw": grid, "use_echorope": echo, "rope_train_frames": None}
+        c1 = ref.allocate_kv_cache(1, 1, cap * T, H, 128, torch.float32)[0]
+        c2 = ref.allocate_kv_cache(1, 1, cap * T, H, 128, torch.float32)[0]
+        for chunk in range(4):
+            q, k, v = (torch.randn(1, 2 * T, H, 128, generator=g) for _ in range(3))
+            kw = dict(current_start=chunk * 2 * T, frame_seqlen=T, sink_size=sink, local_attn_size=cap)
+            x1, u1 = ref.cached_self_attention(q, k, v, c1, rope=rope, **kw)
+            x2, u2 = ref.cached_self_attention(q, k, v, c2, rope=dict(rope, attend=attend), **kw)
+            assert torch.equal(x1, x2)
+            ref.apply_cache_updates([c1], [(0, u1)])
+            ref.apply_cache_updates([c2], [(0, u2)])
+        mk, mv = (torch.randn(1, 2 * T, H, 128, generator=g) for _ in range(2))
+        q, k, v = (torch.randn(1, 2 * T, H, 128, generator=g) for _ in range(3))
+        kw = dict(current_start=8 * T, frame_seqlen=T, sink_size=sink, local_attn_size=cap,
+                  memory_k=mk, memory_v=mv, memory_positions=[9, 2])
+        x1, _ = ref.cached_self_attention(q, k, v, c1, rope=rope, **kw)
+        x2, _ = ref.cached_self_attention(q, k, v, c2, rope=dict(rope, attend=attend), **kw)
+        assert torch.equal(x1, x2)
