@@ -268,7 +268,12 @@ int skv_append_workspace_size(const skv_append_desc* desc, int64_t* bytes);
  * plus the RMSNorm of Q at load (q_inv_rms[b * q_rms_stride_b + row] * q_norm_weight[h *
  * head_dim + c], fp32, before RoPE/PRoPE; the fp8-pool kernel rounds the normalised Q to bf16
  * before quantising it, as the reference's bf16 norm output).  Optional members NULL / 0.
- * rope_t selects RoPE on load, q_xform_t (with q_xform_s, out_xform) RoPE + PRoPE.
+ * rope_t selects RoPE on load, q_xform_t (with q_xform_s, out_xform) RoPE + PRoPE.  On fp8
+ * pools with frames of at least 64 tokens RoPE on load multiplies e4m3 codes: each query row
+ * is rounded to bf16, its height/width pairs turned and rounded to bf16, and for every key frame
+ * its temporal pairs turned by rope_t and rounded to bf16, then quantised with one row scale
+ * max(|turned height/width values|, temporal pair norms) / 448 (no code clips); shorter frames
+ * and PRoPE decode the fp8 tiles to bf16 and multiply in bf16.
  * frame_lens (mask NONE only) lets frames hold fewer than frame_tokens keys, so a window can
  * mix whole frames with spans of other lengths (the H3 prefix rows, memory_kv_attention.py).
  * Segments (n_segments > 0, up to SKV_MAX_SEGMENTS; bf16 pools, bf16 or f32 queries, mask NONE,
