@@ -1521,7 +1521,10 @@ def main():
             aux[name] = {"frames_per_s": round(r["frames_per_s"], 4),
                          "attn_tflops": round(r["attn_tflops"], 1),
                          "attn_avg_ms": round(r["attn_avg_ms"], 4),
-                         "attn_frac_bf16_peak": round(r["attn_tflops"] / BF16_PEAK_TFLOPS, 4),
+                         # c5_rope multiplies e4m3 codes (fp8 peak); c5_prope bf16 (bf16 peak)
+                         ("attn_frac_fp8_peak" if name == "c5_rope" else "attn_frac_bf16_peak"):
+                             round(r["attn_tflops"] / (FP8_PEAK_TFLOPS if name == "c5_rope"
+                                                      else BF16_PEAK_TFLOPS), 4),
                          "append_avg_us": round(r["append_avg_us"], 2),
                          "workload": r["workload"],
                          "note": notes[name]}
