@@ -44,11 +44,12 @@ pytestmark = pytest.mark.gpu
 # tokens) over the decoded fp8 frames against the float64 oracle, on K/V with x20 outlier
 # channels.  The kernel rounds the query to bf16 after turning its temporal pairs per key frame,
 # the oracle rounds the turned key instead; on an outlier key channel that rounding moves a logit
-# by up to ~0.03, so the largest output errors reach ~0.06 while the mean stays at the bf16
-# level.  The bf16 kernel over the same decoded pools measures the same errors (its outputs are
+# by up to ~0.03, so the largest output errors reach ~0.06-0.08 while the mean stays at the bf16
+# level (1.1e-3 to 2.2e-3 over these tests and the random shapes of test_gpu_random_rope.py).
+# The bf16 kernel over the same decoded pools measures the same errors (its outputs are
 # bit-identical, checked below).  A frame decoded with another frame's scale (1.25x or 2x)
 # measures 0.3-4.5 (tests/helpers.py).
-FP8_BF16_MAX, FP8_BF16_MEAN = 0.1, 2e-3
+FP8_BF16_MAX, FP8_BF16_MEAN = 0.1, 3e-3
 
 BF = torch.bfloat16
 F8 = torch.float8_e4m3fn
