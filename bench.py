@@ -46,6 +46,7 @@ C4 = dict(workload="33b-class memory path", layers=48, heads=40, T=1560, chunk_f
 PASSES = ["none"] * 4 + ["commit"]  # stage2.py:683-760: NFE4 then a t=0 commit forward
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
+CPU_PASSES = 5  # timed CPU baseline layer passes per thread count (after one warm-up pass)
 HBM_PEAK_GBPS = 8000.0
 # HBM bytes per steady-state attention launch (Lq 4680 x Lk 32760, H12) measured with rocprofv3
 # on `bench.py --probe`: FETCH_SIZE x2.0 (337.45 MB) + WRITE_SIZE x1.0 (14.38 MB); the scale
@@ -392,7 +393,8 @@ def cpu_baseline(cfg):
     reference's fallback, attention.py:172-188): one steady-state C2 layer pass (rolling eviction
     over a full cache), extrapolated to frames/s of the 30-layer, 5-pass chunk.  Timed with the
     thread count torch starts with (the box's CPU share, OMP_NUM_THREADS) and with os.cpu_count()
-    threads; the faster is reported."""
+    threads, each after one untimed warm-up pass, as the median of CPU_PASSES timed passes; the
+    faster thread count is reported."""
     import torch
 
     from oracle import wan_cache_ref as ref
@@ -408,15 +410,20 @@ def cpu_baseline(cfg):
     q, k, v = (torch.randn(cfg["batch"], Lq, H, 128, generator=g).bfloat16() for _ in range(3))
     avail, total = _host_cores()
     start_threads = torch.get_num_threads()
-    times = {}
+    times, samples = {}, {}
     for threads in sorted({start_threads, total}):
         torch.set_num_threads(threads)
-        t0 = time.perf_counter()
-        ref.cached_self_attention(
-            q, k, v, cache[0], current_start=cap, frame_seqlen=T, sink_size=cfg["sink_f"],
-            local_attn_size=cfg["cap_f"], attn_fn=ref.sdpa_fallback_attention,
-        )
-        times[threads] = time.perf_counter() - t0
+        runs = []
+        for i in range(CPU_PASSES + 1):  # the first pass warms the allocator and the thread pool
+            t0 = time.perf_counter()
+            ref.cached_self_attention(
+                q, k, v, cache[0], current_start=cap, frame_seqlen=T, sink_size=cfg["sink_f"],
+                local_attn_size=cfg["cap_f"], attn_fn=ref.sdpa_fallback_attention,
+            )
+            if i:
+                runs.append(time.perf_counter() - t0)
+        samples[threads] = runs
+        times[threads] = sorted(runs)[len(runs) // 2]
     torch.set_num_threads(start_threads)
     best = min(times, key=times.get)
     dt = times[best]
@@ -427,11 +434,12 @@ def cpu_baseline(cfg):
         "cores": best,
         "kind": "port",
         "sample": (
-            f"1 steady-state layer pass (Lq={Lq}, Lk={cap}, H={H}, rolling eviction) of the "
-            f"reference op sequence in {dt:.2f} s with {best} threads, x{cfg['layers']} layers "
-            f"x{len(PASSES)} passes"
+            f"steady-state layer passes (Lq={Lq}, Lk={cap}, H={H}, rolling eviction) of the "
+            f"reference op sequence: median {dt:.2f} s of {CPU_PASSES} timed passes after a "
+            f"warm-up, {best} threads, x{cfg['layers']} layers x{len(PASSES)} passes"
         ),
         "seconds_by_threads": {str(t): round(x, 3) for t, x in times.items()},
+        "passes_by_threads": {str(t): [round(x, 3) for x in r] for t, r in samples.items()},
         "host_cpu_count": total,
         "host_cores_available": avail,
     }
