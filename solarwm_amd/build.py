@@ -3,6 +3,11 @@
 The library is compiled from ``solarwm_amd/csrc`` into ``solarwm_amd/libsolarkv.so``; nothing is
 JIT-compiled at import time, so the built file travels with the source tree to the GPU host.
 Usage: ``python -m solarwm_amd.build`` (also called by ``__graft_entry__.build()``).
+
+Every translation unit that issues matrix-core products is also compiled to device assembly
+(``--cuda-device-only -S``, side by side with the objects) and checked by ``isa_check``: a
+library in which any path reads an MFMA result before its wait states have elapsed is not
+linked.
 """
 
 from __future__ import annotations
@@ -47,25 +52,41 @@ def sources() -> list[Path]:
 
 def build(verbose: bool = False) -> Path:
     """Compile every source under csrc/ and link libsolarkv.so; returns its path."""
+    from . import isa_check
+
     hipcc = _hipcc()
     with tempfile.TemporaryDirectory(prefix="skv_build_") as tmp:
-        # the translation units compile side by side (one hipcc process each)
-        jobs = []
+        # the translation units compile side by side (one hipcc process each), and so do the
+        # device listings of those with MFMAs
+        jobs, listings = [], []
         for src in sources():
             obj = Path(tmp) / (src.stem + ".o")
-            cmd = [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
-            if verbose:
-                print(" ".join(cmd), flush=True)
-            jobs.append((src, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
-                                                    stderr=subprocess.PIPE, text=True)))
+            cmds = [(obj, [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])]
+            if src.suffix == ".hip" and "__builtin_amdgcn_mfma" in src.read_text():
+                asm = Path(tmp) / (src.stem + ".s")
+                cmds.append((asm, [hipcc, *HIP_FLAGS, "--cuda-device-only", "-S", str(src), "-o", str(asm)]))
+                listings.append(asm)
+            for out_path, cmd in cmds:
+                if verbose:
+                    print(" ".join(cmd), flush=True)
+                jobs.append((src, out_path, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                             stderr=subprocess.PIPE, text=True)))
         objs, failed = [], []
-        for src, obj, proc in jobs:
+        for src, out_path, proc in jobs:
             out, err = proc.communicate()
             if proc.returncode != 0:
                 failed.append(f"hipcc failed on {src.name}:\n{out}\n{err}")
-            objs.append(str(obj))
+            if out_path.suffix == ".o":
+                objs.append(str(out_path))
         if failed:
             raise RuntimeError("\n".join(failed))
+        short = []
+        for asm in listings:
+            for name, paths in isa_check.check_listing(asm.read_text()).items():
+                short += [f"{asm.stem}: {name}: {p}" for p in paths]
+        if short:
+            raise RuntimeError("MFMA results read before their wait states (not linked):\n" +
+                               "\n".join(short))
         tmp_lib = Path(tmp) / LIB_PATH.name
         cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp_lib)]
         res = subprocess.run(cmd, capture_output=True, text=True)

@@ -1822,6 +1822,13 @@ void attn_fp8_kernel(AttnArgs a) {
   // PV(ntau-1): V(ntau-1) was loaded by step ntau-2 (the prologue when ntau = 1), two steps or
   // a barrier earlier
   auto epilogue = [&](const f32x16 (&s_last)[2], i32x8& pprev) __attribute__((always_inline)) {
+    // The last row-sum product (8 passes) was issued at the end of the step just before, and a
+    // VALU read of its result must trail it by 12 wait states.  When the step skips its mask
+    // block, the branch around that block can put settle's first read of tsum 2 issue slots
+    // after the product (hipcc's own hazard pass has been seen to leave that path short, so a
+    // lane read the previous tile's sum, skipped the rare path and summed NaN probabilities).
+    // The wait is spelled out here, tied to tsum so that no read of it moves above it.
+    asm volatile("s_nop 7\n\ts_nop 4" : "+v"(tsum));
     settle(s_last, pprev);
     const char* vl = vb_lds(ntau - 1) + lane16;
 #pragma unroll

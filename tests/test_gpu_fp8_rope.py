@@ -201,6 +201,47 @@ def test_fp8_attention_rope_vs_oracle(gpu, B, H, gh, gw, kpos, qpos, split):
         assert float(e.max()) <= bar_max and float(e.mean()) <= bar_mean
 
 
+def test_fp8_rope_split_segment_ending_on_its_largest_logit(gpu):
+    """Regression: balanced-split segments whose last key tile holds their rows' largest logit.
+
+    With these inputs (N(0,1), one frame of queries over 6 key frames, 256 workgroups over 14
+    q-tiles x 150 tiles) the segment of workgroup 211 covers tiles 80..88 of (head 1, q-tile 4)
+    and row 36 of that q-tile meets its largest logit (log2 units 7.7 against 2.4 before) in
+    tile 88.  Its probabilities then overflow e4m3 and the row-sum product turns NaN, which must
+    send the wave to the rare path before the last PV product.  The read of that row sum once
+    came 2 issue slots after the product on the path that skips the mask block (too early for an
+    8-pass product), so the wave kept the previous tile's sum and rows 36 and 52 (which share the
+    row-sum product's column) came out NaN.  Every row of the split and unsplit launches is
+    checked against the quantisation-exact oracle."""
+    B, H, gh, gw, kpos, qpos = 1, 2, 30, 52, [0, 1, 2, 3, 4, 5], [5]
+    T, n = gh * gw, len(kpos)
+    _say("fp8 rope split, segment ending on its largest logit")
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn((B, T, H, 128), generator=g).to(BF)
+    k = torch.randn((B, n * T, H, 128), generator=g).to(BF)
+    v = torch.randn((B, n * T, H, 128), generator=g).to(BF)
+    f = ref.wan_rope_freqs()
+    v_eff = ref.fp8_fake_quant_frames(v.float(), T).double()
+    want = ref.fp8_rope_attention(q, ref.fp8_rope_copy_decoded(k, (gh, gw), f, T), v_eff,
+                                  (gh, gw), qpos, kpos, T)
+    slots = list(range(n))
+    hw, krp, krs, vp, vs8 = _rope_pools(k, v, B, H, gh, gw, n, slots, gpu)
+    rt = (hw, (gh, gw), rope.temporal_table(qpos, kpos, RopeConfig(grid_hw=(gh, gw)), gpu))
+    args = dict(frame_tokens=T, kscale=krs, vscale=vs8, rope=rt)
+    plan = kernels.attention_plan(q.to(gpu), krp, vp, slots, **args)
+    assert plan["split"] > 0, plan
+    outs = [kernels.attention_frames(q.to(gpu), krp, vp, slots, use_workspace=ws, **args)
+            for ws in (True, False)]
+    torch.cuda.synchronize()
+    rms_v = v_eff.pow(2).mean(dim=1, keepdim=True).sqrt()
+    for mode, out in zip(("split", "unsplit"), outs):
+        assert torch.isfinite(out).all(), (mode, (~torch.isfinite(out)).nonzero()[:4].tolist())
+        e = (out.cpu().double() - want).abs() / rms_v
+        _say(f"  {mode}: normalised error max {float(e.max()):.3e} mean {float(e.mean()):.3e}; "
+             f"rows 1060, 1076 of head 1 max {float(e[0, [1060, 1076], 1].max()):.3e}")
+        assert float(e.max()) <= FP8_NORM_MAX and float(e.mean()) <= FP8_NORM_MEAN, mode
+
+
 @pytest.mark.parametrize("B,H,gh,gw,kpos,qpos", [
     (1, 2, 30, 52, [0, 1, 2, 3, 4, 5], [5]),
     (2, 3, 10, 10, [0, 1, 2, 3, 4, 5, 6, 7], [6, 7]),
