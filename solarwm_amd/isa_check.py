@@ -67,8 +67,8 @@ def functions(asm: str):
     lines = asm.split("\n")
     cur = None
     for i, line in enumerate(lines):
-        m = re.match(r"^(_Z\S+):\s*(;.*)?$", line)
-        if m:
+        m = re.match(r"^([^\s:;]+):\s*;\s*@(\S+)\s*$", line)  # "name: ; @name" opens a function
+        if m and m.group(1) == m.group(2):
             cur = (m.group(1), i)
         elif cur and line.startswith(".Lfunc_end"):
             yield cur[0], lines[cur[1] + 1:i]

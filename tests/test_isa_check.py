@@ -7,7 +7,7 @@ around the mask block straight to the block that compares the sum, one s_nop 0 i
 
 from solarwm_amd import isa_check
 
-HEAD = "_ZN3skv4testEv:                        ; @kernel\n"
+HEAD = "_ZN3skv4testEv:                        ; @_ZN3skv4testEv\n"
 TAIL = "\ts_endpgm\n.Lfunc_end0:\n"
 
 
@@ -105,3 +105,40 @@ def test_unknown_product_form_is_reported():
     body = "\tv_mfma_f32_4x4x4_16b_f16 v[0:3], v[4:5], v[6:7], 0\n"
     (paths,) = _check(body).values()
     assert "unknown" in paths[0].reader
+
+
+def test_real_listing_from_hipcc(tmp_path):
+    """The walk on hipcc's own -S output: a row-sum-shaped product whose result a VALU op reads
+    behind a branch.  hipcc's listing passes; with its s_nop lines deleted the read is short."""
+    import re
+    import shutil
+    import subprocess
+
+    import pytest
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not shutil.os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    src = tmp_path / "k.hip"
+    src.write_text(
+        "#include <hip/hip_runtime.h>\n"
+        "typedef int i32x8 __attribute__((ext_vector_type(8)));\n"
+        "typedef float f32x4 __attribute__((ext_vector_type(4)));\n"
+        'extern "C" __global__ void rowsum_branch(const int* p, float* out, int n) {\n'
+        "  i32x8 a, b;\n"
+        "  for (int i = 0; i < 8; ++i) { a[i] = p[threadIdx.x * 8 + i]; b[i] = p[512 + threadIdx.x * 8 + i]; }\n"
+        "  f32x4 c = {0.f, 0.f, 0.f, 0.f};\n"
+        "  f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);\n"
+        "  float x = 0.f;\n"
+        "  if (n > 3) x = out[threadIdx.x] * 2.f;\n"
+        "  out[threadIdx.x] = d[0] + x;\n"
+        "}\n")
+    asm = tmp_path / "k.s"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "--cuda-device-only", "-S", str(src),
+                    "-o", str(asm)], check=True, capture_output=True)
+    listing = asm.read_text()
+    assert [name for name, _ in isa_check.functions(listing)] == ["rowsum_branch"]
+    assert isa_check.check_listing(listing) == {}
+    stripped = re.sub(r"\n\ts_nop \d+", "", listing)
+    (paths,) = isa_check.check_listing(stripped).values()
+    assert any(p.needed == 12 and p.waited < 12 for p in paths), [str(p) for p in paths]
