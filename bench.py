@@ -36,6 +36,13 @@ CONFIGS = {
                sink_f=1, chunks=40, batch=1, cache="bf16", grid=(22, 40)),
     "c5": dict(workload="wan2.1-1.3b fp8-e4m3 kv, 4 streams", layers=30, heads=12, T=1560,
                chunk_f=3, cap_f=21, sink_f=1, chunks=27, batch=4, cache="fp8", grid=(30, 52)),
+    # the reference's shipped inference (configs/solar_wm/wan22_ti2v_5b/infer_stage2_sgf_81f.yaml:
+    # 16-27 with architectures/ti2v_5b.json): 30 layers, 24 heads, 405-token frames (grid 15 x 27),
+    # 3-frame chunks, 18-frame cache without a sink, window RoPE without EchoRoPE frozen at 21
+    # training frames, fused PRoPE with linear translations; 21 output frames = 7 chunks
+    "release": dict(workload="wan2.2-ti2v-5b release inference", layers=30, heads=24, T=405,
+                    chunk_f=3, cap_f=18, sink_f=0, chunks=7, batch=1, cache="bf16", grid=(15, 27),
+                    echorope=False, rope_train_frames=21, translation="linear"),
 }
 # grid: the latent patch grid of one frame (480x832 video -> 60x104 latent -> 2x2 patches; the
 # 5B model's 16x VAE: 704x1280 -> 44x80 -> 22x40), used by the pre-RoPE (RoPE on load) legs
@@ -90,18 +97,25 @@ def make_inputs(cfg, device, seed=1234, outliers=False):
     return out
 
 
+def _rope_config(cfg):
+    from solarwm_amd import RopeConfig
+
+    return RopeConfig(grid_hw=cfg["grid"], use_echorope=cfg.get("echorope", True),
+                      rope_train_frames=cfg.get("rope_train_frames"))
+
+
 def make_caches(cfg, device, rope=False, prope=False):
     import torch
 
-    from solarwm_amd import PropeConfig, RopeConfig, make_kv_cache_allocator
+    from solarwm_amd import PropeConfig, make_kv_cache_allocator
 
     alloc = make_kv_cache_allocator(
         num_layers=cfg["layers"], num_heads=cfg["heads"], head_dim=128,
         frame_sequence_length=cfg["T"], local_attn_size=cfg["cap_f"], sink_size=cfg["sink_f"],
         num_frame_per_block=cfg["chunk_f"],
         cache_dtype=torch.float8_e4m3fn if cfg["cache"] == "fp8" else None,
-        rope=RopeConfig(grid_hw=cfg["grid"]) if rope or prope else None,
-        prope=PropeConfig() if prope else None,
+        rope=_rope_config(cfg) if rope or prope else None,
+        prope=PropeConfig(camera_translation_transform=cfg.get("translation", "linear")) if prope else None,
     )
     return alloc(cfg["batch"], dtype=torch.bfloat16, device=device)
 
@@ -218,9 +232,11 @@ def _ref_rope_frames(x, grid, positions, freqs):
     gh, gw = grid
     B, L, n, D = x.shape
     F = len(positions)
+    if F == 0:  # an empty part of the window (no sink frames)
+        return x
     ct, ch, cw = 22, 21, 21
     ft, fh, fw = freqs.split([ct, ch, cw], dim=1)
-    pos = torch.tensor(list(positions), device=x.device)
+    pos = torch.tensor(list(positions), dtype=torch.long, device=x.device)
     f_all = torch.cat([ft[pos].view(F, 1, 1, ct).expand(F, gh, gw, ct),
                        fh[:gh].view(1, gh, 1, ch).expand(F, gh, gw, ch),
                        fw[:gw].view(1, 1, gw, cw).expand(F, gh, gw, cw)], dim=-1).reshape(L, 1, -1)
@@ -289,11 +305,10 @@ def reference_gpu_step(cfg, inputs, dense, chunk_ids, rope=False, cams=None):
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
-    from solarwm_amd import RopeConfig
     from solarwm_amd.rope import positions as rope_positions
 
     freqs = _ref_freqs(inputs[0][0].device) if rope else None
-    rcfg = RopeConfig(grid_hw=cfg["grid"]) if rope else None
+    rcfg = _rope_config(cfg) if rope else None
 
     T, Lq = cfg["T"], cfg["chunk_f"] * cfg["T"]
     sink = cfg["sink_f"] * T
@@ -738,16 +753,16 @@ def steady_state(name, device, fill=7, timed=3, rope=False, prope=False):
     return st
 
 
-def c2_rope(device, fill=7, timed=2, prope=False):
-    """Config 2 with a pre-RoPE cache, as the reference keeps it: ours (RoPE applied on load by
-    the kernels) against the reference op sequence that re-ropes the window in float64 every
-    pass, both over steady-state chunks.  ``prope``: the fused-PRoPE camera mode on top
-    (one camera per latent frame, a slow pan), against the reference's per-layer per-token
-    camera matrices and bf16 einsums."""
+def c2_rope(device, fill=7, timed=2, prope=False, name="c2"):
+    """Config 2 (or ``name``) with a pre-RoPE cache, as the reference keeps it: ours (RoPE
+    applied on load by the kernels) against the reference op sequence that re-ropes the window
+    in float64 every pass, both over steady-state chunks.  ``prope``: the fused-PRoPE camera
+    mode on top (one camera per latent frame, a slow pan), against the reference's per-layer
+    per-token camera matrices and bf16 einsums."""
     import torch
 
-    ours = steady_state("c2", device, fill=fill, timed=timed, rope=True, prope=prope)
-    cfg = CONFIGS["c2"]
+    ours = steady_state(name, device, fill=fill, timed=timed, rope=True, prope=prope)
+    cfg = CONFIGS[name]
     inputs = make_inputs(cfg, device)
     T = cfg["T"]
     # the reference's caches start full (global = local end = the 21-frame window), the state
@@ -1519,6 +1534,9 @@ def main():
         log(f"[bench] aux c2_rope: {aux['c2_rope']}")
         aux["c2_prope"] = c2_rope(dev, prope=True)
         log(f"[bench] aux c2_prope: {aux['c2_prope']}")
+        log("[bench] aux release: the reference's shipped inference geometry")
+        aux["release"] = c2_rope(dev, fill=6, timed=2, prope=True, name="release")
+        log(f"[bench] aux release: {aux['release']}")
         notes = {"c5_rope": "fp8 raw frames plus an fp8 RoPE copy of K; attn_fp8_kernel turns "
                             "the query's temporal pairs per key frame and multiplies e4m3 codes",
                  "c5_prope": "fp8 raw frames plus fp8 PRoPE copies; the attention decodes each "
