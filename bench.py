@@ -60,9 +60,9 @@ HBM_PEAK_GBPS = 8000.0
 # factors are what the same counters read for a 1 GiB device copy.  Counters cannot be read
 # from inside the process, so the figure is recorded here for the config it was measured on.
 # Config 5 (one attention call = the unsplit launch, the tail-split launch and the merge, as
-# the roofline's achieved figure is per call): 591.0 + 468.7 + 25.8 MB read, 48.5 + 44.9 +
+# the roofline's achieved figure is per call): 591.0 + 473.0 + 49.9 MB read, 48.5 + 68.2 +
 # 9.1 MB written (profiles/attn_fp8_c5_counters.txt).
-ATTN_TRAFFIC_BYTES = {"c2": 351.83e6, "c5": 1187.9e6}
+ATTN_TRAFFIC_BYTES = {"c2": 351.83e6, "c5": 1239.7e6}
 ATTN_TRAFFIC_FILES = {"c2": "profiles/attn_kernel_c2_traffic.txt",
                       "c5": "profiles/attn_fp8_c5_counters.txt"}
 ATTN_TRAFFIC_SOURCE = ("recorded constant, not measured in this run: rocprofv3 --pmc FETCH_SIZE "

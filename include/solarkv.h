@@ -9,7 +9,7 @@
  * through the descriptor entry points when the caller passes a workspace at least as large as
  * the query functions report:
  *   - attention over an under-filled grid takes the balanced key split (skv_attention_plan:
- *     2 x n_cu x 256 rows x (128 fp16 + 2 floats), 35 MB on 256 CUs);
+ *     2 x n_cu x 256 rows x 130 floats, 68 MB on 256 CUs);
  *   - an fp8 append of a chunk with fewer than 4 (frame, batch, head, K|V) units per CU takes
  *     the one-pass slice kernel (bf16 sources, no K norm, 8-byte aligned workspace: a 128 B
  *     header + 512 B per unit) or else the tile-grid kernels (one float per 64-token tile);
@@ -385,8 +385,8 @@ int skv_h3_rope_prope(const skv_h3_xform_desc* desc, skv_stream_t stream);
 /*
  * skv_attention_ex_noalloc — skv_attention_ex that allocates nothing and takes no workspace:
  * the balanced key split keeps its partial results in a static device array of
- * SKV_NOALLOC_SCRATCH_BYTES per GPU (2 records x 256 rows x (128 fp16 + 2 floats) for each of
- * up to 256 CUs), held by every GPU that calls it until the process ends.  desc->workspace must be NULL
+ * SKV_NOALLOC_SCRATCH_BYTES per GPU (2 records x 256 rows x 130 floats for each of up to 256
+ * CUs), held by every GPU that calls it until the process ends.  desc->workspace must be NULL
  * and workspace_bytes 0; a launch whose split would need more scratch (a device with more than
  * 256 CUs) returns SKV_E_UNSUPPORTED.  Results equal skv_attention_ex's with a workspace.  All
  * calls on one GPU share its array, so calls that overlap on one GPU (different streams) race;
@@ -394,7 +394,7 @@ int skv_h3_rope_prope(const skv_h3_xform_desc* desc, skv_stream_t stream);
  * callers that cannot allocate device memory (code under HIP graph capture, serving loops that
  * forbid allocation).
  */
-#define SKV_NOALLOC_SCRATCH_BYTES 34603008
+#define SKV_NOALLOC_SCRATCH_BYTES 68157440
 int skv_attention_ex_noalloc(const skv_attention_desc* desc, skv_stream_t stream);
 
 /*

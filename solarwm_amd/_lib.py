@@ -29,7 +29,7 @@ SKV_E_LAUNCH = -3
 SKV_MAX_APPEND_FRAMES = 64
 SKV_MAX_FRAMES = 256
 SKV_MAX_SEGMENTS = 64
-SKV_NOALLOC_SCRATCH_BYTES = 34603008
+SKV_NOALLOC_SCRATCH_BYTES = 68157440
 
 # Every symbol include/solarkv.h declares, with (restype, argtypes).
 _i32, _i64, _f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p

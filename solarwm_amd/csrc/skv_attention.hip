@@ -104,7 +104,7 @@ struct AttnArgs {
   // q-tile (in (b, h)-major order) that unit 0 / workgroup 0 of this grid starts at: 0, except
   // for the tail launch of a grid whose last round is split (the full rounds run unsplit first)
   int qt_base;
-  f16* part_o;     // [2*n_wg][256][128] O / row sum (a convex combination of V rows), fp16
+  float* part_o;   // [2*n_wg][256][128] unnormalised O
   float* part_ml;  // [2*n_wg][256][2] (running max in log2 units, row sum)
   // Segments (the SEG instances; n_seg = 0 otherwise): the queries are n_seg consecutive row
   // ranges of seg_rows[s] rows, each attending its own seg_nf[s] consecutive entries of the
@@ -537,22 +537,6 @@ constexpr int attn_wbufs(int ring) { return ring == 4 ? 4 : 2; }
 constexpr size_t attn_lds_bytes(int nw, int rm, int kt_bytes, bool split, bool pk) {
   return (size_t)attn_ring(nw, rm, kt_bytes, split, pk) * kTileBytes +
          (rm == 2 ? (size_t)attn_wbufs(attn_ring(nw, rm, kt_bytes, split, pk)) * kWBuf : 0);
-}
-
-// A split segment's record row: its output O / (scale l) in fp16, where lane (n, hh) holds
-// channels db*32 + g*8 + hh*4 .. +3 in oacc[db][4g .. 4g+3] (both kernels' accumulator layout).
-// O / l is a convex combination of V rows, so fp16's range holds it and its 11-bit mantissa is
-// finer than the bf16 output the merge writes; a row with no visible key (l = 0) stores zeros.
-__device__ inline void store_record(f16* po, const f32x16 (&oacc)[4], float l, float scale, int hh) {
-  typedef f16 f16x4 __attribute__((ext_vector_type(4)));
-  const float inv = l > 0.f ? 1.0f / (l * scale) : 0.f;
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<f16x4*>(po + db * 32 + g * 8 + hh * 4) =
-          f16x4{(f16)(oacc[db][g * 4] * inv), (f16)(oacc[db][g * 4 + 1] * inv),
-                (f16)(oacc[db][g * 4 + 2] * inv), (f16)(oacc[db][g * 4 + 3] * inv)};
 }
 
 // PK: key tiles packed across frame boundaries (PackedWalk; whole frames of T = 8k tokens, 2-byte
@@ -1187,11 +1171,16 @@ void attn_kernel(AttnArgs a) {
 
   const float l_tot = pair_sum(l_run);
   if (SPLIT && (tb > 0 || te < nt)) {
-    // part of a split q-tile: O / l in fp16 (bounded by the largest |V|), the running max and
-    // the row sum
+    // part of a split q-tile: unnormalised O, the running max and the row sum
     if (qlive) {
       const int64_t row = (2 * (int64_t)logical + (seg > 0 ? 1 : 0)) * kBQ + w * 32 + n;
-      store_record(a.part_o + row * kHeadDim, oacc, l_tot, 1.0f, hh);
+      float* po = a.part_o + row * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(po + db * 32 + g * 8 + hh * 4) =
+              f32x4{oacc[db][g * 4], oacc[db][g * 4 + 1], oacc[db][g * 4 + 2], oacc[db][g * 4 + 3]};
       if (hh == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run, l_tot);
     }
     continue;
@@ -1854,11 +1843,19 @@ void attn_fp8_kernel(AttnArgs a) {
   // the matrix core sums both key halves of a query: every lane holds its query's full sum
   const float l_tot = l_run;
   if (SPLIT && (tb > 0 || te < nt)) {
-    // part of a split q-tile: O / (G l) in fp16 (the P scale's G divided out), the running max
-    // in log2 units and the row sum, the record attn_combine_kernel merges
+    // part of a split q-tile: O / G (the P scale's G divided out), the running max in log2
+    // units and the row sum, the record attn_combine_kernel merges
     if (qlive) {
+      const float ig = 1.0f / G;
       const int64_t row = (2 * (int64_t)logical + (seg > 0 ? 1 : 0)) * kBQ + w * 32 + n;
-      store_record(a.part_o + row * kHeadDim, oacc, l_tot, G, hh);
+      float* po = a.part_o + row * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(po + db * 32 + g * 8 + hh * 4) =
+              f32x4{oacc[db][g * 4] * ig, oacc[db][g * 4 + 1] * ig, oacc[db][g * 4 + 2] * ig,
+                    oacc[db][g * 4 + 3] * ig};
       if (hh == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run, l_tot);
     }
     continue;
@@ -1882,9 +1879,8 @@ void attn_fp8_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------------------------
 // Merge of the split q-tiles (AttnArgs.split): workgroup qg of the grid owns q-tile qg.  It finds
 // the split workgroups whose unit ranges cover the q-tile's units [qg*nt, (qg+1)*nt) and
-// combines their records per query row: M = max m_p, w_p = 2^(m_p - M) l_p, O = sum w_p o_p /
-// sum w_p with o_p = O_p / l_p, the record's normalised output (a record with m_p = -inf, all
-// its keys masked, is skipped).  A q-tile inside one workgroup's range was
+// combines their records per query row: M = max m_p, O = sum 2^(m_p - M) O_p / sum 2^(m_p - M)
+// l_p (a record with m_p = -inf has O_p = 0, l_p = 0).  A q-tile inside one workgroup's range was
 // written by attn_kernel itself.  Workgroup (qg, g) merges rows 8g .. 8g+7 of q-tile qg, half a
 // wave per row and 4 channels (one PRoPE group) per lane, so the grid has enough waves in flight
 // to cover the load latency.
@@ -1930,12 +1926,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
       const int64_t row = recs[p] * kSplitBQ + r;
       const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
       if (ml.x == -INFINITY) continue;
-      const float wl = __builtin_amdgcn_exp2f(ml.x - M) * ml.y;  // the record's share of the sum
-      typedef f16 f16x4 __attribute__((ext_vector_type(4)));
-      const f16x4 v = *reinterpret_cast<const f16x4*>(a.part_o + row * kHeadDim + c);
-      L += wl;
-      o0 = fmaf(wl, (float)v[0], o0), o1 = fmaf(wl, (float)v[1], o1);
-      o2 = fmaf(wl, (float)v[2], o2), o3 = fmaf(wl, (float)v[3], o3);
+      const float wgt = __builtin_amdgcn_exp2f(ml.x - M);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + row * kHeadDim + c);
+      L = fmaf(wgt, ml.y, L);
+      o0 = fmaf(wgt, v[0], o0), o1 = fmaf(wgt, v[1], o1);
+      o2 = fmaf(wgt, v[2], o2), o3 = fmaf(wgt, v[3], o3);
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
     float x0v = o0 * inv, x1v = o1 * inv, x2v = o2 * inv, x3v = o3 * inv;
@@ -1970,9 +1965,9 @@ int skv::cu_count() {
 }
 
 // Bytes of the balanced split's records: 2 per workgroup (one per partial segment) of kSplitBQ
-// rows, each row 128 fp16 outputs plus the running max and sum (fp32).
+// rows, each row 128 O floats plus the running max and sum.
 static int64_t split_workspace_bytes(int n_wg) {
-  return (int64_t)2 * n_wg * kSplitBQ * (kHeadDim * (int64_t)sizeof(f16) + 2 * (int64_t)sizeof(float));
+  return (int64_t)2 * n_wg * kSplitBQ * (kHeadDim + 2) * (int64_t)sizeof(float);
 }
 
 template <int NW>
@@ -2349,8 +2344,7 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   a.split = 0;
   a.units = 0;
   a.qt_base = 0;
-  a.part_o = nullptr;
-  a.part_ml = nullptr;
+  a.part_o = a.part_ml = nullptr;
   int64_t split_bytes = 0;
   int split_mode = 0;  // 1: every q-tile shares the CUs; 2: only the last round's q-tiles do
   const int nt = a.nt;
@@ -2449,8 +2443,8 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   if (a.split) {
     // 2 records per split workgroup (n_cu of them): O rows first, then (max, sum) pairs
     const size_t rec_rows = (size_t)2 * n_cu * kSplitBQ;
-    a.part_o = static_cast<f16*>(workspace);
-    a.part_ml = reinterpret_cast<float*>(a.part_o + rec_rows * kHeadDim);
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = a.part_o + rec_rows * kHeadDim;
   }
   if (a.split == 2) {
     // the full rounds unsplit, then the last round's q-tiles [full_wg, n_wg) over every CU

@@ -10,10 +10,9 @@
 namespace {
 
 // Partial-result records of the split: 2 per workgroup (one workgroup per CU) of 256 query
-// rows x (128 fp16 outputs + running max + row sum in fp32).  Sized for 256 CUs (MI355X):
-// 34,603,008 B.
+// rows x (128 O floats + running max + row sum).  Sized for 256 CUs (MI355X): 68,157,440 B.
 constexpr int kScratchCus = 256;
-constexpr int64_t kScratchBytes = (int64_t)2 * kScratchCus * 256 * (128 * 2 + 2 * sizeof(float));
+constexpr int64_t kScratchBytes = (int64_t)2 * kScratchCus * 256 * (128 + 2) * sizeof(float);
 static_assert(kScratchBytes == SKV_NOALLOC_SCRATCH_BYTES, "header constant out of date");
 
 __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];

@@ -221,7 +221,7 @@ def _plan(d):
     return plan
 
 
-SPLIT_BYTES = 2 * 256 * 256 * (128 * 2 + 2 * 4)  # 2 records x 256 rows x (128 fp16 O + fp32 max, sum) per CU
+SPLIT_BYTES = 2 * 256 * 256 * 130 * 4  # 2 records x 256 rows x (128 O + max + sum) per CU
 
 
 @pytest.mark.parametrize("name,B,H,Lq,T,nf,pool,want", [
