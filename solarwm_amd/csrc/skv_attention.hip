@@ -1881,18 +1881,21 @@ void attn_fp8_kernel(AttnArgs a) {
 // the split workgroups whose unit ranges cover the q-tile's units [qg*nt, (qg+1)*nt) and
 // combines their records per query row: M = max m_p, O = sum 2^(m_p - M) O_p / sum 2^(m_p - M)
 // l_p (a record with m_p = -inf has O_p = 0, l_p = 0).  A q-tile inside one workgroup's range was
-// written by attn_kernel itself.  Workgroup (qg, g) merges rows 8g .. 8g+7 of q-tile qg, half a
-// wave per row and 4 channels (one PRoPE group) per lane, so the grid has enough waves in flight
-// to cover the load latency.
+// written by attn_kernel itself.  Workgroup (qg, g) merges rows 32g .. 32g+31 of q-tile qg: half a
+// wave per row and 4 channels (one PRoPE group) per lane, each lane on kCombineRows rows 8 apart
+// whose loads are issued together, so one record search serves 32 rows and the loads of a lane's
+// rows overlap.
 constexpr int kSplitBQ = 256;     // queries per q-tile of the split (8-wave) kernel
 constexpr int kMaxSplitWg = 1024;  // split grids have at most this many workgroups
+constexpr int kCombineRows = 4;    // rows per lane of attn_combine_kernel
+constexpr int kCombineWgs = kSplitBQ / (8 * kCombineRows);  // its workgroups per q-tile
 
 template <typename QT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   __shared__ int64_t recs[kMaxSplitWg];
   __shared__ int n_rec;
   const int nt = a.nt;
-  const int qg = blockIdx.x / (kSplitBQ / 8), rg = blockIdx.x % (kSplitBQ / 8);
+  const int qg = blockIdx.x / kCombineWgs, rg = blockIdx.x % kCombineWgs;
   const int64_t x0 = (int64_t)qg * nt, x1 = x0 + nt - 1;
   auto lo = [&](int i) { return (int64_t)i * a.units / a.n_wg; };
   auto owner = [&](int64_t x) {  // the workgroup whose range holds unit x
@@ -1915,25 +1918,42 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int h = bh % a.H, b = bh / a.H;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = (lane & 31) * 4;
-  {
-    const int r = rg * 8 + 2 * w + (lane >> 5);
-    const int qrow = qt * kSplitBQ + r;
-    if (qrow >= a.Lq) return;
-    float M = -INFINITY;
-    for (int p = 0; p < nr; ++p) M = fmaxf(M, a.part_ml[(recs[p] * kSplitBQ + r) * 2]);
-    float L = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-    for (int p = 0; p < nr; ++p) {
-      const int64_t row = recs[p] * kSplitBQ + r;
+  const int r0 = rg * (8 * kCombineRows) + 2 * w + (lane >> 5);  // rows r0 + 8 j
+  // rows past Lq read records in bounds (every record holds kSplitBQ rows) and store nothing
+  float M[kCombineRows];
+#pragma unroll
+  for (int j = 0; j < kCombineRows; ++j) M[j] = -INFINITY;
+  for (int p = 0; p < nr; ++p) {
+#pragma unroll
+    for (int j = 0; j < kCombineRows; ++j)
+      M[j] = fmaxf(M[j], a.part_ml[(recs[p] * kSplitBQ + r0 + 8 * j) * 2]);
+  }
+  float L[kCombineRows], o[kCombineRows][4];
+#pragma unroll
+  for (int j = 0; j < kCombineRows; ++j) {
+    L[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[j][e] = 0.f;
+  }
+  for (int p = 0; p < nr; ++p) {
+#pragma unroll
+    for (int j = 0; j < kCombineRows; ++j) {
+      const int64_t row = recs[p] * kSplitBQ + r0 + 8 * j;
       const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
       if (ml.x == -INFINITY) continue;
-      const float wgt = __builtin_amdgcn_exp2f(ml.x - M);
+      const float wgt = __builtin_amdgcn_exp2f(ml.x - M[j]);
       const f32x4 v = *reinterpret_cast<const f32x4*>(a.part_o + row * kHeadDim + c);
-      L = fmaf(wgt, ml.y, L);
-      o0 = fmaf(wgt, v[0], o0), o1 = fmaf(wgt, v[1], o1);
-      o2 = fmaf(wgt, v[2], o2), o3 = fmaf(wgt, v[3], o3);
+      L[j] = fmaf(wgt, ml.y, L[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[j][e] = fmaf(wgt, v[e], o[j][e]);
     }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
-    float x0v = o0 * inv, x1v = o1 * inv, x2v = o2 * inv, x3v = o3 * inv;
+  }
+#pragma unroll
+  for (int j = 0; j < kCombineRows; ++j) {
+    const int qrow = qt * kSplitBQ + r0 + 8 * j;
+    if (qrow >= a.Lq) break;  // rows grow with j
+    const float inv = L[j] > 0.f ? 1.0f / L[j] : 0.f;
+    float x0v = o[j][0] * inv, x1v = o[j][1] * inv, x2v = o[j][2] * inv, x3v = o[j][3] * inv;
     if (a.pq_o) {  // PRoPE: P_q of the query's frame on every group of the output
       const float* po = a.pq_o + ((int64_t)b * a.n_qframes + qrow / a.T) * 16;
       const float y0 = fmaf(po[0], x0v, fmaf(po[1], x1v, fmaf(po[2], x2v, po[3] * x3v)));
@@ -2434,11 +2454,11 @@ static int attention_impl(const void* q, int q_dtype, int64_t q_sb, int64_t q_st
   const int rm = prope ? 2 : rope ? 1 : 0;
   auto combine = [&](const AttnArgs& c, int n_q) {
     if (q_dtype == SKV_BF16)
-      hipLaunchKernelGGL((attn_combine_kernel<bf16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
+      hipLaunchKernelGGL((attn_combine_kernel<bf16>), dim3(n_q * kCombineWgs), dim3(256), 0, s, c);
     else if (q_dtype == SKV_F16)
-      hipLaunchKernelGGL((attn_combine_kernel<f16>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
+      hipLaunchKernelGGL((attn_combine_kernel<f16>), dim3(n_q * kCombineWgs), dim3(256), 0, s, c);
     else
-      hipLaunchKernelGGL((attn_combine_kernel<float>), dim3(n_q * (kSplitBQ / 8)), dim3(256), 0, s, c);
+      hipLaunchKernelGGL((attn_combine_kernel<float>), dim3(n_q * kCombineWgs), dim3(256), 0, s, c);
   };
   if (a.split) {
     // 2 records per split workgroup (n_cu of them): O rows first, then (max, sum) pairs
