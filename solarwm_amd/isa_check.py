@@ -24,7 +24,9 @@ import re
 from dataclasses import dataclass
 
 # passes of each MFMA form the kernels use (gfx950, dense): 32x32x64 fp8 = 65536 MACs at 1024
-# MACs per clock per SIMD = 64 clocks = 16 passes of 4 clocks; the others likewise
+# MACs per clock per SIMD = 64 clocks = 16 passes of 4 clocks; the others likewise.  Passes + 4
+# is exactly the wait hipcc's hazard pass leaves before a VALU read in straight-line code (20,
+# 12, 12, 12, 8 wait states; tests/test_isa_check.py compiles one product of each form).
 PASSES = {
     "v_mfma_f32_32x32x64_f8f6f4": 16,
     "v_mfma_scale_f32_32x32x64_f8f6f4": 16,

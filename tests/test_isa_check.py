@@ -142,3 +142,53 @@ def test_real_listing_from_hipcc(tmp_path):
     stripped = re.sub(r"\n\ts_nop \d+", "", listing)
     (paths,) = isa_check.check_listing(stripped).values()
     assert any(p.needed == 12 and p.waited < 12 for p in paths), [str(p) for p in paths]
+
+
+def test_pass_table_matches_hipcc(tmp_path):
+    """The wait each MFMA form needs (its passes + EXTRA_WAIT) is exactly what hipcc's hazard pass
+    puts between the product and a VALU read of its result in straight-line code."""
+    import shutil
+    import subprocess
+
+    import pytest
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not shutil.os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    head = ("#include <hip/hip_runtime.h>\n"
+            "typedef int i32x8 __attribute__((ext_vector_type(8)));\n"
+            "typedef float f32x4 __attribute__((ext_vector_type(4)));\n"
+            "typedef float f32x16 __attribute__((ext_vector_type(16)));\n"
+            "typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));\n"
+            "typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));\n")
+    forms = {  # kernel name: (operand type, accumulator type, product)
+        "k_f8_32": ("i32x8", "f32x16", "__builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0)"),
+        "k_f8_16": ("i32x8", "f32x4", "__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0)"),
+        "k_bf16_32": ("bf16x8", "f32x16", "__builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0)"),
+        "k_f16_32": ("f16x8", "f32x16", "__builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0)"),
+        "k_bf16_16": ("bf16x8", "f32x4", "__builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0)"),
+    }
+    body = head + "".join(
+        f'extern "C" __global__ void {name}(const {op}* p, float* out) {{\n'
+        f"  {op} a = p[threadIdx.x], b = p[64 + threadIdx.x];\n"
+        f"  {acc} c = {{}};\n  {acc} d = {call};\n  out[threadIdx.x] = d[0] + 1.0f;\n}}\n"
+        for name, (op, acc, call) in forms.items())
+    src = tmp_path / "k.hip"
+    src.write_text(body)
+    asm = tmp_path / "k.s"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "--cuda-device-only", "-S", str(src),
+                    "-o", str(asm)], check=True, capture_output=True)
+    seen = {}
+    for name, lines in isa_check.functions(asm.read_text()):
+        ins = [t for t in (ln.split(";")[0].strip() for ln in lines) if t and not t.startswith(".")
+               and not t.endswith(":")]
+        i = next(k for k, t in enumerate(ins) if "mfma" in t.split()[0])
+        op = ins[i].split()[0]
+        waited = 0
+        for t in ins[i + 1:]:
+            if t.startswith("v_add_f32"):
+                break
+            waited += int(t.split()[1]) + 1 if t.startswith("s_nop") else 1
+        seen[op] = waited
+        assert waited == isa_check.PASSES[op] + isa_check.EXTRA_WAIT, (name, op, waited)
+    assert len(seen) == len(forms)
