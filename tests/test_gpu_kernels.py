@@ -416,8 +416,10 @@ def test_fp8_attention_unit_scale_vs_bf16_oracle(gpu, B, H, Lq, T, n):
 def assert_fp8_close_normalised(got, q, k, v, T, mask=None):
     """Outlier data: compare with the quantisation-aware oracle (fp8 cache frames and fp8 query
     rows decoded, fp64 softmax) and normalise the error by each channel's V RMS; what remains is
-    the fp8 rounding of P and fp32 accumulation."""
-    from .helpers import FP8_NORM_MAX, FP8_NORM_MEAN
+    the fp8 rounding of P and fp32 accumulation.  The mean bar is FP8_NORM_MEAN, or the margin
+    times the error that P's rounding alone causes on the case where that is larger (few rows
+    over few effective keys)."""
+    from .helpers import FP8_NORM_MAX, FP8_NORM_MEAN, FP8_P_ROUNDING_MARGIN, fp8_p_rounding_error
 
     want = ref.attention(ref.fp8_fake_quant_rows(q), ref.fp8_fake_quant_frames(k.float(), T),
                          ref.fp8_fake_quant_frames(v.float(), T), mask=mask,
@@ -426,9 +428,12 @@ def assert_fp8_close_normalised(got, q, k, v, T, mask=None):
     got = got.detach().cpu().double()
     assert torch.isfinite(got).all()
     e = (got - want).abs() / rms_v
-    _say(f"fp8 normalised error: max {float(e.max()):.3e} mean {float(e.mean()):.3e}")
+    e_p = float(fp8_p_rounding_error(q, k, v, T, mask=mask).mean())
+    bar_mean = max(FP8_NORM_MEAN, FP8_P_ROUNDING_MARGIN * e_p)
+    _say(f"fp8 normalised error: max {float(e.max()):.3e} mean {float(e.mean()):.3e} "
+         f"(P rounding alone: mean {e_p:.3e})")
     assert float(e.max()) <= FP8_NORM_MAX, f"normalised max error {float(e.max()):.3e}"
-    assert float(e.mean()) <= FP8_NORM_MEAN, f"normalised mean error {float(e.mean()):.3e}"
+    assert float(e.mean()) <= bar_mean, f"normalised mean error {float(e.mean()):.3e} > {bar_mean:.3e}"
 
 
 @pytest.mark.parametrize("B,H,Lq,T,n", [(1, 2, 256, 130, 4), (4, 3, 390, 390, 3), (1, 12, 1170, 390, 6),

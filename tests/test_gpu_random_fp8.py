@@ -42,7 +42,9 @@ def _case(seed):
     return T, n, H, B, Lq, qdt, outliers, zero, causal, r.randrange(1 << 30)
 
 
-@pytest.mark.parametrize("seed", range(16))
+# 20209: one query row over 4680 keys with outlier channels and an all-zero V frame, whose
+# softmax rests on about 12 keys (the mean bar then follows P's rounding, tests/helpers.py)
+@pytest.mark.parametrize("seed", [*range(16), 20209])
 def test_random_fp8_shape_vs_quantised_oracle(gpu, seed):
     T, n, H, B, Lq, qdt, outliers, zero, causal, s = _case(seed)
     print("fp8 case", seed, dict(T=T, n=n, H=H, B=B, Lq=Lq, q=qdt, outliers=outliers, zero=zero,
