@@ -107,8 +107,12 @@ def positions(cfg: RopeConfig, *, num_sink_frames: int, num_local_frames: int,
     else:
         q_start, local_start = nl - nb, 0
     if q_start < 0 or local_start < 0:
+        if sink_branch:  # the reference's two checks word for word (causal_model.py:859, :766)
+            raise ValueError(
+                f"EchoRoPE underflow while assigning sink/local positions: B={nb}, R={nl}, "
+                f"sink={ns}, q_start={q_start}, local_start={local_start}, pmax={pmax}")
         raise ValueError(
-            f"EchoRoPE underflow while assigning positions: B={nb}, R={nl}, sink={ns}, "
+            f"EchoRoPE underflow while assigning window-relative positions: B={nb}, R={nl}, "
             f"q_start={q_start}, local_start={local_start}, pmax={pmax}")
     keys = list(range(ns)) + list(range(local_start, local_start + nl))
     if keys and max(keys + [q_start + nb - 1]) >= cfg.table_len:

@@ -36,6 +36,21 @@ def test_positions_match_oracle(use_echorope, rtf):
             range(want["local_start"], want["local_start"] + nl))
 
 
+def test_underflow_messages_name_the_reference_check():
+    """A window that does not fit the positions raises the reference's ValueError of that path:
+    sink/local positions (causal_model.py:859) or window-relative positions (:766)."""
+    cfg = rope.RopeConfig(grid_hw=(3, 4), use_echorope=False, rope_train_frames=4)
+    kw = dict(num_local_frames=5, num_new_frames=2, max_attention_size=9 * 12, frame_tokens=12,
+              current_start_frame=20)
+    with pytest.raises(ValueError, match=r"^EchoRoPE underflow while assigning sink/local "
+                                         r"positions: B=2, R=5, sink=1, q_start=2, local_start=-1"):
+        rope.positions(cfg, num_sink_frames=1, sink_branch=True, **kw)
+    with pytest.raises(ValueError, match=r"^EchoRoPE underflow while assigning window-relative "
+                                         r"positions: B=3, R=2, q_start=-1, local_start=0"):
+        rope.positions(cfg, num_sink_frames=0, sink_branch=False,
+                       **dict(kw, num_local_frames=2, num_new_frames=3))
+
+
 def test_tables_match_oracle_freqs():
     f = ref.wan_rope_freqs()
     cfg = rope.RopeConfig(grid_hw=(5, 7))
