@@ -27,9 +27,6 @@ import torch
 
 from . import _lib, h3, kernels
 
-_GEOM_ERR = "num_frames must be a positive multiple of num_frame_per_block"
-
-
 def attend_segments(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
                     segs: Sequence[tuple[int, Sequence[int], Sequence[int] | None]], *,
                     frame_tokens: int, softmax_scale: float | None = None,
@@ -74,15 +71,22 @@ def teacher_forcing_frame_lists(*, num_frames: int, num_frame_per_block: int,
     frames 0..F-1, noisy F..2F-1): the union of the reference's key intervals
     (causal_model.py:434-468) in frames, duplicates removed."""
     F, nb = num_frames, num_frame_per_block
-    if nb <= 0 or F % nb:
-        raise ValueError(_GEOM_ERR)
-    if not 0 <= sink_size <= F or sink_size % nb:
-        raise ValueError(f"sink_size={sink_size} must be whole {nb}-frame chunks within {F} frames")
+    # the reference's checks, in its order and words (causal_model.py:357-386)
+    if nb <= 0:
+        raise ValueError(f"num_frame_per_block must be positive, got {nb}")
+    if F % nb:
+        raise ValueError(f"num_frames={F} must be divisible by num_frame_per_block={nb}")
+    sink_size = int(sink_size)
+    if sink_size < 0 or sink_size > F:
+        raise ValueError(f"sink_size must be in [0, {F}], got {sink_size}")
+    if sink_size % nb:
+        raise ValueError(f"sink_size={sink_size} must contain whole {nb}-frame chunks")
     chunks = F // nb
     default = max(0, chunks - 1)
     m = default if max_prior_clean_chunks is None else int(max_prior_clean_chunks)
     if not 0 <= m <= default:
-        raise ValueError(f"max_prior_clean_chunks must be in [0, {default}], got {m}")
+        raise ValueError(f"model.max_prior_clean_chunks must be in [0, {default}] for a "
+                         f"{chunks}-chunk window, got {m}")
     out = []
     for c in range(chunks):  # clean queries
         frames = set(range(max(0, c - m) * nb if sink_size else 0, (c + 1) * nb))

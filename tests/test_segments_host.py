@@ -19,9 +19,20 @@ def test_teacher_forcing_frame_lists_match_mask():
 
 
 def test_teacher_forcing_frame_list_errors():
-    with pytest.raises(ValueError):
-        teacher_forcing_frame_lists(num_frames=5, num_frame_per_block=2)
-    with pytest.raises(ValueError):
-        teacher_forcing_frame_lists(num_frames=6, num_frame_per_block=2, sink_size=1)
-    with pytest.raises(ValueError):
-        teacher_forcing_frame_lists(num_frames=6, num_frame_per_block=2, max_prior_clean_chunks=3)
+    """The reference's checks and messages, in its order (causal_model.py:357-386)."""
+    cases = [
+        (dict(num_frames=6, num_frame_per_block=0), "num_frame_per_block must be positive, got 0"),
+        (dict(num_frames=5, num_frame_per_block=2),
+         "num_frames=5 must be divisible by num_frame_per_block=2"),
+        (dict(num_frames=6, num_frame_per_block=2, sink_size=8), r"sink_size must be in \[0, 6\], got 8"),
+        (dict(num_frames=6, num_frame_per_block=2, sink_size=-2), r"sink_size must be in \[0, 6\], got -2"),
+        (dict(num_frames=6, num_frame_per_block=2, sink_size=1),
+         "sink_size=1 must contain whole 2-frame chunks"),
+        (dict(num_frames=6, num_frame_per_block=2, max_prior_clean_chunks=3),
+         r"model.max_prior_clean_chunks must be in \[0, 2\] for a 3-chunk window, got 3"),
+        (dict(num_frames=6, num_frame_per_block=2, max_prior_clean_chunks=-1),
+         r"model.max_prior_clean_chunks must be in \[0, 2\] for a 3-chunk window, got -1"),
+    ]
+    for kw, msg in cases:
+        with pytest.raises(ValueError, match="^" + msg + "$"):
+            teacher_forcing_frame_lists(**kw)
