@@ -18,7 +18,7 @@ from oracle import segments_ref as sr
 from solarwm_amd import h3
 from solarwm_amd.segments import H3WindowCache
 
-from .helpers import assert_attn_close
+from .helpers import MAX_ABS, MEAN_ABS
 
 pytestmark = pytest.mark.gpu
 
@@ -37,6 +37,22 @@ def _tables(n, g, dtype):
 
 def _matrices(b, n, g):
     return (torch.randn(b, n, 4, 4, generator=g) * 0.6)
+
+
+def _assert_projected_close(got, want, out_matrix):
+    """Output rows are the attention output mapped by each row's 4x4 camera block (channels in
+    groups of 4).  The map turns an attention error e into at most gain * e, with gain the
+    block's larger absolute row or column sum for that channel, so each element's bar is the
+    attention bar of tests/helpers.py times its gain (at least 1), and the mean bar likewise."""
+    m = out_matrix.detach().cpu().abs().double()
+    gain = torch.maximum(m.sum(-1), m.sum(-2)).clamp_min(1.0)        # [b, rows, 4]
+    gain = gain[..., torch.arange(128) % 4][:, :, None, :]            # [b, rows, 1, 128]
+    got = got.detach().cpu().double()
+    assert torch.isfinite(got).all(), "non-finite attention output"
+    err = (got - want.double()).abs()
+    worst = float((err / gain).max())
+    assert worst <= MAX_ABS, f"max-abs error {worst:.3e} x gain > {MAX_ABS}"
+    assert float(err.mean()) <= MEAN_ABS * float(gain.expand_as(err).mean()), float(err.mean())
 
 
 @pytest.mark.parametrize("tdt,mdt,mb,rope,cam", [
@@ -98,7 +114,8 @@ def test_prope_project_and_qkv_separate(gpu):
     torch.testing.assert_close(back.cpu().float(), v.float(), rtol=0.05, atol=0.05)
 
 
-@pytest.mark.parametrize("P,nb", [(150, 1), (0, 2)])
+# (37, 2): outputs up to 3.4 after the camera blocks, one of them 2 bf16 units off
+@pytest.mark.parametrize("P,nb", [(150, 1), (0, 2), (37, 2)])
 def test_h3_window_rollout_vs_oracle(gpu, P, nb):
     """Eight chunks through H3WindowCache (two evaluations each, the second commits) against
     the oracle's transformed window evaluation; history past five chunks rolls off."""
@@ -128,7 +145,7 @@ def test_h3_window_rollout_vs_oracle(gpu, P, nb):
                                                   k_rotary=(kc, ks), q_matrix=qm, kv_matrix=kvm,
                                                   out_matrix=om, commit=commit)
             torch.cuda.synchronize()
-            assert_attn_close(got, want)
+            _assert_projected_close(got, want, om)
     assert [e[0] for e in cache.history(1, 8)] == [3, 4, 5, 6, 7]
     with pytest.raises(RuntimeError):
         cache.history(0, 2)
@@ -169,4 +186,4 @@ def test_h3_memory_kv_vs_oracle(gpu, n_bank, audio_rows):
                                        out_matrix=om, history_kv_matrix=hm)
         oc.commit(0, c, k[:, prefix:], v[:, prefix:])
         torch.cuda.synchronize()
-        assert_attn_close(got, want)
+        _assert_projected_close(got, want, om)
