@@ -39,20 +39,37 @@ def _matrices(b, n, g):
     return (torch.randn(b, n, 4, 4, generator=g) * 0.6)
 
 
-def _assert_projected_close(got, want, out_matrix):
-    """Output rows are the attention output mapped by each row's 4x4 camera block (channels in
-    groups of 4).  The map turns an attention error e into at most gain * e, with gain the
-    block's larger absolute row or column sum for that channel, so each element's bar is the
-    attention bar of tests/helpers.py times its gain (at least 1), and the mean bar likewise."""
-    m = out_matrix.detach().cpu().abs().double()
-    gain = torch.maximum(m.sum(-1), m.sum(-2)).clamp_min(1.0)        # [b, rows, 4]
-    gain = gain[..., torch.arange(128) % 4][:, :, None, :]            # [b, rows, 1, 128]
-    got = got.detach().cpu().double()
+def _exact_projected(o, matrix):
+    """Channels [96, 128) of an unrounded attention output mapped by the bf16 camera blocks in
+    float64 (y_i = sum_j m_ij x_j per group of 4, as oracle/h3_ref.prope_project without its
+    roundings); o [B, S, H, 128] float64, matrix [B or 1, S, 4, 4]."""
+    m = matrix.to(torch.bfloat16).double()[:, :, None, None]  # [B|1, S, 1, 1, 4, 4]
+    b, n, h, _ = o.shape
+    x = o[..., 96:].reshape(b, n, h, 8, 4)
+    out = o.clone()
+    out[..., 96:] = (m * x[..., None, :]).sum(-1).reshape(b, n, h, 32)
+    return out
+
+
+def _errors(got, want):
+    d = (got.double() - want.double()).abs().flatten()
+    return float(d.max()), float(d.kthvalue(max(1, int(d.numel() * 0.999))).values), float(d.mean())
+
+
+def _assert_within_reference(got, want, exact):
+    """Camera blocks scale values (and their bf16 steps) by up to ~5 on both the value and the
+    output side, so, as for fused PRoPE (tests/test_gpu_prope.py), the bars follow the
+    reference's own arithmetic: against the unrounded float64 evaluation ``exact``, our max
+    error stays within 2.5x the reference's (``want``, the oracle's bf16 roundings), the
+    99.9th percentile and the mean within 1.25x, or within the plain bf16 bars if looser."""
+    got = got.detach().cpu()
     assert torch.isfinite(got).all(), "non-finite attention output"
-    err = (got - want.double()).abs()
-    worst = float((err / gain).max())
-    assert worst <= MAX_ABS, f"max-abs error {worst:.3e} x gain > {MAX_ABS}"
-    assert float(err.mean()) <= MEAN_ABS * float(gain.expand_as(err).mean()), float(err.mean())
+    e_ours, e_ref = _errors(got, exact), _errors(want, exact)
+    _say(f"  (max, p99.9, mean) ours {tuple(f'{e:.2e}' for e in e_ours)} "
+         f"reference {tuple(f'{e:.2e}' for e in e_ref)}")
+    assert e_ours[0] <= max(MAX_ABS, 2.5 * e_ref[0]), "max"
+    assert e_ours[1] <= max(MAX_ABS / 2, 1.25 * e_ref[1]), "p99.9"
+    assert e_ours[2] <= max(MEAN_ABS, 1.25 * e_ref[2]), "mean"
 
 
 @pytest.mark.parametrize("tdt,mdt,mb,rope,cam", [
@@ -141,11 +158,17 @@ def test_h3_window_rollout_vs_oracle(gpu, P, nb):
                                q_rotary=(qc.to(gpu), qs.to(gpu)), k_rotary=(kc.to(gpu), ks.to(gpu)),
                                q_matrix=qm.to(gpu), kv_matrix=kvm.to(gpu), out_matrix=om.to(gpu),
                                commit=commit)
+            hist = oc.history(1, c)
+            keys = torch.cat([pk, *(e[1] for e in hist), k], 1)
+            vals = torch.cat([pv, *(e[2] for e in hist), v], 1)
+            exact = _exact_projected(sr.attention(ref.rope_prope(q, qc, qs, qm),
+                                                  ref.rope_prope(keys, kc, ks, kvm),
+                                                  ref.prope_project(vals, kvm)).double(), om)
             want = ref.windowed_rollout_attention(q, k, v, pk, pv, oc, 1, c, q_rotary=(qc, qs),
                                                   k_rotary=(kc, ks), q_matrix=qm, kv_matrix=kvm,
                                                   out_matrix=om, commit=commit)
             torch.cuda.synchronize()
-            _assert_projected_close(got, want, om)
+            _assert_within_reference(got, want, exact)
     assert [e[0] for e in cache.history(1, 8)] == [3, 4, 5, 6, 7]
     with pytest.raises(RuntimeError):
         cache.history(0, 2)
@@ -184,6 +207,12 @@ def test_h3_memory_kv_vs_oracle(gpu, n_bank, audio_rows):
                                        n_bank=n_bank, audio_rows=audio_rows, rotary=(cos, sin),
                                        history_rotary=(hc, hs), q_matrix=qm, kv_matrix=km,
                                        out_matrix=om, history_kv_matrix=hm)
+        hkt = ref.rope_prope(hk, hc, hs, hm) if hrows else hk
+        hvt = ref.prope_project(hv, hm) if hrows else hv
+        o = sr.memory_kv_attention(ref.rope_prope(q, cos, sin, qm), ref.rope_prope(k, cos, sin, km),
+                                   ref.prope_project(v, km), hkt, hvt, text_rows=text,
+                                   frame_rows=T, n_bank=n_bank, audio_rows=audio_rows)
+        exact = _exact_projected(o.double(), om)
         oc.commit(0, c, k[:, prefix:], v[:, prefix:])
         torch.cuda.synchronize()
-        _assert_projected_close(got, want, om)
+        _assert_within_reference(got, want, exact)
